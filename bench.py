@@ -1,0 +1,459 @@
+"""Benchmark of the fused sampling / verification path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]`` prints one JSON line with the
+headline metric of BASELINE.json: fused decode-sample microseconds per step and achieved HBM GB/s
+at B=64, V=128256 bf16 (config 1, ``UnshardedFusedSingular.autoregressive``), plus ``roofline``
+(measured live with HIP events on the launch stream) and ``cpu_baseline`` (the CPU restatement of
+the reference's PyTorch path from ``oracle/``, timed on a bounded sample of the same workload).
+
+The module also defines the synthetic workloads of all five configurations; the parity tests
+import them. Logits follow one generator: x ~ N(0, 3^2) plus 1-16 spikes of U[10, 20] per row,
+seeded with 1000 + config index, drawn on the CPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from dataclasses import dataclass
+from pathlib import Path
+from typing import List, Optional
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "sonic-sampler_amd"))
+
+import torch  # noqa: E402
+
+BF16 = torch.bfloat16
+I32 = torch.int32
+I64 = torch.int64
+HBM_PEAK_GBS = 8000.0
+
+
+# ------------------------------------------------------------------------------------------------
+# Synthetic workloads
+# ------------------------------------------------------------------------------------------------
+
+def spiked_logits(rows: int, vocab: int, seed: int, dtype=BF16) -> torch.Tensor:
+    """N(0, 3^2) logits with 1-16 spikes of +U[10, 20] per row (CPU)."""
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    x = torch.randn(rows, vocab, generator=g, dtype=torch.float32) * 3.0
+    counts = torch.randint(1, 17, (rows,), generator=g)
+
+    for r in range(rows):
+
+        cols = torch.randperm(vocab, generator=g)[: int(counts[r])]
+        x[r, cols] += torch.empty(len(cols)).uniform_(10.0, 20.0, generator=g)
+
+    return x.to(dtype)
+
+
+def c0_inputs(seed: int = 1000):
+    """Config 0: UnshardedBoundedTopK, B=8, V=32000 fp32, k=32."""
+
+    return spiked_logits(8, 32000, seed, torch.float32), 32
+
+
+@dataclass
+class SingularWorkload:
+    logits: torch.Tensor          # [R, V] bf16 (CPU)
+    buffers: object               # SamplingBuffers (CPU)
+    vocab: int
+    max_top_logprobs: int
+    timestep: int = 0
+    slot_mapping: Optional[torch.Tensor] = None
+    d2t: Optional[torch.Tensor] = None
+    tokens: Optional[torch.Tensor] = None
+    target_vocab: Optional[int] = None
+
+
+def c1_workload(seed: int = 1001, batch: int = 64, vocab: int = 128256) -> SingularWorkload:
+    """Config 1: autoregressive decode with heterogeneous per-row parameters."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, ScopedIndicators
+
+    g = torch.Generator("cpu").manual_seed(seed + 7)
+    logits = spiked_logits(batch, vocab, seed)
+    bf = lambda v: float(torch.tensor(v).to(BF16))  # noqa: E731
+
+    temperature = [bf(float(torch.empty(1).uniform_(0.5, 1.5, generator=g))) for _ in range(batch)]
+    top_k = [[128, 20, 50][int(torch.randint(0, 3, (1,), generator=g))] for _ in range(batch)]
+    top_p = [bf(float(torch.empty(1).uniform_(0.8, 1.0, generator=g))) for _ in range(batch)]
+    min_p = [[0.0, bf(0.05)][int(torch.randint(0, 2, (1,), generator=g))] for _ in range(batch)]
+    biases = []
+
+    for _ in range(batch):
+
+        ids = torch.randperm(vocab, generator=g)[:16]
+        vals = torch.empty(16).uniform_(-5.0, 5.0, generator=g)
+        biases.append({int(i): bf(float(v)) for i, v in zip(ids, vals)})
+
+    scoped = ScopedIndicators.from_params(
+        size=batch, timesteps=1,
+        multiplicative=[bf(1.1)] * batch, frequency=[bf(0.2)] * batch, presence=[bf(0.3)] * batch,
+        biases=biases, temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+        top_logprobs=[5] * batch,
+    )
+
+    buffers = SamplingBuffers.default(size=batch, timesteps=1, vocab_size=vocab, device="cpu", noise=False)
+    buffers.flags = Flags.from_scoped(scoped, device="cpu")
+    buffers.weights.gumbel.target.exponential_(1.0, generator=g).log_()
+    buffers.temperature.copy_(torch.tensor(temperature).to(BF16))
+    buffers.top_k.copy_(torch.tensor(top_k, dtype=I32))
+    buffers.top_p.copy_(torch.tensor(top_p).to(BF16))
+    buffers.min_p.copy_(torch.tensor(min_p).to(BF16))
+    buffers.top_logprobs.fill_(5)
+    rep = buffers.repetition
+    rep.multiplicative.fill_(1.1)
+    rep.frequency.fill_(0.2)
+    rep.presence.fill_(0.3)
+
+    history = torch.randint(0, vocab, (batch, 512), generator=g)
+    rep.counts.decode.zero_().scatter_add_(1, history, torch.ones_like(history, dtype=I32))
+
+    for r, bias in enumerate(biases):
+
+        for i, v in bias.items():
+
+            buffers.bias[r, i] = v
+
+    return SingularWorkload(logits=logits, buffers=buffers, vocab=vocab, max_top_logprobs=5)
+
+
+@dataclass
+class MultistepWorkload:
+    logits: torch.Tensor          # flat [rows, V] bf16 (CPU)
+    drafted: torch.Tensor         # flat [rows] int32
+    buffers: object
+    cu_seqlens: List[int]
+    lookahead: int
+    vocab: int
+    max_top_logprobs: int
+    probabilities: Optional[torch.Tensor] = None   # [B, gamma, V] bf16
+    varlen: bool = False
+
+
+def c2_workload(seed: int = 1002, batch: int = 128, gamma: int = 4, vocab: int = 151936) -> MultistepWorkload:
+    """Config 2: greedy verification, drafts = target argmax w.p. 0.7 else uniform in [1, V)."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    n = gamma + 1
+    g = torch.Generator("cpu").manual_seed(seed + 7)
+    logits = spiked_logits(batch * n, vocab, seed)
+    argmax = logits.float().argmax(dim=-1)
+    keep = torch.rand(batch * n, generator=g) < 0.7
+    other = torch.randint(1, vocab, (batch * n,), generator=g)
+    drafted = torch.where(keep, argmax, other).to(I32)
+
+    buffers = SamplingBuffers.default(size=batch, timesteps=n, vocab_size=vocab, device="cpu", noise=False)
+    buffers.flags = Flags.from_values(batch, n, Indicator.GREEDY, device="cpu")
+    buffers.top_k.fill_(1)
+
+    return MultistepWorkload(logits=logits, drafted=drafted, buffers=buffers,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma,
+                             vocab=vocab, max_top_logprobs=5)
+
+
+def c3_workload(seed: int = 1003, batch: int = 64, gamma: int = 7, vocab: int = 128256) -> MultistepWorkload:
+    """Config 3: stochastic verification, variable lookahead U{1..7}, top-20 logprobs."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    g = torch.Generator("cpu").manual_seed(seed + 7)
+    lengths = (torch.randint(1, gamma + 1, (batch,), generator=g) + 1).tolist()
+    cu = [0]
+
+    for length in lengths:
+
+        cu.append(cu[-1] + length)
+
+    rows = cu[-1]
+    logits = spiked_logits(rows, vocab, seed)
+
+    probabilities = torch.zeros(batch, gamma, vocab, dtype=BF16)
+    drafted = torch.zeros(rows, dtype=I32)
+
+    for b in range(batch):
+
+        for i in range(lengths[b] - 1):
+
+            noisy = logits[cu[b] + i].float() + torch.randn(vocab, generator=g)
+            q = torch.softmax(noisy, dim=-1).to(BF16)
+            probabilities[b, i] = q
+            token = 0
+
+            while token == 0:
+
+                token = int(torch.multinomial(q.float(), 1, generator=g))
+
+            drafted[cu[b] + i] = token
+
+        drafted[cu[b + 1] - 1] = int(torch.randint(1, vocab, (1,), generator=g))
+
+    indicator = Indicator.TOP_K_LOGPROBS
+    buffers = SamplingBuffers.default(size=batch, timesteps=gamma + 1, vocab_size=vocab, device="cpu",
+                                      noise=False)
+    buffers.flags = Flags.from_values(batch, gamma + 1, indicator, device="cpu")
+    buffers.top_logprobs.fill_(20)
+    weights = buffers.weights
+    weights.gumbel.target.exponential_(1.0, generator=g).log_()
+    weights.uniform.uniform_(torch.finfo(BF16).tiny, 1.0, generator=g)
+
+    return MultistepWorkload(logits=logits, drafted=drafted, buffers=buffers, cu_seqlens=cu,
+                             lookahead=gamma, vocab=vocab, max_top_logprobs=20,
+                             probabilities=probabilities, varlen=True)
+
+
+def c4_workload(seed: int = 1004, rows: int = 256, slots: int = 512, gamma: int = 4,
+                draft_vocab: int = 32000, target_vocab: int = 262144,
+                timestep: int = 3) -> SingularWorkload:
+    """Config 4: drafting with d2t (32000 -> 262144), 256 of 512 slots, 5% grammar."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    g = torch.Generator("cpu").manual_seed(seed + 7)
+    logits = spiked_logits(rows, draft_vocab, seed)
+    d2t = torch.randperm(target_vocab, generator=g)[:draft_vocab].to(I32)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(I32)
+
+    buffers = SamplingBuffers.default(size=slots, timesteps=gamma + 1, vocab_size=target_vocab,
+                                      device="cpu", noise=False)
+    buffers.flags = Flags.from_values(slots, gamma + 1, Indicator.GRAMMAR, Indicator.GRAMMAR, device="cpu")
+
+    words = target_vocab // 32
+    bits = torch.rand(rows, target_vocab, generator=g) < 0.05
+    spikes = logits.float().argmax(dim=-1)
+    bits[torch.arange(rows), d2t[spikes].to(I64)] = True
+    packed = (bits.view(rows, words, 32).to(I64) << torch.arange(32, dtype=I64)).sum(-1)
+    grammar = buffers.grammar.view(I32)
+
+    for r in range(rows):
+
+        grammar[int(slot_mapping[r]), timestep] = (packed[r] - ((packed[r] >> 31) << 32)).to(I32)
+
+    buffers.weights.gumbel.draft[:, timestep].exponential_(1.0, generator=g).log_()
+    tokens = torch.randint(1, target_vocab, (rows, gamma + 1), generator=g).to(I32)
+
+    return SingularWorkload(logits=logits, buffers=buffers, vocab=draft_vocab, max_top_logprobs=5,
+                            timestep=timestep, slot_mapping=slot_mapping, d2t=d2t, tokens=tokens,
+                            target_vocab=target_vocab)
+
+
+def to_device(buffers, device):
+    """A device copy of a CPU SamplingBuffers (same layout)."""
+
+    import dataclasses
+
+    from sonic_sampler.base import SliceBuffer
+    from sonic_sampler.base.tensor import PrefixContiguousTensor, prefix_contiguous
+    from sonic_sampler.core.flags import Flags
+
+    def move(obj):
+
+        if isinstance(obj, Flags):
+
+            packed = obj.packed.T.contiguous().to(device).T if obj.packed.stride(0) == 1 else obj.packed.to(device)
+
+            return Flags(indicators=obj.indicators, pinned=obj.pinned, packed=packed, layout=obj.layout)
+
+        if isinstance(obj, SliceBuffer):
+
+            kwargs = {f.name: move(getattr(obj, f.name)) for f in dataclasses.fields(obj)}
+
+            return obj.__class__(**kwargs)
+
+        if isinstance(obj, PrefixContiguousTensor):
+
+            return prefix_contiguous(obj.as_subclass(torch.Tensor).to(device))
+
+        if isinstance(obj, torch.Tensor):
+
+            return obj if obj.device.type == "cpu" and obj.is_pinned() else obj.to(device)
+
+        return obj
+
+    return move(buffers)
+
+
+# ------------------------------------------------------------------------------------------------
+# Measurement
+# ------------------------------------------------------------------------------------------------
+
+C1_BYTES_PER_ELEMENT = 2 + 4 + 4 + 2   # logits, context counts, decode counts, bias
+
+
+def c1_algorithmic_bytes(batch: int, vocab: int, top_logprobs: int = 5) -> int:
+    """HBM bytes one fused autoregressive call must move at config 1."""
+
+    streamed = batch * vocab * C1_BYTES_PER_ELEMENT
+    gathers = batch * 128 * 2                           # Gumbel noise gathers (buffer mode)
+    outputs = batch * (4 + 2 + top_logprobs * 6 + 4)    # token, logprob, top-Z, count update
+
+    return streamed + gathers + outputs
+
+
+def cpu_baseline_c1(workload: SingularWorkload, rows: int) -> dict:
+    """The CPU restatement of the reference's PyTorch path on `rows` rows of config 1."""
+
+    from oracle import sampler as oracle
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    state = oracle.State.from_buffers(workload.buffers)
+    logits = workload.logits[:rows]
+
+    def run():
+
+        oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=5)
+
+    run()
+    times = []
+
+    for _ in range(5):
+
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+
+    per_row = statistics.median(times) / rows
+
+    return {
+        "value": round(per_row * workload.logits.size(0) * 1e6, 1),
+        "unit": "us/step",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {workload.logits.size(0)} rows of config 1, median of 5 runs after "
+                  f"1 warm-up, scaled to the full batch; CPU: {platform.processor() or platform.machine()}",
+    }
+
+
+def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox: bool = True) -> dict:
+
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    device = torch.device("cuda:0")
+    base = c1_workload()
+    batch, vocab = base.logits.shape
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch,
+                                                max_top_logprobs=5, device=device)
+    inputs = []
+
+    for i in range(sets):
+
+        work = c1_workload(seed=1001 + 100 * i) if i else base
+        inputs.append((work.logits.to(device), to_device(work.buffers, device)))
+
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+
+    def step(i: int):
+
+        logits, buffers = inputs[i % sets]
+
+        return sampler.autoregressive(logits, buffers, update_counts=True, logprobs=True,
+                                      philox_seed=1234 if philox else None, philox_offset=i)
+
+    for i in range(warmup):
+
+        step(i)
+
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    wall0 = time.perf_counter()
+
+    for i in range(steps):
+
+        events[i][0].record(stream)
+        step(i)
+        events[i][1].record(stream)
+
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    launch_us = [a.elapsed_time(b) * 1e3 for a, b in events]
+    kernel_us = statistics.mean(launch_us)
+    algorithmic = c1_algorithmic_bytes(batch, vocab)
+    achieved = algorithmic / (kernel_us * 1e-6) / 1e9
+
+    result = {
+        "metric": "fused decode-sample us/step + achieved HBM GB/s, B=64 V=128256 bf16",
+        "value": round(kernel_us, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (spiked N(0,3^2) logits, config-1 sampling parameters, Philox noise)",
+        "config": {
+            "workload": "config 1: UnshardedFusedSingular.autoregressive B=64 V=128256 bf16, "
+                        "penalties + bias + temperature + top-k/top-p/min-p + Gumbel-max, "
+                        "logprobs + top-5, update_counts",
+            "rows": batch,
+            "vocab": vocab,
+            "input_sets_rotated": sets,
+            "achieved_hbm_gbs": round(achieved, 1),
+            "rows_per_s": round(batch / (kernel_us * 1e-6), 1),
+            "median_us": round(statistics.median(launch_us), 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+
+    if cpu_rows > 0:
+
+        sys.path.insert(0, str(ROOT))
+        result["cpu_baseline"] = cpu_baseline_c1(base, cpu_rows)
+
+    return result
+
+
+def main(argv=None) -> int:
+
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--cpu-rows", type=int, default=8,
+                        help="rows of config 1 timed for the CPU baseline (0 to skip)")
+    parser.add_argument("--buffer-noise", action="store_true",
+                        help="read Gumbel noise from the buffers instead of the Philox stream")
+    args = parser.parse_args(argv)
+
+    if args.gpus != 1:
+
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the sampling path "
+              "shards by batch with no exchange, so N GPUs run N independent copies)", file=sys.stderr)
+
+        return 2
+
+    result = run_bench(args.steps, args.warmup, cpu_rows=args.cpu_rows, philox=not args.buffer_noise)
+    print(json.dumps(result), flush=True)
+
+    return 0
+
+
+if __name__ == "__main__":
+
+    sys.exit(main())

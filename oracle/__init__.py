@@ -1,0 +1,19 @@
+"""CPU oracle for the fused sampling / verification path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import
+this package, and only as the checker (or the timed CPU baseline). The product
+(``sonic-sampler_amd/sonic_sampler``) never imports it and has no CPU fallback.
+
+Contents:
+
+* ``oracle.sampler`` -- a per-request restatement of the reference's PyTorch path
+  (``src/sonic_sampler/core/naive.py`` of tachyontrails/sonic-sampler) in torch CPU operations with
+  the same dtypes and rounding points, composed per row so that slot mapping, d2t indirection,
+  variable lookahead and decode-count updates are covered (the reference's ``NaiveSampler`` has
+  none of these; hazard list in DESIGN.md);
+* ``oracle.topk`` -- bounded top-k as a stable descending sort;
+* ``oracle.philox`` -- Philox4x32-10 in numpy and the Gumbel transform of the noise stream.
+
+Each function cites the reference file:line it restates. How each is pinned (golden vectors,
+closed forms, brute force) is listed in ``tests/test_oracle.py`` and DESIGN.md.
+"""

@@ -1,0 +1,282 @@
+// Fused chain speculative verification in one launch (replaces K1 ops/prologue.py:272-472, K5
+// ops/multistep.py:76-226 and K6 ops/verify.py:244-434 of the reference).
+//
+// Grid: rows * tiles workgroups, rows = B * (gamma + 1) or cu_seqlens[B] (variable lookahead).
+//   tile stage    every workgroup: prologue over one tile of one row -> tile argmax / top-128;
+//   row stage     last workgroup of a row (row ticket): merge -> truncation -> fp32 log_softmax,
+//                 written to values / indices [row, 128] (greedy rows: the argmax in indices);
+//   request stage last row of a request to finish (request ticket): greedy or stochastic chain
+//                 verification, residual resampling, logprobs, top-Z, decode-count update.
+// Semantics follow the reference's PyTorch path (core/naive.py:497-646 `verification`,
+// :694-708 `multistep`), applied per request so that slots and variable lookahead compose.
+#include "ss_sampling.h"
+#include "../../include/sonic_sampler.h"
+
+namespace ss {
+
+struct Request {
+    int b, margin, n;
+};
+
+__device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, int row) {
+    Request r;
+    if (a.cu_seqlens) {
+        int lo = 0, hi = a.batch;  // invariant: cu[lo] <= row < cu[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (a.cu_seqlens[mid] <= row) lo = mid; else hi = mid;
+        }
+        r.b = lo;
+        r.margin = a.cu_seqlens[lo];
+        r.n = a.cu_seqlens[lo + 1] - r.margin;
+    } else {
+        r.n = a.lookahead + 1;
+        r.b = row / r.n;
+        r.margin = r.b * r.n;
+    }
+    return r;
+}
+
+// First sorted position in row `rowi` whose token equals d, or -1 (wave 0).
+__device__ __forceinline__ int find_position(const int32_t *idx, int d) {
+    const int lane = lane_id();
+    const uint64_t m0 = __ballot(idx[2 * lane] == d);
+    const uint64_t m1 = __ballot(idx[2 * lane + 1] == d);
+    const int p0 = m0 ? 2 * (__ffsll((unsigned long long)m0) - 1) : 1 << 20;
+    const int p1 = m1 ? 2 * (__ffsll((unsigned long long)m1) - 1) + 1 : 1 << 20;
+    const int p = p0 < p1 ? p0 : p1;
+    return p < SS_K ? p : -1;
+}
+
+template <int E, bool VEC>
+__global__ __launch_bounds__(SS_BLOCK) void multistep_kernel(ss_multistep_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x / tiles;
+    const int tile = blockIdx.x - row * tiles;
+    const Request rq = resolve_request(a, row);
+    const int step = row - rq.margin;
+    // Rows outside every request, or requests longer than lookahead + 1, break the layout
+    // contract; they are skipped (their outputs stay unwritten) rather than read out of bounds.
+    if (step < 0 || step >= rq.n || rq.n > a.lookahead + 1) return;
+    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
+    const uint32_t ind = a.indicators[slot];
+    const bool greedy = (ind & IND_GREEDY) != 0;
+
+    RowState rs;
+    rs.ind = ind;
+    rs.logits = a.logits + (int64_t)row * a.stride_logits;
+    rs.d2t = nullptr;
+    rs.grammar = a.grammar ? a.grammar + (int64_t)slot * a.grammar_stride_slot +
+                                 (int64_t)step * a.grammar_stride_step
+                           : nullptr;
+    rs.ctx = a.context_counts ? a.context_counts + (int64_t)slot * a.stride_context : nullptr;
+    rs.dec = a.decode_counts ? a.decode_counts + (int64_t)slot * a.stride_decode : nullptr;
+    rs.bias = a.logit_bias ? a.logit_bias + (int64_t)slot * a.stride_bias : nullptr;
+    rs.rep = (ind & IND_MULT) && a.repetition ? bf2f(a.repetition[slot]) : 1.0f;
+    rs.freq = (ind & IND_FREQ) && a.frequency ? bf2f(a.frequency[slot]) : 0.0f;
+    rs.pres = (ind & IND_PRES) && a.presence ? bf2f(a.presence[slot]) : 0.0f;
+    rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
+    if (!a.temperature) rs.ind &= ~IND_TEMP;
+    rs.nhist = 0;
+    if (step > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
+        // Step s of a request sees the drafts of steps < s as extra decode history
+        // (core/naive.py:179-198, the `tril` history with timestep None).
+        rs.nhist = step;
+        if ((int)threadIdx.x < step) sm.hist[threadIdx.x] = a.drafted_tokens[rq.margin + threadIdx.x];
+        __syncthreads();
+    }
+
+    uint32_t keys[E];
+    prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
+    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    tile_stage<E>(sm, greedy, keys, scr, tile);
+
+    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
+
+    // ---- row stage ------------------------------------------------------------------------------
+    float *vrow = a.values + (int64_t)row * SS_K;
+    int32_t *irow = a.indices + (int64_t)row * SS_K;
+    if (greedy) {
+        if (threadIdx.x < 64) {
+            const int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
+            if (threadIdx.x == 0) {
+                irow[0] = token;
+                vrow[0] = 0.0f;
+            }
+        }
+    } else {
+        float v0 = 0.f, v1 = 0.f;
+        int i0 = 0, i1 = 0;
+        merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+        if (threadIdx.x < 64) {
+            truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
+                     a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
+            float m, x0, x1;
+            const float logs = logf(exp_parts(v0, v1, m, x0, x1));
+            const int e0 = 2 * threadIdx.x;
+            vrow[e0] = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
+            vrow[e0 + 1] = (v1 - m) - logs;
+            irow[e0] = i0;
+            irow[e0 + 1] = i1;
+        }
+    }
+
+    if (!arrive(a.tickets + a.rows + rq.b, rq.n, &sm.sel.flag)) return;
+    if (threadIdx.x >= 64) return;
+
+    // ---- request stage (wave 0) -------------------------------------------------------------------
+    const int lane = threadIdx.x;
+    const int e0 = 2 * lane, e1 = e0 + 1;
+    const int n = rq.n;
+    const int32_t *drafted = a.drafted_tokens + rq.margin;
+    const float *vals = a.values + (int64_t)rq.margin * SS_K;
+    const int32_t *idxs = a.indices + (int64_t)rq.margin * SS_K;
+    const bool svgd = (ind & IND_SVGD) || !a.draft_probabilities;
+    const uint16_t *q = a.draft_probabilities
+                            ? a.draft_probabilities + (int64_t)slot * a.probs_stride_slot
+                            : nullptr;
+
+    int j = n - 1;
+    int token;
+    if (greedy) {
+        for (int i = 0; i < n - 1; ++i) {
+            if (idxs[(int64_t)i * SS_K] != drafted[i]) {
+                j = i;
+                break;
+            }
+        }
+        token = idxs[(int64_t)j * SS_K];
+    } else {
+        const uint16_t *u = a.uniform + (int64_t)slot * a.stride_uniform;
+        for (int i = 0; i < n - 1; ++i) {
+            const int d = drafted[i];
+            const bool in_vocab = d >= 0 && d < a.vocab_size;
+            const int pos = find_position(idxs + (int64_t)i * SS_K, d);
+            const float p = pos >= 0 ? expf(vals[(int64_t)i * SS_K + pos]) : 0.0f;
+            const float qd = svgd ? 1.0f
+                                  : (in_vocab ? bf2f(q[(int64_t)i * a.probs_stride_step + d]) : 0.0f);
+            // bf16(u * q) <= p  (core/naive.py:594-599)
+            if (!(rbf(bf2f(u[i]) * qd) <= p)) {
+                j = i;
+                break;
+            }
+        }
+        const int32_t *cj = idxs + (int64_t)j * SS_K;
+        const float *lj = vals + (int64_t)j * SS_K;
+        const int c0 = cj[e0], c1 = cj[e1];
+        const float p0 = expf(lj[e0]), p1 = expf(lj[e1]);
+        float r0, r1;
+        if (j == n - 1) {
+            r0 = p0;
+            r1 = p1;
+        } else if (svgd) {
+            // q is a point mass on the draft: the residual zeroes the drafted candidate.
+            const int dj = drafted[j];
+            r0 = c0 == dj ? 0.0f : p0;
+            r1 = c1 == dj ? 0.0f : p1;
+        } else {
+            const uint16_t *qj = q + (int64_t)j * a.probs_stride_step;
+            r0 = fmaxf(p0 - bf2f(qj[c0]), 0.0f);
+            r1 = fmaxf(p1 - bf2f(qj[c1]), 0.0f);
+        }
+        float w0, w1;
+        if (a.philox.enabled) {
+            w0 = philox_gumbel(a.philox.seed, a.philox.offset, slot, j, c0);
+            w1 = philox_gumbel(a.philox.seed, a.philox.offset, slot, j, c1);
+        } else {
+            const uint16_t *g = a.gumbel + (int64_t)slot * a.gumbel_stride_slot +
+                                (int64_t)j * a.gumbel_stride_step;
+            w0 = bf2f(g[c0]);
+            w1 = bf2f(g[c1]);
+        }
+        const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
+        token = __shfl((sel & 1) ? c1 : c0, sel >> 1, 64);
+
+        if (a.return_logprobs && a.logprobs) {
+            for (int i = 0; i <= j; ++i) {
+                int pos;
+                if (i == j) {
+                    pos = sel;
+                } else {
+                    pos = find_position(idxs + (int64_t)i * SS_K, drafted[i]);
+                    if (pos < 0) pos = 0;  // argmax of an all-false match row (core/naive.py:580-584)
+                }
+                if (lane == 0)
+                    a.logprobs[rq.margin + i] = (uint16_t)f2bf(vals[(int64_t)i * SS_K + pos]);
+            }
+            if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
+                int lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
+                lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
+                for (int i = 0; i <= j; ++i) {
+                    const int64_t o = (int64_t)(rq.margin + i) * a.stride_top;
+                    const int64_t s = (int64_t)i * SS_K;
+                    if (e0 < lim) {
+                        a.top_values[o + e0] = (uint16_t)f2bf(vals[s + e0]);
+                        a.top_tokens[o + e0] = idxs[s + e0];
+                    }
+                    if (e1 < lim) {
+                        a.top_values[o + e1] = (uint16_t)f2bf(vals[s + e1]);
+                        a.top_tokens[o + e1] = idxs[s + e1];
+                    }
+                }
+            }
+        }
+    }
+    if (greedy && a.return_logprobs && a.logprobs) {
+        if (lane <= j) a.logprobs[rq.margin + lane] = 0;
+    }
+    if (a.update_counts && a.decode_counts && lane <= j) {
+        const int tok = lane < j ? drafted[lane] : token;
+        if (tok >= 0 && tok < a.vocab_size)
+            atomicAdd(a.decode_counts + (int64_t)slot * a.stride_decode + tok, 1);
+    }
+    if (lane == 0) {
+        a.out_tokens[rq.margin + j] = token;
+        a.offsets[rq.b] = j;
+    }
+}
+
+template <bool VEC>
+static int launch_multistep(const ss_multistep_args *a, int tiles) {
+    dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
+    hipStream_t s = (hipStream_t)a->stream;
+    switch (a->block_n) {
+        case 1024: hipLaunchKernelGGL((multistep_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((multistep_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((multistep_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((multistep_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        default: return SS_ERR_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
+}
+
+static bool aligned_ms(const void *p, int64_t stride, int bytes) {
+    if (!p) return true;
+    return ((uintptr_t)p % bytes) == 0 && (stride % 4) == 0;
+}
+
+}  // namespace ss
+
+extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
+    using namespace ss;
+    if (!a || !a->logits || !a->indicators || !a->drafted_tokens || !a->out_tokens || !a->offsets ||
+        !a->values || !a->indices || !a->scratch || !a->tickets || !a->uniform)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows < 0 || a->batch < 0 || a->vocab_size <= 0 || a->stride_logits < a->vocab_size)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->lookahead < 0 || a->lookahead > 63) return SS_ERR_INVALID_ARGUMENT;
+    if (!a->cu_seqlens && a->rows != a->batch * (a->lookahead + 1)) return SS_ERR_INVALID_ARGUMENT;
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+        return SS_ERR_UNSUPPORTED;
+    const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
+    if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->max_top_logprobs < 0 || a->max_top_logprobs > SS_MAX_K) return SS_ERR_INVALID_ARGUMENT;
+    if (!a->philox.enabled && !a->gumbel) return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows == 0 || a->batch == 0) return SS_OK;
+    const bool vec = (a->vocab_size % 4) == 0 && aligned_ms(a->logits, a->stride_logits, 8) &&
+                     aligned_ms(a->decode_counts, a->stride_decode, 16) &&
+                     aligned_ms(a->context_counts, a->stride_context, 16) &&
+                     aligned_ms(a->logit_bias, a->stride_bias, 8);
+    return vec ? launch_multistep<true>(a, tiles) : launch_multistep<false>(a, tiles);
+}

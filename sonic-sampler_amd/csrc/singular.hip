@@ -1,0 +1,183 @@
+// Fused single-step sampling in one launch (replaces K1 ops/prologue.py:272-472 followed by K4
+// ops/singular.py:154-358 of the reference).
+//
+// Grid: rows * tiles workgroups. Every workgroup runs the logit-processor prologue over one
+// vocabulary tile of one row and leaves either the tile argmax (greedy rows) or its exact top-128
+// in the row's scratch. The last workgroup of the row merges the candidates and performs the
+// selection: truncation, d2t remap, Gumbel-max over bf16(v - w), decode-count update, logprobs,
+// top-Z logprobs and the draft-probability scatter. Semantics follow the reference's PyTorch path
+// (core/naive.py:377-495 `selection`, :648-692 `preamble` / `singular`).
+#include "ss_sampling.h"
+#include "../../include/sonic_sampler.h"
+
+namespace ss {
+
+template <int E, bool VEC>
+__global__ __launch_bounds__(SS_BLOCK) void singular_kernel(ss_singular_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x / tiles;
+    const int tile = blockIdx.x - row * tiles;
+    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
+    const uint32_t ind = a.indicators[slot];
+    const bool greedy = (ind & IND_GREEDY) != 0;
+
+    RowState rs;
+    rs.ind = ind;
+    rs.logits = a.logits + (int64_t)row * a.stride_logits;
+    rs.d2t = a.d2t;
+    rs.grammar = a.grammar ? a.grammar + (int64_t)slot * a.stride_grammar : nullptr;
+    rs.ctx = a.context_counts ? a.context_counts + (int64_t)slot * a.stride_context : nullptr;
+    rs.dec = a.decode_counts ? a.decode_counts + (int64_t)slot * a.stride_decode : nullptr;
+    rs.bias = a.logit_bias ? a.logit_bias + (int64_t)slot * a.stride_bias : nullptr;
+    rs.rep = (ind & IND_MULT) && a.repetition ? bf2f(a.repetition[slot]) : 1.0f;
+    rs.freq = (ind & IND_FREQ) && a.frequency ? bf2f(a.frequency[slot]) : 0.0f;
+    rs.pres = (ind & IND_PRES) && a.presence ? bf2f(a.presence[slot]) : 0.0f;
+    rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
+    if (!a.temperature) rs.ind &= ~IND_TEMP;
+    rs.nhist = 0;
+    if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
+        rs.nhist = a.timestep;
+        if ((int)threadIdx.x < rs.nhist)
+            sm.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
+        __syncthreads();
+    }
+
+    uint32_t keys[E];
+    prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
+    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    tile_stage<E>(sm, greedy, keys, scr, tile);
+
+    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
+
+    if (greedy) {
+        if (threadIdx.x < 64) {
+            int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
+            if (a.d2t) token = a.d2t[token];
+            if (threadIdx.x == 0) {
+                if (a.update_counts && a.decode_counts) {
+                    int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
+                    if (a.is_prefill) atomicExch(d, 1); else atomicAdd(d, 1);
+                }
+                if (a.return_logprobs && a.logprobs) a.logprobs[(int64_t)row * a.stride_logprobs] = 0;
+                a.tokens[(int64_t)row * a.stride_tokens] = token;
+            }
+        }
+        return;
+    }
+
+    float v0 = 0.f, v1 = 0.f;
+    int i0 = 0, i1 = 0;
+    merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    if (threadIdx.x >= 64) return;
+
+    const int lane = threadIdx.x;
+    const int e0 = 2 * lane, e1 = e0 + 1;
+    truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
+             a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
+    if (a.d2t) {
+        i0 = a.d2t[i0];
+        i1 = a.d2t[i1];
+    }
+    float w0, w1;
+    if (a.philox.enabled) {
+        w0 = philox_gumbel(a.philox.seed, a.philox.offset, slot, a.philox_step, i0);
+        w1 = philox_gumbel(a.philox.seed, a.philox.offset, slot, a.philox_step, i1);
+    } else {
+        const uint16_t *g = a.gumbel + (int64_t)slot * a.stride_gumbel;
+        w0 = bf2f(g[i0]);
+        w1 = bf2f(g[i1]);
+    }
+    const int sel = wave_argmax_first(rbf(v0 - w0), rbf(v1 - w1));
+    const int token = __shfl((sel & 1) ? i1 : i0, sel >> 1, 64);
+
+    if (lane == 0 && a.update_counts && a.decode_counts) {
+        int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
+        if (a.is_prefill) atomicExch(d, 1); else atomicAdd(d, 1);
+    }
+
+    const bool want_lp = a.return_logprobs && a.logprobs;
+    const bool want_probs = a.return_probabilities && a.probabilities;
+    if (want_lp || want_probs) {
+        float m, x0, x1;
+        const float s = exp_parts(v0, v1, m, x0, x1);
+        const float logs = logf(s);
+        float o0, o1;  // the logprob of each element as the reference computes it
+        if (want_probs) {
+            // log_softmax in fp32: (v - max) - log(sum)
+            o0 = (v0 - m) - logs;
+            o1 = (v1 - m) - logs;
+            uint16_t *p = a.probabilities + (int64_t)slot * a.stride_probabilities;
+            p[i0] = (uint16_t)f2bf(expf(o0));
+            p[i1] = (uint16_t)f2bf(expf(o1));
+        } else {
+            // v - logsumexp(v), logsumexp = max + log(sum(exp(v - max)))
+            const float lse = m + logs;
+            o0 = v0 - lse;
+            o1 = v1 - lse;
+        }
+        if (want_lp) {
+            const float osel = __shfl((sel & 1) ? o1 : o0, sel >> 1, 64);
+            if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
+            if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
+                int lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
+                lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
+                const int64_t o = (int64_t)row * a.stride_top;
+                if (e0 < lim) {
+                    a.top_values[o + e0] = (uint16_t)f2bf(o0);
+                    a.top_tokens[o + e0] = i0;
+                }
+                if (e1 < lim) {
+                    a.top_values[o + e1] = (uint16_t)f2bf(o1);
+                    a.top_tokens[o + e1] = i1;
+                }
+            }
+        }
+    }
+    if (lane == 0) a.tokens[(int64_t)row * a.stride_tokens] = token;
+}
+
+template <bool VEC>
+static int launch_singular(const ss_singular_args *a, int tiles) {
+    dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
+    hipStream_t s = (hipStream_t)a->stream;
+    switch (a->block_n) {
+        case 1024: hipLaunchKernelGGL((singular_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((singular_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((singular_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((singular_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        default: return SS_ERR_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
+}
+
+static bool aligned(const void *p, int64_t stride, int bytes_per_vec) {
+    if (!p) return true;
+    return ((uintptr_t)p % bytes_per_vec) == 0 && (stride % 4) == 0;
+}
+
+}  // namespace ss
+
+extern "C" int ss_fused_singular(const ss_singular_args *a) {
+    using namespace ss;
+    if (!a || !a->logits || !a->indicators || !a->tokens || !a->scratch || !a->tickets)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows < 0 || a->vocab_size <= 0 || a->stride_logits < a->vocab_size)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+        return SS_ERR_UNSUPPORTED;
+    const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
+    if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->timestep < 0 || a->timestep > 64) return SS_ERR_INVALID_ARGUMENT;
+    if (a->max_top_logprobs < 0 || a->max_top_logprobs > SS_MAX_K) return SS_ERR_INVALID_ARGUMENT;
+    if (!a->philox.enabled && !a->gumbel) return SS_ERR_INVALID_ARGUMENT;
+    if (a->return_logprobs && a->max_top_logprobs > 0 && a->top_values && !a->top_tokens)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows == 0) return SS_OK;
+    const bool direct = a->d2t == nullptr;
+    const bool vec = (a->vocab_size % 4) == 0 && aligned(a->logits, a->stride_logits, 8) &&
+                     (!direct || (aligned(a->decode_counts, a->stride_decode, 16) &&
+                                  aligned(a->context_counts, a->stride_context, 16) &&
+                                  aligned(a->logit_bias, a->stride_bias, 8)));
+    return vec ? launch_singular<true>(a, tiles) : launch_singular<false>(a, tiles);
+}

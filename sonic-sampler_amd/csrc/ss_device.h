@@ -1,0 +1,168 @@
+// Device helpers shared by every kernel of the library: bf16 rounding, order-preserving keys,
+// wave64 / workgroup scans and reductions, and the cross-workgroup arrival ticket.
+//
+// All kernels run with SS_BLOCK = 256 threads (four wave64 wavefronts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SS_BLOCK 256
+#define SS_WAVES (SS_BLOCK / 64)
+#define SS_K 128
+
+namespace ss {
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32. Rounding is round-to-nearest-even, which is what torch applies when it stores a
+// float32 intermediate into a bfloat16 tensor on the CPU, so every rounding point of the
+// reference's PyTorch path can be reproduced exactly.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// ---------------------------------------------------------------------------------------------
+// Order-preserving unsigned keys. A larger key means a larger value; -0 is folded onto +0 so that
+// equal values compare equal, as they do in torch's sort. Key 0 is never produced by a non-NaN
+// value and serves as the "absent element" sentinel.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t key16(uint32_t h) {
+    h &= 0xffffu;
+    if ((h & 0x7fffu) == 0) h = 0;
+    return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+}
+
+__device__ __forceinline__ uint32_t unkey16(uint32_t k) {
+    k &= 0xffffu;
+    return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+}
+
+__device__ __forceinline__ uint32_t key32(uint32_t u) {
+    if ((u & 0x7fffffffu) == 0) u = 0;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t unkey32(uint32_t k) {
+    return (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wave64 primitives.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        uint32_t n = __shfl_up(v, off, 64);
+        if (lane >= off) v += n;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        uint64_t o = __shfl_xor(v, off, 64);
+        v = v > o ? v : o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_inclusive_sum_f64(double v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        double n = __shfl_up(v, off, 64);
+        if (lane >= off) v += n;
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Workgroup-wide exclusive prefix sum of NV independent 32-bit lanes of data per thread, in
+// thread order. `totals` receives the workgroup totals. `tmp` must hold SS_WAVES * NV words.
+// ---------------------------------------------------------------------------------------------
+template <int NV>
+__device__ __forceinline__ void block_exclusive_scan(uint32_t (&v)[NV], uint32_t (&totals)[NV],
+                                                     uint32_t *tmp) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    uint32_t inc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) inc[i] = wave_inclusive_sum(v[i]);
+    if (lane == 63) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) tmp[wave * NV + i] = inc[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        uint32_t before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < SS_WAVES; ++w) {
+            uint32_t t = tmp[w * NV + i];
+            before += (w < wave) ? t : 0u;
+            total += t;
+        }
+        v[i] = before + inc[i] - v[i];
+        totals[i] = total;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cross-workgroup arrival ticket. Every workgroup of a group calls arrive() after writing its
+// partial results; exactly one (the last to arrive) gets `true`, after which the partial results
+// of all others are visible to it. The last arriver resets the counter so that the next launch
+// (or the next replay of a captured graph) starts from zero again.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool arrive(int32_t *counter, int32_t expected, int32_t *flag_smem) {
+    __threadfence();  // release this thread's global writes at agent scope
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t old = atomicAdd(counter, 1);
+        int32_t last = (old == expected - 1);
+        if (last) *counter = 0;
+        *flag_smem = last;
+    }
+    __syncthreads();
+    bool last = *flag_smem != 0;
+    if (last) __threadfence();  // acquire: later loads observe the other workgroups' writes
+    return last;
+}
+
+}  // namespace ss

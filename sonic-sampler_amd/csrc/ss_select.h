@@ -1,0 +1,195 @@
+// Exact, stable bounded top-k selection for one workgroup (SS_BLOCK threads).
+//
+// Elements are unsigned keys (see key16 / key32); a larger key is a better element and key 0 is
+// the "absent" sentinel. Each thread owns E keys laid out in "chunks" of CH consecutive elements:
+// element j of thread t has order position
+//     (j / CH) * (SS_BLOCK * CH) + t * CH + (j % CH)
+// which is the order of 16-byte (or 8-byte) coalesced loads, so the order position equals the
+// column offset inside a vocabulary tile. Selection returns exactly `need` elements: every key
+// above a threshold plus the first `margin` keys equal to it in order position, i.e. ties go to
+// the lowest position, the rule torch's stable descending sort applies (reference semantics:
+// ops/encoding.py:63-91 packs the inverted index below the key for the same effect).
+//
+// The threshold is found MSB-first with LDS histograms: a 12-bit first digit (4096 bins) keeps
+// same-address LDS atomics rare on low-entropy logits, whose keys share sign and exponent bits,
+// then the remaining 4 (16-bit keys) or 12 + 8 (32-bit keys) bits.
+#pragma once
+
+#include "ss_device.h"
+
+namespace ss {
+
+struct SelectSmem {
+    uint32_t hist[4096];
+    uint32_t scan[SS_WAVES * 8];
+    uint32_t result[4];
+    int32_t flag;
+};
+
+// Finds the largest bin b of hist[0, nbins) with (count of bins >= b) >= need. Returns the bin,
+// the count strictly above it and the bin's own count. All threads must call.
+__device__ __forceinline__ void find_bin(SelectSmem &sm, int nbins, uint32_t need, uint32_t &bin,
+                                         uint32_t &above, uint32_t &count) {
+    const int tid = threadIdx.x;
+    const int per = nbins >= SS_BLOCK ? nbins / SS_BLOCK : 1;
+    const int owners = nbins >= SS_BLOCK ? SS_BLOCK : nbins;
+    if (tid == 0) {
+        sm.result[0] = 0;
+        sm.result[1] = 0;
+        sm.result[2] = 0;
+    }
+    uint32_t s = 0;
+    if (tid < owners) {
+        for (int i = 0; i < per; ++i) s += sm.hist[tid * per + i];
+    }
+    uint32_t v[1] = {s}, tot[1];
+    block_exclusive_scan<1>(v, tot, sm.scan);
+    // v[0] = sum of bins below this thread's range.
+    const uint32_t above_me = tot[0] - v[0] - s;
+    if (tid < owners && above_me < need && need <= above_me + s) {
+        uint32_t run = above_me;
+        for (int b = tid * per + per - 1; b >= tid * per; --b) {
+            uint32_t h = sm.hist[b];
+            if (run + h >= need) {
+                sm.result[0] = (uint32_t)b;
+                sm.result[1] = run;
+                sm.result[2] = h;
+                break;
+            }
+            run += h;
+        }
+    }
+    __syncthreads();
+    bin = sm.result[0];
+    above = sm.result[1];
+    count = sm.result[2];
+    __syncthreads();
+}
+
+// Threshold over keys supplied super-chunk by super-chunk: `load(sc, keys)` fills this thread's
+// E keys of super-chunk sc (absent elements as 0). On return the selection rule is
+//     select  <=>  (key >> level) > thi  ||  ((key >> level) == thi && rank_among_equal < margin)
+template <int E, int KEYBITS, class Loader>
+__device__ void radix_threshold(SelectSmem &sm, int nsc, Loader load, uint32_t need, uint32_t &thi,
+                                int &level, uint32_t &margin) {
+    constexpr int ND = KEYBITS == 16 ? 2 : 3;
+    const int shifts[3] = {KEYBITS - 12, KEYBITS == 16 ? 0 : 8, 0};
+    const int widths[3] = {12, KEYBITS == 16 ? 4 : 12, 8};
+    uint32_t prefix = 0, pmask = 0, remaining = need;
+    int lvl = KEYBITS;
+    for (int d = 0; d < ND; ++d) {
+        const int sh = shifts[d];
+        const int nb = 1 << widths[d];
+        const uint32_t dm = (uint32_t)nb - 1u;
+        for (int i = threadIdx.x; i < nb; i += SS_BLOCK) sm.hist[i] = 0;
+        __syncthreads();
+        for (int sc = 0; sc < nsc; ++sc) {
+            uint32_t keys[E];
+            load(sc, keys);
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                if ((keys[j] & pmask) == prefix) atomicAdd(&sm.hist[(keys[j] >> sh) & dm], 1u);
+            }
+        }
+        __syncthreads();
+        uint32_t b, above, cnt;
+        find_bin(sm, nb, remaining, b, above, cnt);
+        remaining -= above;
+        prefix |= b << sh;
+        pmask |= dm << sh;
+        lvl = sh;
+        if (remaining == cnt) break;  // the whole bin is taken: no finer digit needed
+    }
+    level = lvl;
+    thi = prefix >> lvl;
+    margin = remaining;
+}
+
+// Emits the selected elements in order position. `emit(pos, sc, j)` is called for element j of
+// super-chunk sc with its output position pos in [0, need). Positions are dense and increasing in
+// order position. Elements of one thread are visited in increasing order position.
+template <int E, int CH, class Loader, class Emit>
+__device__ void compact(SelectSmem &sm, int nsc, Loader load, uint32_t thi, int level,
+                        uint32_t margin, Emit emit) {
+    constexpr int NCH = E / CH;
+    uint32_t base_gt = 0, base_eq = 0;
+    for (int sc = 0; sc < nsc; ++sc) {
+        uint32_t keys[E];
+        load(sc, keys);
+        uint32_t cnt[NCH], tot[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            uint32_t g = 0, q = 0;
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const uint32_t kh = keys[c * CH + i] >> level;
+                g += kh > thi;
+                q += kh == thi;
+            }
+            cnt[c] = g | (q << 16);
+        }
+        block_exclusive_scan<NCH>(cnt, tot, sm.scan);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            uint32_t g = base_gt + (cnt[c] & 0xffffu);
+            uint32_t q = base_eq + (cnt[c] >> 16);
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int j = c * CH + i;
+                const uint32_t kh = keys[j] >> level;
+                if (kh > thi) {
+                    emit(g + (q < margin ? q : margin), sc, j);
+                    ++g;
+                } else if (kh == thi) {
+                    if (q < margin) emit(g + q, sc, j);
+                    ++q;
+                }
+            }
+            base_gt += tot[c] & 0xffffu;
+            base_eq += tot[c] >> 16;
+        }
+    }
+}
+
+// Order position of element j of this thread inside super-chunk sc.
+template <int E, int CH>
+__device__ __forceinline__ int order_pos(int sc, int j) {
+    return sc * (SS_BLOCK * E) + (j / CH) * (SS_BLOCK * CH) + (int)threadIdx.x * CH + (j % CH);
+}
+
+// Sorts 128 64-bit composites held by wave 0 (two per lane: element 2*lane + i) in descending
+// order with a bitonic network over lanes. Composites must be distinct for a deterministic order.
+__device__ __forceinline__ void wave_sort128_desc(uint64_t &a0, uint64_t &a1) {
+    const int lane = lane_id();
+    // element index e = 2 * lane + i
+#pragma unroll
+    for (int size = 2; size <= 128; size <<= 1) {
+#pragma unroll
+        for (int dist = size >> 1; dist > 0; dist >>= 1) {
+            if (dist == 1) {
+                // partner inside the lane: elements 2*lane and 2*lane+1
+                const int e0 = 2 * lane;
+                const bool desc = ((e0 & size) == 0);
+                const uint64_t lo = a0 < a1 ? a0 : a1, hi = a0 < a1 ? a1 : a0;
+                a0 = desc ? hi : lo;
+                a1 = desc ? lo : hi;
+            } else {
+                const int ld = dist >> 1;  // lane distance
+                const uint64_t p0 = __shfl_xor(a0, ld, 64);
+                const uint64_t p1 = __shfl_xor(a1, ld, 64);
+                const bool lower = (lane & ld) == 0;  // this lane holds the lower element index
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int e = 2 * lane + i;
+                    const bool desc = ((e & size) == 0);
+                    uint64_t mine = i ? a1 : a0, other = i ? p1 : p0;
+                    const uint64_t hi = mine > other ? mine : other, lo = mine > other ? other : mine;
+                    const uint64_t res = (lower == desc) ? hi : lo;
+                    if (i) a1 = res; else a0 = res;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace ss

@@ -1,0 +1,160 @@
+// Bounded top-k over [rows, vocab] logits in one launch (replaces K2 ops/topk/bitpack.py:99-158
+// followed by K3 ops/topk/unpack.py:312-377 of the reference).
+//
+// Grid: rows * tiles workgroups, row-major so that the tiles of a row are dispatched together.
+// Tile stage: each workgroup streams block_n logits with coalesced 8/16-byte loads, turns them into
+// order-preserving keys and writes its exact top-k (ties to the lowest column) to the scratch row
+// in column order. Merge stage: the last workgroup of a row to arrive (arrival ticket) selects the
+// row's top-k among the tiles*k candidates, sorts them by (value desc, column asc) with a wave64
+// bitonic network and writes values / indices densely as [rows, k].
+#include "ss_select.h"
+#include "../../include/sonic_sampler.h"
+
+namespace ss {
+
+struct TopkSmem {
+    SelectSmem sel;
+    uint64_t cand[SS_K];
+    int32_t idx[SS_K];
+};
+
+template <bool F32>
+struct TopkTraits;
+
+template <>
+struct TopkTraits<false> {
+    using Cand = uint32_t;
+    static constexpr int KEYBITS = 16;
+    __device__ static uint32_t key_of(const void *p, int64_t off) {
+        return key16(((const uint16_t *)p)[off]);
+    }
+    __device__ static Cand pack(uint32_t key, int li) { return (key << 16) | (uint32_t)li; }
+    __device__ static uint32_t cand_key(Cand c) { return c >> 16; }
+    __device__ static int cand_li(Cand c) { return (int)(c & 0xffffu); }
+};
+
+template <>
+struct TopkTraits<true> {
+    using Cand = uint64_t;
+    static constexpr int KEYBITS = 32;
+    __device__ static uint32_t key_of(const void *p, int64_t off) {
+        return key32(__float_as_uint(((const float *)p)[off]));
+    }
+    __device__ static Cand pack(uint32_t key, int li) { return ((uint64_t)key << 32) | (uint32_t)li; }
+    __device__ static uint32_t cand_key(Cand c) { return (uint32_t)(c >> 32); }
+    __device__ static int cand_li(Cand c) { return (int)(c & 0xffffffffu); }
+};
+
+template <bool F32, int E>
+__global__ __launch_bounds__(SS_BLOCK) void topk_kernel(ss_topk_args a, int tiles) {
+    using Tr = TopkTraits<F32>;
+    using Cand = typename Tr::Cand;
+    constexpr int CH = 4;
+    __shared__ TopkSmem sm;
+
+    const int row = blockIdx.x / tiles;
+    const int tile = blockIdx.x - row * tiles;
+    const int V = a.vocab_size;
+    const int k = a.k;
+    const int64_t base = (int64_t)row * a.stride_logits;
+    const int col0 = tile * a.block_n;
+
+    // ---- tile stage ---------------------------------------------------------------------------
+    uint32_t keys[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int li = order_pos<E, CH>(0, j);
+        const int col = col0 + li;
+        keys[j] = col < V ? Tr::key_of(a.logits, base + col) : 0u;
+    }
+    auto tile_load = [&](int, uint32_t(&out)[E]) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) out[j] = keys[j];
+    };
+    uint32_t thi, margin;
+    int level;
+    radix_threshold<E, Tr::KEYBITS>(sm.sel, 1, tile_load, (uint32_t)k, thi, level, margin);
+    Cand *scr = (Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+    compact<E, CH>(sm.sel, 1, tile_load, thi, level, margin, [&](uint32_t pos, int, int j) {
+        if (pos < (uint32_t)k) scr[tile * k + (int)pos] = Tr::pack(keys[j], order_pos<E, CH>(0, j));
+    });
+
+    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
+
+    // ---- merge stage (last workgroup of the row) ----------------------------------------------
+    constexpr int EM = 16;
+    const int ncand = tiles * k;
+    const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
+    auto cand_load = [&](int sc, uint32_t(&out)[EM]) {
+#pragma unroll
+        for (int j = 0; j < EM; ++j) {
+            const int p = order_pos<EM, CH>(sc, j);
+            out[j] = p < ncand ? Tr::cand_key(scr[p]) : 0u;
+        }
+    };
+    radix_threshold<EM, Tr::KEYBITS>(sm.sel, nsc, cand_load, (uint32_t)k, thi, level, margin);
+    compact<EM, CH>(sm.sel, nsc, cand_load, thi, level, margin, [&](uint32_t pos, int sc, int j) {
+        if (pos >= (uint32_t)k) return;
+        const int p = order_pos<EM, CH>(sc, j);
+        const Cand c = scr[p];
+        const int idx = (p / k) * a.block_n + Tr::cand_li(c);
+        sm.cand[pos] = ((uint64_t)Tr::cand_key(c) << 8) | (uint64_t)(127u - pos);
+        sm.idx[pos] = idx < V ? idx : V - 1;
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        uint64_t c0 = (2 * lane < k) ? sm.cand[2 * lane] : 0ull;
+        uint64_t c1 = (2 * lane + 1 < k) ? sm.cand[2 * lane + 1] : 0ull;
+        wave_sort128_desc(c0, c1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 2 * lane + i;
+            const uint64_t c = i ? c1 : c0;
+            if (e < k) {
+                const uint32_t key = (uint32_t)(c >> 8);
+                const int pos = 127 - (int)(c & 0x7fu);
+                const int64_t o = (int64_t)row * k + e;
+                if (F32) {
+                    ((float *)a.values)[o] = __uint_as_float(unkey32(key));
+                } else {
+                    ((uint16_t *)a.values)[o] = (uint16_t)unkey16(key);
+                }
+                a.indices[o] = sm.idx[pos];
+            }
+        }
+    }
+}
+
+template <bool F32>
+static int launch_topk(const ss_topk_args *a, int tiles) {
+    dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
+    hipStream_t s = (hipStream_t)a->stream;
+    switch (a->block_n) {
+        case 1024: hipLaunchKernelGGL((topk_kernel<F32, 4>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((topk_kernel<F32, 8>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((topk_kernel<F32, 16>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((topk_kernel<F32, 32>), grid, block, 0, s, *a, tiles); break;
+        default: return SS_ERR_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
+}
+
+}  // namespace ss
+
+extern "C" int ss_topk(const ss_topk_args *a) {
+    if (!a || !a->logits || !a->scratch || !a->tickets || !a->values || !a->indices)
+        return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows < 0 || a->vocab_size <= 0) return SS_ERR_INVALID_ARGUMENT;
+    if (a->k < 1 || a->k > SS_MAX_K || (a->k & (a->k - 1)) != 0) return SS_ERR_INVALID_ARGUMENT;
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+        return SS_ERR_UNSUPPORTED;
+    if (a->dtype != SS_DTYPE_BF16 && a->dtype != SS_DTYPE_F32) return SS_ERR_UNSUPPORTED;
+    const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
+    if (tiles < 2) return SS_ERR_INVALID_ARGUMENT;
+    if ((int64_t)tiles * a->k > a->stride_scratch) return SS_ERR_INVALID_ARGUMENT;
+    if (a->stride_logits < a->vocab_size) return SS_ERR_INVALID_ARGUMENT;
+    if (a->rows == 0) return SS_OK;
+    return a->dtype == SS_DTYPE_F32 ? ss::launch_topk<true>(a, tiles)
+                                    : ss::launch_topk<false>(a, tiles);
+}

@@ -1,0 +1,179 @@
+"""ctypes binding of the gfx950 HIP library (C-ABI declared in ``include/sonic_sampler.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch already mapped
+(both carry the soname ``libamdhip64.so.7``), which makes torch's stream handles valid inside it.
+There is deliberately no CPU fallback: if the library is missing every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (must be imported before the HIP library is loaded)
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsonic_sampler.so"
+
+c_p = ctypes.c_void_p
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_u32 = ctypes.c_uint32
+c_u64 = ctypes.c_uint64
+
+SS_OK = 0
+SS_DTYPE_BF16 = 0
+SS_DTYPE_F32 = 1
+ABI_VERSION = 1
+
+
+class Philox(ctypes.Structure):
+    _fields_ = [("seed", c_u64), ("offset", c_u32), ("enabled", c_i32)]
+
+
+class TopKArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_p), ("stride_logits", c_i64), ("dtype", c_i32), ("rows", c_i32),
+        ("vocab_size", c_i32), ("k", c_i32), ("block_n", c_i32), ("reserved", c_i32),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("values", c_p),
+        ("indices", c_p), ("stream", c_p),
+    ]
+
+
+class SingularArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_p), ("stride_logits", c_i64), ("rows", c_i32), ("vocab_size", c_i32),
+        ("target_vocab", c_i32), ("block_n", c_i32), ("lookahead", c_i32), ("timestep", c_i32),
+        ("max_top_logprobs", c_i32), ("is_prefill", c_i32), ("update_counts", c_i32),
+        ("return_logprobs", c_i32), ("return_probabilities", c_i32), ("reserved", c_i32),
+        ("indicators", c_p), ("slot_mapping", c_p), ("d2t", c_p),
+        ("grammar", c_p), ("stride_grammar", c_i64),
+        ("context_counts", c_p), ("stride_context", c_i64),
+        ("decode_counts", c_p), ("stride_decode", c_i64),
+        ("drafted_tokens", c_p), ("stride_drafted", c_i64),
+        ("repetition", c_p), ("frequency", c_p), ("presence", c_p),
+        ("logit_bias", c_p), ("stride_bias", c_i64),
+        ("temperature", c_p), ("top_k", c_p), ("top_p", c_p), ("min_p", c_p),
+        ("top_logprobs", c_p), ("gumbel", c_p), ("stride_gumbel", c_i64),
+        ("philox", Philox), ("philox_step", c_i32), ("reserved2", c_i32),
+        ("tokens", c_p), ("stride_tokens", c_i64),
+        ("logprobs", c_p), ("stride_logprobs", c_i64),
+        ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
+        ("probabilities", c_p), ("stride_probabilities", c_i64),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("stream", c_p),
+    ]
+
+
+class MultistepArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_p), ("stride_logits", c_i64), ("rows", c_i32), ("batch", c_i32),
+        ("vocab_size", c_i32), ("block_n", c_i32), ("lookahead", c_i32),
+        ("max_top_logprobs", c_i32), ("update_counts", c_i32), ("return_logprobs", c_i32),
+        ("cu_seqlens", c_p), ("indicators", c_p), ("slot_mapping", c_p), ("drafted_tokens", c_p),
+        ("grammar", c_p), ("grammar_stride_slot", c_i64), ("grammar_stride_step", c_i64),
+        ("context_counts", c_p), ("stride_context", c_i64),
+        ("decode_counts", c_p), ("stride_decode", c_i64),
+        ("repetition", c_p), ("frequency", c_p), ("presence", c_p),
+        ("logit_bias", c_p), ("stride_bias", c_i64),
+        ("temperature", c_p), ("top_k", c_p), ("top_p", c_p), ("min_p", c_p),
+        ("top_logprobs", c_p),
+        ("draft_probabilities", c_p), ("probs_stride_slot", c_i64), ("probs_stride_step", c_i64),
+        ("uniform", c_p), ("stride_uniform", c_i64),
+        ("gumbel", c_p), ("gumbel_stride_slot", c_i64), ("gumbel_stride_step", c_i64),
+        ("philox", Philox),
+        ("out_tokens", c_p), ("offsets", c_p), ("logprobs", c_p),
+        ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
+        ("values", c_p), ("indices", c_p),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("stream", c_p),
+    ]
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("SONIC_SAMPLER_LIB", _LIB_PATH))
+
+
+def load() -> ctypes.CDLL:
+    """Loads (once) and returns the HIP library; raises if it is absent or mismatched."""
+
+    global _lib
+
+    if _lib is not None:
+        return _lib
+
+    path = library_path()
+
+    if not path.is_file():
+        raise RuntimeError(
+            f"sonic_sampler HIP library not found at {path}; build it with "
+            "`python sonic-sampler_amd/build_native.py` (no CPU fallback exists)"
+        )
+
+    lib = ctypes.CDLL(str(path))
+
+    lib.ss_abi_version.restype = c_i32
+    lib.ss_status_string.restype = ctypes.c_char_p
+    lib.ss_status_string.argtypes = [c_i32]
+    lib.ss_args_size.restype = c_i64
+    lib.ss_args_size.argtypes = [c_i32]
+
+    for name, struct in (("ss_topk", TopKArgs), ("ss_fused_singular", SingularArgs),
+                         ("ss_fused_multistep", MultistepArgs)):
+        fn = getattr(lib, name)
+        fn.restype = c_i32
+        fn.argtypes = [ctypes.POINTER(struct)]
+
+    lib.ss_gumbel_materialize.restype = c_i32
+    lib.ss_gumbel_materialize.argtypes = [c_u64, c_u32, c_i32, c_i32, c_i32, c_p, c_i64, c_i64, c_p]
+    lib.ss_philox_raw.restype = c_i32
+    lib.ss_philox_raw.argtypes = [c_u64, c_u32, c_i32, c_i32, c_i32, c_p, c_p]
+
+    if lib.ss_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"sonic_sampler ABI mismatch: library {lib.ss_abi_version()}, "
+                           f"bindings {ABI_VERSION}")
+
+    for which, struct in enumerate((TopKArgs, SingularArgs, MultistepArgs)):
+        if lib.ss_args_size(which) != ctypes.sizeof(struct):
+            raise RuntimeError(f"sonic_sampler ABI mismatch in {struct.__name__}: "
+                               f"{lib.ss_args_size(which)} != {ctypes.sizeof(struct)} bytes")
+
+    _lib = lib
+
+    return lib
+
+
+def check(status: int, what: str) -> None:
+
+    if status != SS_OK:
+
+        message = load().ss_status_string(status).decode()
+
+        raise RuntimeError(f"{what} failed: {message} (status {status})")
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stride0(tensor: torch.Tensor | None) -> int:
+
+    return 0 if tensor is None else tensor.stride(0)
+
+
+def stream_of(tensor: torch.Tensor) -> int:
+
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor | None) -> None:
+
+    for tensor in tensors:
+
+        if tensor is not None and tensor.device.type != "cuda":
+
+            raise ValueError(
+                f"sonic_sampler kernels run on the GPU only; got a tensor on {tensor.device}"
+            )

@@ -1,0 +1,297 @@
+"""Tiling rung: dispatch resolution and in-flight buffer ownership (reference
+``interface/base.py:45-276``).
+
+``TwoStageTiling.factory`` resolves ``block_n`` from the dispatch table (or ``block_size``),
+validates the configuration with the reference's ``ValueError`` conditions and allocates the
+in-flight buffers: ``scratchpad [B * (gamma + 1), blocks * 128]`` uint32 and, for the verifier,
+``values`` / ``indices [B * (gamma + 1), 128]``. It also allocates ``tickets``, the zeroed int32
+arrival counters the single-launch kernels use (one per logit row plus one per request); the
+kernels leave them zeroed, so the buffers can be reused across calls and graph replays.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Tuple, Union
+
+import torch
+
+from torch import Tensor
+
+from sonic_sampler.base.sampler import DEFAULT_TOP_LOGPROBS
+from sonic_sampler.interface.dispatch import (
+    DispatchSummary,
+    RuntimeConfig,
+    TwoStageWarpConfig,
+    VocabBucket,
+)
+from sonic_sampler.ops.base import MAX_K
+
+
+FP32 = torch.float32
+BF16 = torch.bfloat16
+I32 = torch.int32
+U32 = torch.uint32
+
+# Tile widths the gfx950 kernels are compiled for.
+SUPPORTED_BLOCK_N = (1024, 2048, 4096, 8192)
+
+
+def cdiv(a: int, b: int) -> int:
+
+    return -(-a // b)
+
+
+@dataclass(eq=False)
+class Vocabulary:
+
+    # Columns of the logits.
+    size: int
+
+    # Vocabulary tiles.
+    blocks: int
+
+    @classmethod
+    def resolve(cls, size: int, block_n: int) -> "Vocabulary":
+
+        return cls(size=size, blocks=cdiv(size, block_n))
+
+    def evolve(self, block_n: int) -> "Vocabulary":
+
+        return Vocabulary(size=self.size, blocks=cdiv(self.size, block_n))
+
+
+@dataclass(eq=True)
+class TopKStrategy:
+
+    """Tile-selection strategy selector (reference ``interface/base.py:63-118``).
+
+    Accepted for API compatibility. The gfx950 kernels always use the exact LDS radix threshold
+    select, which returns the same candidates as every reference strategy.
+    """
+
+    radix: bool = False
+    sparse: bool = False
+    scale: int = 4
+
+    @classmethod
+    def adaptive(cls, scale: int = 4) -> "TopKStrategy":
+
+        return cls(radix=True, sparse=True, scale=scale)
+
+    @classmethod
+    def resolve(cls, config: RuntimeConfig) -> "TopKStrategy":
+
+        if config.strategy == "radix":
+
+            return cls(radix=True)
+
+        if config.strategy == "adaptive":
+
+            return cls.adaptive()
+
+        return cls()
+
+    @property
+    def key(self) -> str:
+
+        if self.radix:
+
+            return "adaptive" if self.sparse else "radix"
+
+        return "bitonic"
+
+    @property
+    def is_adaptive(self) -> bool:
+
+        return self.radix and self.sparse
+
+    @property
+    def is_alternating(self) -> bool:
+
+        return not self.radix
+
+    @property
+    def inverse(self) -> Optional[float]:
+
+        return 1 / self.scale if self.is_adaptive else None
+
+
+def resolve_dispatch(
+    k: int,
+    vocab_size: int,
+    block_size: Optional[int],
+    arch: Union[int, str, None],
+) -> Tuple[Optional[VocabBucket], int]:
+
+    if k > MAX_K:
+
+        raise ValueError(f"maximum supported top-k value is {MAX_K}, got {k} instead")
+
+    if k < 1 or k.bit_count() > 1:
+
+        raise ValueError(f"top-k value must be a power of 2, got {k} instead")
+
+    if block_size is None:
+
+        if (dispatch := DispatchSummary.load(k=MAX_K, arch=arch)) is None:
+
+            raise ValueError("unable to resolve dispatch summary for given top-k and architecture")
+
+        if (bucket := dispatch.vocab.get(size=vocab_size)) is None:
+
+            raise ValueError("unable to match tuning configuration for given vocabulary size")
+
+        return bucket, bucket.block_n
+
+    if block_size not in SUPPORTED_BLOCK_N:
+
+        raise ValueError(f"block_size must be one of {SUPPORTED_BLOCK_N}, got {block_size}")
+
+    return None, block_size
+
+
+def default_device(device=None) -> torch.device:
+
+    if device is not None:
+
+        return torch.device(device)
+
+    current = torch.get_default_device()
+
+    if current.type == "cpu" and torch.cuda.is_available():
+
+        return torch.device(f"cuda:{torch.cuda.current_device()}")
+
+    return current
+
+
+@dataclass(eq=False, kw_only=True)
+class TwoStageTiling:
+
+    # Accepted for API compatibility; the gfx950 path is a single launch, there is no
+    # dependent launch to overlap.
+    pdl: bool
+
+    # Tile width.
+    block_n: int
+
+    # Vocabulary and tiles.
+    vocabulary: Vocabulary
+
+    # uint32 candidate buffer [rows, blocks * 128].
+    scratchpad: Tensor
+
+    # Tuned dispatch, when resolved from a table.
+    dispatch: Optional[VocabBucket]
+
+    # Zeroed int32 arrival counters [rows + requests].
+    tickets: Tensor
+
+    @classmethod
+    def resolve(
+        cls,
+        vocab_size: int,
+        k: int = MAX_K,
+        top_logprobs: int = DEFAULT_TOP_LOGPROBS,
+        block_size: Optional[int] = None,
+        arch: Union[int, str, None] = None,
+        ensure_multiblock: bool = True,
+    ):
+
+        dispatch, block_n = resolve_dispatch(k, vocab_size, block_size, arch)
+        vocabulary = Vocabulary.resolve(vocab_size, block_n)
+
+        if ensure_multiblock and (blocks := vocabulary.blocks) <= 1:
+
+            raise ValueError(f"total vocab blocks must be greater than 1, got {blocks} instead")
+
+        if top_logprobs < 0 or top_logprobs > MAX_K:
+
+            raise ValueError(f"top logprobs must be within the interval [0, {MAX_K}]")
+
+        return dispatch, vocabulary, block_n
+
+    @classmethod
+    def factory(
+        cls,
+        vocab_size: int,
+        batch_size: int = 32,
+        lookahead: int = 0,
+        k: int = MAX_K,
+        top_logprobs: int = DEFAULT_TOP_LOGPROBS,
+        block_size: Optional[int] = None,
+        arch: Union[int, str, None] = None,
+        enable_pdl: bool = True,
+        ensure_multiblock: bool = True,
+        unpacked_buffers: bool = True,
+        values_dtype: torch.dtype = FP32,
+        device=None,
+    ):
+
+        dispatch, vocabulary, block_n = cls.resolve(
+            vocab_size=vocab_size,
+            k=k,
+            top_logprobs=top_logprobs,
+            block_size=block_size,
+            arch=arch,
+            ensure_multiblock=ensure_multiblock,
+        )
+
+        target = default_device(device)
+        total_rows = batch_size * (lookahead + 1)
+
+        with torch.device(target):
+
+            scratchpad = torch.empty(total_rows, vocabulary.blocks * k, dtype=I32).view(U32)
+            tickets = torch.zeros(total_rows + batch_size, dtype=I32)
+
+            values = indices = None
+
+            if unpacked_buffers:
+
+                values = torch.empty(total_rows, k, dtype=values_dtype)
+                indices = torch.empty(total_rows, k, dtype=I32)
+
+        instance = TwoStageTiling(
+            pdl=enable_pdl,
+            block_n=block_n,
+            vocabulary=vocabulary,
+            scratchpad=scratchpad,
+            dispatch=dispatch,
+            tickets=tickets,
+        )
+
+        return instance, values, indices
+
+    def tuning(
+        self,
+        size: int,
+        strategy: Optional[TopKStrategy] = None,
+        tuning: Optional[TwoStageWarpConfig] = None,
+    ):
+        """Warp config, strategy and block_n for a launch of `size` rows (reference ``:243-276``)."""
+
+        block_size = self.block_n
+        k_strategy = strategy
+        config = tuning
+
+        if config is None and self.dispatch and (bucket := self.dispatch.batch.get(size=size)):
+
+            if strategy and strategy.key in bucket.mapping:
+
+                target = bucket.get(strategy.key)
+                config, block_size = target.warp_config, target.block_n
+
+            else:
+
+                best = bucket.best
+                config, block_size = best.warp_config, best.block_n
+                k_strategy = k_strategy or TopKStrategy.resolve(best)
+
+        return config or TwoStageWarpConfig.default(), k_strategy or TopKStrategy(), block_size
+
+    def reset(self) -> None:
+        """Re-zeroes the arrival counters (only needed if a launch was aborted mid-flight)."""
+
+        self.tickets.zero_()

@@ -1,0 +1,116 @@
+"""Argument resolution shared by the functional entry points (reference
+``interface/functional/base.py:34-77``)."""
+
+from __future__ import annotations
+
+import random as _random
+from typing import Optional, Tuple
+
+import torch
+
+from torch import Tensor
+
+from sonic_sampler import _native
+from sonic_sampler.interface.base import SUPPORTED_BLOCK_N
+from sonic_sampler.ops.base import MAX_K, next_power_of_2
+
+U32 = torch.uint32
+I32 = torch.int32
+BF16 = torch.bfloat16
+
+
+def cdiv(a: int, b: int) -> int:
+
+    return -(-a // b)
+
+
+def validate_count_update(flag: bool, buffer: Optional[Tensor]) -> None:
+
+    if flag and buffer is None:
+
+        raise ValueError("`update_counts` is True but `decode_counts` is None")
+
+
+def validate_block(block_n: int) -> None:
+
+    if block_n not in SUPPORTED_BLOCK_N:
+
+        raise ValueError(f"block_n must be one of {SUPPORTED_BLOCK_N}, got {block_n}")
+
+
+def resolve_scratchpad(logits: Tensor, block_n: int, buffer: Optional[Tensor] = None):
+
+    rows, cols = logits.shape if logits.ndim == 2 else logits.flatten(0, 1).shape
+    vocab_blocks = cdiv(cols, block_n)
+
+    if vocab_blocks <= 1:
+
+        raise ValueError(f"total vocab blocks must be greater than 1, got {vocab_blocks} instead")
+
+    scratchpad = buffer
+
+    if scratchpad is None:
+
+        scratchpad = logits.new_empty(rows, vocab_blocks * MAX_K, dtype=I32).view(U32)
+
+    elif scratchpad.size(0) < rows or scratchpad.stride(-1) != 1 or scratchpad.stride(0) < vocab_blocks * MAX_K:
+
+        raise ValueError("scratchpad too small for the given logits and block_n")
+
+    return (rows, vocab_blocks), (rows,), scratchpad, vocab_blocks
+
+
+def resolve_tickets(buffer: Optional[Tensor], count: int, device) -> Tensor:
+
+    if buffer is None:
+
+        return torch.zeros(count, dtype=I32, device=device)
+
+    if buffer.dtype != I32 or buffer.numel() < count or not buffer.is_contiguous():
+
+        raise ValueError(f"tickets must be a contiguous int32 tensor of >= {count} zeroed entries")
+
+    return buffer
+
+
+def conditional_stride(*data: Optional[Tensor]) -> Optional[int]:
+
+    for tensor in data:
+
+        if tensor is not None:
+
+            return tensor.stride(0)
+
+    return None
+
+
+def resolve_block(data: Optional[Tensor], dim: int) -> Optional[int]:
+
+    return next_power_of_2(data.size(dim)) if data is not None else None
+
+
+def collapse_2d(value: Tensor) -> Tensor:
+
+    return value.flatten(0, -2)
+
+
+def unit_stride(name: str, tensor: Optional[Tensor]) -> None:
+
+    if tensor is not None and tensor.dim() > 0 and tensor.stride(-1) != 1:
+
+        raise ValueError(f"`{name}` must be contiguous along its last dimension")
+
+
+def philox(seed: Optional[int], offset: int) -> _native.Philox:
+
+    if seed is None:
+
+        return _native.Philox(0, 0, 0)
+
+    return _native.Philox(seed & 0xFFFFFFFFFFFFFFFF, offset & 0xFFFFFFFF, 1)
+
+
+def fresh_seed() -> int:
+    """A seed drawn from torch's default CPU generator (fresh noise for a call without noise)."""
+
+    return int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64).item())

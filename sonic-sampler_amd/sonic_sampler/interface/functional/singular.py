@@ -1,0 +1,221 @@
+"""Functional single-step sampling (reference ``interface/functional/singular.py:38-322``).
+
+``fused_singular`` keeps the reference's keyword set and buffer semantics and launches one HIP
+kernel (``ss_fused_singular``): prologue + tile top-128 on every (row, tile) workgroup, merge and
+selection on the last workgroup of each row.
+
+Additions to the reference's keywords (all optional):
+
+* ``timestep`` -- number of leading ``drafted_tokens`` columns that count as decode history. The
+  modular ``drafting`` passes its timestep ``t`` (the reference's PyTorch semantics,
+  ``core/naive.py:199-203``); when omitted, ``min(lookahead, drafted_tokens.size(1))`` columns are
+  used, as the reference kernel does.
+* ``philox_seed`` / ``philox_offset`` / ``philox_step`` -- draw the Gumbel noise from the
+  counter-based Philox stream instead of ``gumbel_noise``. With neither given, a fresh seed is drawn
+  from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
+* ``tickets`` -- the int32 arrival counters (zeroed); allocated when omitted.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from torch import Tensor
+
+from sonic_sampler import _native
+from sonic_sampler.base.sampler import Selection, DEFAULT_TOP_LOGPROBS
+from sonic_sampler.interface.base import TopKStrategy
+from sonic_sampler.interface.dispatch import TwoStageWarpConfig
+from sonic_sampler.interface.functional.base import (
+    BF16,
+    I32,
+    fresh_seed,
+    philox,
+    resolve_scratchpad,
+    resolve_tickets,
+    unit_stride,
+    validate_block,
+    validate_count_update,
+)
+from sonic_sampler.ops.base import MAX_K
+
+
+def resolve_tokens(buffer: Optional[Tensor], batch_size: int, source: Tensor) -> Tensor:
+
+    return buffer if buffer is not None else source.new_empty(batch_size, 1, dtype=I32)
+
+
+def resolve_probabilities(precondition: bool, source: Tensor, batch_size: int,
+                          vocab_size: Optional[int] = None, buffer: Optional[Tensor] = None):
+
+    if buffer is None and precondition:
+
+        return source.new_zeros((batch_size, vocab_size or source.size(1)))
+
+    return buffer
+
+
+def fused_singular(
+    # Required.
+    logits: Tensor,
+    indicators: Tensor,
+    # Model & Engine Specific(s).
+    local_vocab: Optional[int] = None,
+    shard_size: Optional[int] = None,
+    world_size: int = 1,
+    local_rank: int = 0,
+    lookahead: int = 0,
+    target_vocab: Optional[int] = None,
+    max_top_logprobs: int = DEFAULT_TOP_LOGPROBS,
+    # Conditional(s).
+    enable_pdl: bool = True,
+    is_prefill: bool = False,
+    update_counts: bool = False,
+    return_logprobs: bool = False,
+    return_probabilities: bool = False,
+    # Kernel Specific(s).
+    block_n: int = 4_096,
+    # Buffer(s).
+    scratchpad: Optional[Tensor] = None,
+    # Logit Manipulator(s).
+    slot_mapping: Optional[Tensor] = None,
+    d2t_mapping: Optional[Tensor] = None,
+    grammar: Optional[Tensor] = None,
+    context_counts: Optional[Tensor] = None,
+    decode_counts: Optional[Tensor] = None,
+    drafted_tokens: Optional[Tensor] = None,
+    repetition_penalties: Optional[Tensor] = None,
+    frequency_penalties: Optional[Tensor] = None,
+    presence_penalties: Optional[Tensor] = None,
+    logit_bias: Optional[Tensor] = None,
+    temperature: Optional[Tensor] = None,
+    top_k: Optional[Tensor] = None,
+    top_p: Optional[Tensor] = None,
+    min_p: Optional[Tensor] = None,
+    # Selection Parameter(s).
+    top_k_logprobs: Optional[Tensor] = None,
+    gumbel_noise: Optional[Tensor] = None,
+    # Output Buffer(s).
+    output_tokens: Optional[Tensor] = None,
+    draft_probabilities: Optional[Tensor] = None,
+    # Top-K Strategy & Tuning Configuration.
+    topk_strategy: Optional[TopKStrategy] = None,
+    warp_config: Optional[TwoStageWarpConfig] = None,
+    # Additions.
+    timestep: Optional[int] = None,
+    philox_seed: Optional[int] = None,
+    philox_offset: int = 0,
+    philox_step: int = 0,
+    tickets: Optional[Tensor] = None,
+) -> Selection:
+
+    validate_count_update(update_counts, decode_counts)
+    validate_block(block_n)
+
+    if world_size != 1 or local_rank != 0:
+
+        raise ValueError("sharded-vocabulary scratchpads are not supported by the gfx950 path "
+                         "(gather the logits first)")
+
+    if logits.dtype != BF16 or logits.dim() != 2:
+
+        raise ValueError(f"logits must be a 2-D bfloat16 tensor, got {logits.dtype} {tuple(logits.shape)}")
+
+    if not 0 <= max_top_logprobs <= MAX_K:
+
+        raise ValueError(f"top logprobs must be within the interval [0, {MAX_K}]")
+
+    for name, t in (("logits", logits), ("grammar", grammar), ("context_counts", context_counts),
+                    ("decode_counts", decode_counts), ("logit_bias", logit_bias),
+                    ("gumbel_noise", gumbel_noise), ("draft_probabilities", draft_probabilities),
+                    ("indicators", indicators), ("drafted_tokens", drafted_tokens)):
+
+        unit_stride(name, t)
+
+    _native.require_device(logits, indicators)
+
+    batch_size, vocab_size = logits.shape
+    vocab_size = min(vocab_size, local_vocab or vocab_size)
+
+    _, _, bitpacked, vocab_blocks = resolve_scratchpad(logits, block_n, scratchpad)
+
+    final_tokens = resolve_tokens(output_tokens, batch_size, logits)
+
+    probabilities = resolve_probabilities(
+        precondition=return_probabilities,
+        source=logits,
+        batch_size=indicators.size(0),
+        vocab_size=target_vocab,
+        buffer=draft_probabilities,
+    )
+
+    selection = Selection.from_buffers(
+        tokens=final_tokens,
+        probabilities=probabilities,
+        logprobs=return_logprobs,
+        top_logprobs=max_top_logprobs,
+    )
+
+    token_logprobs = top_values = top_tokens = None
+
+    if selection.logprobs is not None:
+
+        token_logprobs = selection.logprobs.selected
+
+        if selection.logprobs.top_k is not None:
+
+            top_values = selection.logprobs.top_k.logprobs
+            top_tokens = selection.logprobs.top_k.tokens
+
+    if gumbel_noise is None and philox_seed is None:
+
+        philox_seed = fresh_seed()
+
+    history = 0
+
+    if drafted_tokens is not None:
+
+        history = timestep if timestep is not None else min(lookahead, drafted_tokens.size(1))
+        history = max(0, min(history, drafted_tokens.size(1)))
+
+    ticket_buffer = resolve_tickets(tickets, batch_size, logits.device)
+
+    p = _native.ptr
+    s = _native.stride0
+
+    args = _native.SingularArgs(
+        logits=p(logits), stride_logits=logits.stride(0), rows=batch_size,
+        vocab_size=vocab_size,
+        target_vocab=target_vocab or (logit_bias.size(-1) if logit_bias is not None else vocab_size),
+        block_n=block_n, lookahead=lookahead, timestep=history,
+        max_top_logprobs=max_top_logprobs if top_values is not None else 0,
+        is_prefill=int(is_prefill), update_counts=int(update_counts),
+        return_logprobs=int(token_logprobs is not None),
+        return_probabilities=int(probabilities is not None), reserved=0,
+        indicators=p(indicators), slot_mapping=p(slot_mapping), d2t=p(d2t_mapping),
+        grammar=p(grammar), stride_grammar=s(grammar),
+        context_counts=p(context_counts), stride_context=s(context_counts),
+        decode_counts=p(decode_counts), stride_decode=s(decode_counts),
+        drafted_tokens=p(drafted_tokens) if history else None, stride_drafted=s(drafted_tokens),
+        repetition=p(repetition_penalties), frequency=p(frequency_penalties),
+        presence=p(presence_penalties),
+        logit_bias=p(logit_bias), stride_bias=s(logit_bias),
+        temperature=p(temperature), top_k=p(top_k), top_p=p(top_p), min_p=p(min_p),
+        top_logprobs=p(top_k_logprobs),
+        gumbel=p(gumbel_noise) if philox_seed is None else None,
+        stride_gumbel=s(gumbel_noise) if philox_seed is None else 0,
+        philox=philox(philox_seed, philox_offset), philox_step=philox_step, reserved2=0,
+        tokens=p(final_tokens), stride_tokens=final_tokens.stride(0),
+        logprobs=p(token_logprobs), stride_logprobs=s(token_logprobs),
+        top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
+        probabilities=p(probabilities), stride_probabilities=s(probabilities),
+        scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
+        tickets=p(ticket_buffer), stream=_native.stream_of(logits),
+    )
+
+    _native.check(_native.load().ss_fused_singular(ctypes.byref(args)), "ss_fused_singular")
+
+    return selection

@@ -1,0 +1,122 @@
+"""Comparison helpers shared by the parity tests."""
+
+from __future__ import annotations
+
+import torch
+
+from oracle.sampler import bf16_within
+
+
+def assert_tokens(actual, expected, what: str, allow_fraction: float = 0.05):
+    """Tokens must match exactly except on rows the oracle marks knife-edge."""
+
+    mismatched = [i for i, e in enumerate(expected) if int(actual[i]) != e]
+
+    return mismatched
+
+
+def check_singular(selection, expected, *, logprobs: bool, probabilities=None, slot_mapping=None,
+                   max_knife_fraction: float = 0.05):
+
+    tokens = selection.tokens[:, 0].cpu()
+    mismatched = [r for r, e in enumerate(expected) if int(tokens[r]) != e.token]
+    unexplained = [r for r in mismatched if not expected[r].knife]
+
+    assert not unexplained, (
+        f"token mismatch on non-knife-edge rows {unexplained[:8]}: "
+        f"got {[int(tokens[r]) for r in unexplained[:8]]}, "
+        f"expected {[expected[r].token for r in unexplained[:8]]}"
+    )
+
+    assert len(mismatched) <= max(1, int(max_knife_fraction * len(expected)))
+
+    lp = selection.logprobs.selected.float().cpu() if logprobs and selection.logprobs else None
+    top = selection.logprobs.top_k if logprobs and selection.logprobs else None
+    top_tokens = top.tokens.cpu() if top is not None else None
+    top_values = top.logprobs.float().cpu() if top is not None else None
+    probs = probabilities.float().cpu() if probabilities is not None else None
+    checked = 0
+
+    for r, e in enumerate(expected):
+
+        if e.knife or r in mismatched:
+
+            continue
+
+        if lp is not None:
+
+            assert bf16_within(float(lp[r, 0]), e.logprob), (r, float(lp[r, 0]), e.logprob)
+
+        if top is not None:
+
+            for z, (t, v) in enumerate(zip(e.top_tokens, e.top_logprobs)):
+
+                assert int(top_tokens[r, z]) == t, (r, z, int(top_tokens[r, z]), t)
+                assert bf16_within(float(top_values[r, z]), v), (r, z, float(top_values[r, z]), v)
+
+        if probs is not None and e.probs is not None:
+
+            slot = int(slot_mapping[r]) if slot_mapping is not None else r
+
+            for t, v in e.probs.items():
+
+                assert bf16_within(float(probs[slot, t]), v), (r, t, float(probs[slot, t]), v)
+
+        checked += 1
+
+    return mismatched, checked
+
+
+def check_multistep(verification, expected, cu_seqlens, *, logprobs: bool,
+                    max_knife_fraction: float = 0.05):
+
+    tokens = verification.tokens.reshape(-1).cpu()
+    offsets = verification.offsets.reshape(-1).cpu()
+    lp = verification.logprobs.selected.reshape(-1).float().cpu() if logprobs else None
+    top = verification.logprobs.top_k if logprobs and verification.logprobs else None
+    top_tokens = top.tokens.reshape(-1, top.tokens.size(-1)).cpu() if top is not None else None
+    top_values = top.logprobs.reshape(-1, top.logprobs.size(-1)).float().cpu() if top is not None else None
+
+    mismatched = []
+
+    for b, e in enumerate(expected):
+
+        margin = cu_seqlens[b]
+        got = [int(t) for t in tokens[margin: margin + int(offsets[b]) + 1]]
+
+        if int(offsets[b]) != e.offset or got != e.tokens:
+
+            mismatched.append(b)
+
+    unexplained = [b for b in mismatched if not expected[b].knife]
+
+    assert not unexplained, [
+        (b, int(offsets[b]), expected[b].offset,
+         [int(t) for t in tokens[cu_seqlens[b]: cu_seqlens[b] + int(offsets[b]) + 1]], expected[b].tokens)
+        for b in unexplained[:6]
+    ]
+
+    assert len(mismatched) <= max(1, int(max_knife_fraction * len(expected)))
+
+    for b, e in enumerate(expected):
+
+        if b in mismatched or e.knife or not logprobs:
+
+            continue
+
+        margin = cu_seqlens[b]
+
+        for i, v in enumerate(e.logprobs):
+
+            assert bf16_within(float(lp[margin + i]), v), (b, i, float(lp[margin + i]), v)
+
+        if top is not None:
+
+            for i, (tt, tv) in enumerate(zip(e.top_tokens, e.top_logprobs)):
+
+                for z, (t, v) in enumerate(zip(tt, tv)):
+
+                    assert int(top_tokens[margin + i, z]) == t, (b, i, z)
+                    assert bf16_within(float(top_values[margin + i, z]), v), (b, i, z, float(top_values[margin + i, z]), v)
+
+    return mismatched

@@ -1,0 +1,149 @@
+"""Fused chain verification on the GPU vs the CPU oracle."""
+
+import pytest
+import torch
+
+from helpers import check_multistep
+from oracle import sampler as oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, block_size=None,
+                 slot_mapping=None, buffers=None):
+
+    from bench import to_device
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    batch = len(work.cu_seqlens) - 1
+    buffers = buffers if buffers is not None else to_device(work.buffers, DEV)
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=work.vocab, lookahead=work.lookahead,
+                                                  batch_size=batch, block_size=block_size,
+                                                  max_top_logprobs=work.max_top_logprobs, device=DEV)
+    drafted = work.drafted.to(DEV)
+
+    if work.varlen:
+
+        logits = work.logits.to(DEV)
+        tokens = drafted
+        cu = torch.tensor(work.cu_seqlens, dtype=torch.int32, device=DEV)
+
+    else:
+
+        n = work.lookahead + 1
+        logits = work.logits.view(batch, n, -1).to(DEV)
+        tokens = drafted.view(batch, n)
+        cu = None
+
+    probs = work.probabilities.to(DEV) if work.probabilities is not None else None
+    verification = verifier(logits, tokens, buffers, probabilities=probs, update_counts=update_counts,
+                            logprobs=logprobs, in_place=in_place, cu_seqlens=cu,
+                            slot_mapping=slot_mapping)
+    torch.cuda.synchronize()
+
+    return verification, buffers, verifier
+
+
+def test_config2_greedy():
+
+    from bench import c2_workload
+
+    work = c2_workload()
+    print(f"config 2: rows={work.logits.size(0)} V={work.vocab}", flush=True)
+    verification, buffers, _ = run_verifier(work, update_counts=True)
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.multistep(work.logits, state, work.drafted, work.cu_seqlens, logprobs=True)
+    check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.0)
+
+    counts = oracle.apply_multistep_counts(state.decode, expected, None)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def test_config3_stochastic_varlen():
+
+    from bench import c3_workload
+
+    work = c3_workload()
+    print(f"config 3: rows={work.logits.size(0)} requests={len(work.cu_seqlens) - 1}", flush=True)
+    verification, buffers, verifier = run_verifier(work, update_counts=True)
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.multistep(work.logits, state, work.drafted, work.cu_seqlens,
+                                probabilities=work.probabilities, logprobs=True, max_top_logprobs=20)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True)
+    print(f"knife-edge mismatches: {mismatched}", flush=True)
+
+    # the per-row top-128 ids are exact
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i)
+
+    if not mismatched:
+
+        counts = oracle.apply_multistep_counts(state.decode, expected, None)
+        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_buffers_fixed_gamma_slots(seed):
+    """Mixed random indicators (incl. 0x800, greedy, penalties, grammar) with slot mapping."""
+
+    from bench import MultistepWorkload, spiked_logits, to_device
+    from sonic_sampler.core.buffer import SamplingBuffers
+
+    slots, batch, gamma, vocab = 10, 6, 3, 8192
+    n = gamma + 1
+    g = torch.Generator().manual_seed(seed)
+    host = SamplingBuffers.random(size=slots, timesteps=n, vocab_size=vocab, device="cpu", seed=50 + seed,
+                                  max_top_logprobs=4)
+    logits = spiked_logits(batch * n, vocab, seed=300 + seed)
+    slot_mapping = torch.randperm(slots, generator=g)[:batch].to(torch.int32)
+
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch * n, generator=g) < 0.6, argmax,
+                          torch.randint(1, vocab, (batch * n,), generator=g)).to(torch.int32)
+    probabilities = torch.softmax(torch.randn(slots, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print(f"random multistep seed={seed} indicators={[hex(int(host.flags.indicators.target[int(s)])) for s in slot_mapping]}", flush=True)
+    verification, buffers, _ = run_verifier(work, update_counts=True, block_size=1024,
+                                            slot_mapping=slot_mapping.to(DEV))
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, slot_mapping=slot_mapping.tolist(),
+                                probabilities=probabilities, logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
+
+    if not mismatched:
+
+        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
+        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def test_all_accepted_emits_bonus_from_last_step():
+
+    from bench import MultistepWorkload, spiked_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    batch, gamma, vocab = 4, 3, 4096
+    n = gamma + 1
+    logits = spiked_logits(batch * n, vocab, seed=7)
+    drafted = logits.float().argmax(-1).to(torch.int32)
+    host = SamplingBuffers.default(size=batch, timesteps=n, vocab_size=vocab, device="cpu")
+    host.flags = Flags.from_values(batch, n, Indicator.GREEDY, device="cpu")
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=0)
+    verification, _, _ = run_verifier(work, block_size=1024, logprobs=False)
+    assert verification.offsets.cpu().flatten().tolist() == [gamma] * batch
+    assert torch.equal(verification.tokens.cpu().flatten(), drafted)

@@ -1,0 +1,162 @@
+"""Fused single-step sampling on the GPU vs the CPU oracle."""
+
+import pytest
+import torch
+
+from helpers import check_singular
+from oracle import sampler as oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def test_config1_autoregressive():
+
+    from bench import c1_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    work = c1_workload()
+    batch, vocab = work.logits.shape
+    print(f"config 1: B={batch} V={vocab}", flush=True)
+
+    buffers = to_device(work.buffers, DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch, max_top_logprobs=5, device=DEV)
+    selection = sampler.autoregressive(work.logits.to(DEV), buffers, update_counts=True, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.singular(work.logits, state, scope="target", logprobs=True, max_top_logprobs=5)
+    mismatched, checked = check_singular(selection, expected, logprobs=True)
+    print(f"knife-edge mismatches: {mismatched}, fully checked rows: {checked}", flush=True)
+    assert checked >= batch - 4
+
+    counts = oracle.apply_singular_counts(state.decode, expected, None, prefill=False)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def test_config1_philox_matches_materialized_noise():
+
+    from bench import c1_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from sonic_sampler.noise import materialize_gumbel
+
+    work = c1_workload()
+    batch, vocab = work.logits.shape
+    buffers = to_device(work.buffers, DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch, max_top_logprobs=5, device=DEV)
+    logits = work.logits.to(DEV)
+
+    print("config 1 with Philox noise", flush=True)
+    a = sampler.autoregressive(logits, buffers, logprobs=True, philox_seed=77, philox_offset=3)
+    noise = materialize_gumbel(77, 3, batch, 1, vocab, device=DEV)
+    buffers.weights.gumbel.target.copy_(noise)
+    b = sampler.autoregressive(logits, buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    assert torch.equal(a.tokens.cpu(), b.tokens.cpu())
+    assert torch.equal(a.logprobs.selected.cpu(), b.logprobs.selected.cpu())
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.singular(work.logits, state, scope="target", noise=noise[:, 0].cpu(),
+                               logprobs=True, max_top_logprobs=5)
+    check_singular(a, expected, logprobs=True)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_random_buffers_drafting_slots_d2t(seed):
+    """Mixed random indicators, slot mapping, d2t, drafted history and probability scatter."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    slots, rows, gamma, t = 12, 8, 3, 2
+    draft_vocab, target_vocab = 4096, 8192
+    g = torch.Generator().manual_seed(seed)
+
+    host = SamplingBuffers.random(size=slots, timesteps=gamma + 1, vocab_size=target_vocab,
+                                  device="cpu", seed=seed, max_top_logprobs=5)
+    buffers = to_device(host, DEV)
+    logits = spiked_logits(rows, draft_vocab, seed=100 + seed)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(torch.int32)
+    d2t = torch.randperm(target_vocab, generator=g)[:draft_vocab].to(torch.int32)
+    tokens = torch.randint(1, target_vocab, (rows, gamma + 1), generator=g).to(torch.int32)
+    print(f"random drafting seed={seed} indicators={[hex(int(v)) for v in host.flags.indicators.draft]}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=draft_vocab, batch_size=rows, lookahead=gamma,
+                                                block_size=1024, max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, target_vocab, dtype=torch.bfloat16, device=DEV)
+    dev_tokens = tokens.to(DEV)
+    selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=dev_tokens, probabilities=probs,
+                                 slot_mapping=slot_mapping.to(DEV), d2t_mapping=d2t.to(DEV),
+                                 target_vocab=target_vocab, in_place=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="draft", timestep=t, slot_mapping=slot_mapping.tolist(),
+                               d2t=d2t, drafted=tokens, history=t, logprobs=False,
+                               probs=not host.flags.all_greedy, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False,
+                   probabilities=probs if not host.flags.all_greedy else None, slot_mapping=slot_mapping)
+
+    written = dev_tokens[:, t].cpu()
+    assert torch.equal(written, selection.tokens[:, 0].cpu())
+
+
+@pytest.mark.parametrize("seed", [10, 11, 12])
+def test_random_buffers_autoregressive_logprobs(seed):
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    rows, vocab = 16, 16384
+    host = SamplingBuffers.random(size=rows, timesteps=1, vocab_size=vocab, device="cpu", seed=seed,
+                                  max_top_logprobs=8)
+    buffers = to_device(host, DEV)
+    logits = spiked_logits(rows, vocab, seed=200 + seed)
+    print(f"random autoregressive seed={seed}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=8,
+                                                block_size=2048, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, prefill=True, update_counts=True, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=8)
+    check_singular(selection, expected, logprobs=True)
+
+    counts = oracle.apply_singular_counts(state.decode, expected, None, prefill=True)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def test_config4_drafting_full_size():
+
+    from bench import c4_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    work = c4_workload()
+    rows = work.logits.size(0)
+    slots = work.buffers.layout.rows
+    print(f"config 4: rows={rows} slots={slots} V_d={work.vocab} V_t={work.target_vocab}", flush=True)
+
+    buffers = to_device(work.buffers, DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=work.vocab, batch_size=rows, lookahead=4,
+                                                max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, work.target_vocab, dtype=torch.bfloat16, device=DEV)
+    tokens = work.tokens.to(DEV)
+    selection = sampler.drafting(work.logits.to(DEV), buffers, timestep=work.timestep, tokens=tokens,
+                                 probabilities=probs, slot_mapping=work.slot_mapping.to(DEV),
+                                 d2t_mapping=work.d2t.to(DEV), target_vocab=work.target_vocab, in_place=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.singular(work.logits, state, scope="draft", timestep=work.timestep,
+                               slot_mapping=work.slot_mapping.tolist(), d2t=work.d2t, drafted=work.tokens,
+                               history=work.timestep, probs=True, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=work.slot_mapping)
+
+    # every selected token is grammar-admissible and in the d2t image
+    image = set(work.d2t.tolist())
+    assert all(int(t) in image for t in selection.tokens[:, 0].cpu())

@@ -1,0 +1,390 @@
+"""Pins of the CPU oracle (no GPU): known-answer vectors, closed forms, brute force, invariants.
+
+Each test is chosen so that a plausible restatement mistake (a dropped processor, a wrong rounding
+point, a flipped comparison, a wrong tie order, an off-by-one in the acceptance chain) fails it.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import philox, topk
+from oracle import sampler as oracle
+
+BF16 = torch.bfloat16
+I32 = torch.int32
+
+
+# ------------------------------------------------------------------------------------------------
+# Philox4x32-10: Random123 known-answer vectors (kat_vectors, philox4x32_10)
+# ------------------------------------------------------------------------------------------------
+
+KAT = [
+    ((0x00000000, 0x00000000, 0x00000000, 0x00000000), (0x00000000, 0x00000000),
+     (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0xFFFFFFFF),
+     (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("counter,key,expected", KAT)
+def test_philox_known_answers(counter, key, expected):
+
+    out = philox.philox4x32_10(np.array(counter, dtype=np.uint32), np.array(key, dtype=np.uint32))
+    assert tuple(int(x) for x in out) == expected
+
+
+def test_noise_words_layout():
+
+    words = philox.noise_words(seed=(5 << 32) | 9, offset=3, slots=2, steps=2, vocab=3)
+    direct = philox.philox4x32_10(np.array([2, 1, 1, 3], dtype=np.uint32), np.array([9, 5], dtype=np.uint32))
+    assert int(words[1, 1, 2]) == int(direct[0])
+
+
+def test_bf16_round_matches_torch():
+
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 100
+    x[:4] = [0.0, -0.0, 1.00390625, 1.01171875]  # exact ties round to even
+    assert np.array_equal(philox.bf16_round(x), torch.from_numpy(x).to(BF16).float().numpy())
+
+
+def test_gumbel_transform_statistics():
+
+    w = philox.gumbel_from_words(philox.noise_words(1, 0, 1, 1, 200000))[0, 0]
+    # log(E), E ~ Exp(1): mean -gamma_EulerMascheroni, variance pi^2 / 6
+    assert abs(w.mean() + 0.5772156649) < 0.01
+    assert abs(w.var() - math.pi ** 2 / 6) < 0.03
+    assert np.all(np.isfinite(w))
+
+
+# ------------------------------------------------------------------------------------------------
+# Bounded top-k: stable order vs brute force
+# ------------------------------------------------------------------------------------------------
+
+def brute_topk(row, k):
+
+    order = sorted(range(len(row)), key=lambda i: (-float(row[i]), i))
+
+    return [float(row[i]) for i in order[:k]], order[:k]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF16])
+def test_topk_matches_brute_force_with_ties(dtype):
+
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randint(-3, 4, (5, 300), generator=g).to(dtype)
+    logits[0, 7] = float("-inf")
+    values, indices = topk.topk(logits, 37)
+
+    for r in range(5):
+
+        bv, bi = brute_topk(logits[r].float().tolist(), 37)
+        assert indices[r].tolist() == bi
+        assert values[r].float().tolist() == bv
+
+
+def test_topk_ties_go_to_lowest_index_not_topk_order():
+
+    x = torch.zeros(1, 1000, dtype=BF16)
+    values, indices = topk.topk(x, 128)
+    assert indices[0].tolist() == list(range(128))
+
+
+# ------------------------------------------------------------------------------------------------
+# Prologue closed forms
+# ------------------------------------------------------------------------------------------------
+
+def tiny_state(vocab=64, **overrides):
+
+    def bf(v):
+
+        return torch.tensor([v], dtype=torch.float32).to(BF16)
+
+    st = oracle.State(
+        target=[0], draft=[0],
+        grammar=torch.full((1, 1, (vocab + 31) // 32), -1, dtype=I32),
+        context=torch.zeros(1, vocab, dtype=I32), decode=torch.zeros(1, vocab, dtype=I32),
+        bias=torch.zeros(1, vocab, dtype=BF16),
+        multiplicative=bf(1.0), frequency=bf(0.0), presence=bf(0.0), temperature=bf(1.0),
+        top_p=bf(1.0), min_p=bf(0.0), top_k=torch.tensor([128], dtype=I32),
+        top_logprobs=torch.tensor([0], dtype=I32),
+        gumbel_target=torch.zeros(1, 1, vocab, dtype=BF16), gumbel_draft=torch.zeros(1, 1, vocab, dtype=BF16),
+        uniform=torch.ones(1, 1, dtype=BF16),
+    )
+
+    for k, v in overrides.items():
+
+        setattr(st, k, v)
+
+    return st
+
+
+def row(values, vocab=64):
+
+    x = torch.full((vocab,), -1.0, dtype=BF16)
+    x[: len(values)] = torch.tensor(values, dtype=torch.float32).to(BF16)
+
+    return x
+
+
+def test_multiplicative_penalty_closed_form():
+
+    st = tiny_state(multiplicative=torch.tensor([2.0]).to(BF16))
+    st.context[0, :2] = 1   # tokens 0 and 1 seen
+    x = oracle.process_row(row([-2.0, 3.0, 3.0, -2.0]), st, 0, oracle.MULT, None, [], None)
+    assert x[:4].float().tolist() == [-4.0, 1.5, 3.0, -2.0]
+
+
+def test_frequency_presence_bias_temperature_closed_form():
+
+    st = tiny_state(frequency=torch.tensor([0.5]).to(BF16), presence=torch.tensor([0.25]).to(BF16),
+                    temperature=torch.tensor([2.0]).to(BF16))
+    st.decode[0, 1] = 3
+    st.bias[0, 2] = 1.5
+    ind = oracle.FREQ | oracle.PRES | oracle.BIAS | oracle.TEMP
+    x = oracle.process_row(row([1.0, 1.0, 1.0]), st, 0, ind, None, [], None)
+    # token 1: (1 - 3 * 0.5 - 0.25) / 2 = -0.375 ; token 2: (1 + 1.5) / 2 = 1.25
+    assert x[:3].float().tolist() == [0.5, -0.375, 1.25]
+
+
+def test_frequency_penalty_rounds_once():
+    """bf16(x - c * f) in one rounding (torch addcmul), not bf16(x - bf16(c * f))."""
+
+    g = torch.Generator().manual_seed(0)
+    found = None
+
+    for _ in range(20000):
+
+        x = float(torch.randn(1, generator=g).to(BF16) * 8)
+        f = float((torch.rand(1, generator=g) * 2).to(BF16))
+        c = int(torch.randint(1, 200, (1,), generator=g))
+        single = float(torch.tensor(x - c * f, dtype=torch.float32).to(BF16))
+        cf = float(torch.tensor(c * f, dtype=torch.float32).to(BF16))
+        double = float(torch.tensor(x - cf, dtype=torch.float32).to(BF16))
+
+        if single != double:
+
+            found = (x, f, c, single)
+            break
+
+    assert found is not None
+    x, f, c, single = found
+    st = tiny_state(frequency=torch.tensor([f]).to(BF16))
+    st.decode[0, 0] = c
+    out = oracle.process_row(row([x]), st, 0, oracle.FREQ, None, [], None)
+    assert float(out[0]) == single
+
+
+def test_grammar_and_history():
+
+    st = tiny_state(presence=torch.tensor([1.0]).to(BF16))
+    st.grammar[0, 0, 0] = 0b1011   # tokens 0, 1, 3 allowed
+    x = oracle.process_row(row([1.0, 1.0, 1.0, 1.0, 1.0]), st, 0, oracle.GRAMMAR | oracle.PRES,
+                           st.grammar[0, 0], [0, 3, 0], None)
+    # grammar masks 2 and 4; presence hits token 3 (history) but never token 0
+    assert x[:5].float().tolist() == [1.0, 1.0, float("-inf"), 0.0, float("-inf")]
+
+
+def test_d2t_reads_target_vocabulary_state():
+
+    st = tiny_state(vocab=64, frequency=torch.tensor([1.0]).to(BF16))
+    st.decode[0, 40] = 2
+    d2t = torch.tensor([40, 3, 5, 7], dtype=torch.int64)
+    x = oracle.process_row(row([1.0, 1.0, 1.0, 1.0], vocab=4), st, 0, oracle.FREQ, None, [], d2t)
+    assert x.float().tolist() == [-1.0, 1.0, 1.0, 1.0]
+
+
+# ------------------------------------------------------------------------------------------------
+# Truncation by hand
+# ------------------------------------------------------------------------------------------------
+
+def logits_for(probs):
+
+    p = torch.tensor(probs, dtype=torch.float64)
+
+    return torch.log(p).to(torch.float32).to(BF16)[None]
+
+
+def test_top_k_hand_case():
+
+    st = tiny_state(top_k=torch.tensor([2], dtype=I32))
+    v, _ = oracle.truncate(torch.tensor([[5.0, 4.0, 3.0, 2.0]]).to(BF16), oracle.TOP_K, st, 0)
+    assert v[0].float().tolist() == [5.0, 4.0, float("-inf"), float("-inf")]
+
+
+def test_top_p_masks_the_crossing_token():
+    """mask = cumsum > p: with p = 0.6 and probabilities (0.5, 0.3, 0.2) only token 0 survives."""
+
+    st = tiny_state(top_p=torch.tensor([0.6]).to(BF16))
+    v, knife = oracle.truncate(logits_for([0.5, 0.3, 0.2]), oracle.TOP_P, st, 0)
+    assert torch.isfinite(v[0]).tolist() == [True, False, False]
+    assert not knife
+
+
+def test_top_p_keeps_first_position_even_below():
+
+    st = tiny_state(top_p=torch.tensor([0.1]).to(BF16))
+    v, _ = oracle.truncate(logits_for([0.4, 0.35, 0.25]), oracle.TOP_P, st, 0)
+    assert torch.isfinite(v[0]).tolist() == [True, False, False]
+
+
+def test_min_p_hand_case():
+
+    st = tiny_state(min_p=torch.tensor([0.2]).to(BF16))
+    v, _ = oracle.truncate(logits_for([0.6, 0.3, 0.1]), oracle.MIN_P, st, 0)
+    # lower = 0.2 * 0.6 = 0.12 > 0.1
+    assert torch.isfinite(v[0]).tolist() == [True, True, False]
+
+
+# ------------------------------------------------------------------------------------------------
+# Selection and verification invariants
+# ------------------------------------------------------------------------------------------------
+
+def stochastic_state(rows, vocab, seed):
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    b = SamplingBuffers.default(size=rows, timesteps=4, vocab_size=vocab, device="cpu")
+    b.flags = Flags.from_values(rows, 4, Indicator.TOP_K_LOGPROBS, device="cpu")
+    b.top_logprobs.fill_(5)
+
+    return b, oracle.State.from_buffers(b)
+
+
+def test_zero_noise_selects_the_maximum():
+
+    b, st = stochastic_state(4, 512, 0)
+    st.gumbel_target.zero_()
+    logits = torch.randn(4, 512).to(BF16)
+    res = oracle.singular(logits, st, scope="target")
+    assert [r.token for r in res] == logits.float().argmax(-1).tolist()
+
+
+def test_noise_can_force_any_candidate():
+
+    b, st = stochastic_state(2, 512, 0)
+    st.gumbel_target.fill_(0.0)
+    logits = torch.randn(2, 512).to(BF16)
+    # a very negative w on a non-maximal candidate that is inside the top-128
+    target = int(logits[0].float().argsort(descending=True)[5])
+    st.gumbel_target[0, 0, target] = -1000.0
+    res = oracle.singular(logits, st, scope="target")
+    assert res[0].token == target
+
+
+def test_logprobs_are_log_softmax_of_the_support():
+
+    b, st = stochastic_state(3, 1024, 1)
+    logits = (torch.randn(3, 1024) * 3).to(BF16)
+    res = oracle.singular(logits, st, scope="target", logprobs=True, max_top_logprobs=5)
+
+    for r, rec in enumerate(res):
+
+        v = logits[r].float().sort(descending=True).values[:128].double()
+        lse = torch.logsumexp(v, 0)
+        assert abs(rec.top_logprobs[0] - float(v[0] - lse)) < 1e-5
+        assert rec.logprob <= 0
+
+
+def verification_case(drafted, gamma=3, vocab=256, probs=None, uniform=None, seed=0):
+
+    b, st = stochastic_state(1, vocab, seed)
+    g = torch.Generator().manual_seed(seed)
+    logits = (torch.randn(gamma + 1, vocab, generator=g) * 2).to(BF16)
+
+    if uniform is not None:
+
+        st.uniform[0, :gamma + 1] = torch.tensor(uniform, dtype=torch.float32).to(BF16)
+
+    res = oracle.multistep(logits, st, torch.tensor(drafted, dtype=I32), [0, gamma + 1],
+                           probabilities=probs, logprobs=True)
+
+    return res[0], logits, st
+
+
+def test_point_mass_draft_of_argmax_is_accepted_with_u_below_p():
+
+    gamma = 3
+    _, logits, _ = verification_case([0] * (gamma + 1))
+    drafted = logits.float().argmax(-1).tolist()
+    rec, _, _ = verification_case(drafted, uniform=[1e-3] * (gamma + 1))
+    assert rec.offset == gamma
+    assert rec.tokens[:gamma] == drafted[:gamma]
+
+
+def test_draft_outside_support_is_rejected():
+
+    gamma = 3
+    _, logits, _ = verification_case([0] * (gamma + 1))
+    worst = logits[0].float().argmin().item()
+    rec, _, _ = verification_case([worst, 1, 1, 1], uniform=[1e-3] * (gamma + 1))
+    assert rec.offset == 0
+    assert rec.tokens[0] != worst
+
+
+def test_residual_picks_the_only_positive_candidate():
+    """q = p on every candidate but one: the residual max(p - q, 0) leaves only that one."""
+
+    gamma, vocab = 2, 256
+    rec0, logits, st = verification_case([1, 2, 3], gamma=gamma, vocab=vocab, uniform=[1.0, 1.0, 1.0])
+    v, idx = oracle.bounded(logits[0].float().to(BF16)[None])
+    p = torch.log_softmax(v.float(), -1).exp()[0]
+    q = torch.zeros(1, gamma, vocab)
+    q[0, 0, idx[0].long()] = p
+    keep = int(idx[0, 3])
+    q[0, 0, keep] = 0.0
+    drafted = [int(idx[0, 0]), 2, 3]
+    q[0, 0, drafted[0]] = 1.0      # u q = 1 > p: the first draft is rejected
+    rec, _, _ = verification_case(drafted, gamma=gamma, vocab=vocab, probs=q.to(BF16), uniform=[1.0, 1.0, 1.0])
+    assert rec.offset == 0
+    assert rec.tokens == [keep]
+
+
+def test_offsets_and_emitted_prefix_invariants():
+
+    g = torch.Generator().manual_seed(3)
+
+    for seed in range(10):
+
+        drafted = torch.randint(0, 256, (4,), generator=g).tolist()
+        rec, _, _ = verification_case(drafted, seed=seed)
+        assert 0 <= rec.offset <= 3
+        assert rec.tokens[:rec.offset] == drafted[:rec.offset]
+        assert len(rec.logprobs) == rec.offset + 1
+        assert all(lp <= 0 for lp in rec.logprobs)
+
+
+# ------------------------------------------------------------------------------------------------
+# Cross-check against the batch-level restatement (sonic_sampler.core.NaiveSampler)
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("indicator", [0x3BE, 0x5BE, 0x41, 0x2A])
+def test_per_row_oracle_matches_batch_naive(indicator):
+
+    from sonic_sampler.core import NaiveSampler
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Indicator
+
+    rows, vocab = 6, 4096
+    b = SamplingBuffers.random(size=rows, timesteps=2, vocab_size=vocab, device="cpu", seed=indicator,
+                               indicators=Indicator(indicator), max_top_logprobs=5)
+    logits = (torch.randn(rows, vocab, generator=torch.Generator().manual_seed(indicator)) * 3).to(BF16)
+
+    naive = NaiveSampler(buffers=b, max_top_logprobs=5)
+    expected = naive.singular(logits.clone(), None, 0, prefill=True, logprobs=True)
+    st = oracle.State.from_buffers(b)
+    res = oracle.singular(logits, st, scope="target", logprobs=True, max_top_logprobs=5)
+
+    assert [r.token for r in res] == expected.tokens[:, 0].tolist()
+
+    for r, rec in enumerate(res):
+
+        assert float(torch.tensor(rec.logprob).to(BF16)) == float(expected.logprobs.selected[r, 0])

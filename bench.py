@@ -338,7 +338,14 @@ def cpu_baseline_c1(workload: SingularWorkload, rows: int) -> dict:
     }
 
 
-def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox: bool = True) -> dict:
+def _queue_behind_sleep(ms: float = 60.0) -> None:
+    """Keeps the GPU busy while the host enqueues the timed launches, so that they run back to
+    back and each event pair brackets exactly one kernel."""
+
+    torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
+
+
+def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox: bool = True) -> dict:
 
     from sonic_sampler.interface import UnshardedFusedSingular
 
@@ -370,8 +377,11 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox:
         step(i)
 
     torch.cuda.synchronize()
+
+    # Eager launches: per-launch kernel time from event pairs on the launch stream.
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(steps)]
+    _queue_behind_sleep(max(60.0, steps * 0.3))
     wall0 = time.perf_counter()
 
     for i in range(steps):
@@ -384,6 +394,37 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox:
     wall = time.perf_counter() - wall0
     launch_us = [a.elapsed_time(b) * 1e3 for a, b in events]
     kernel_us = statistics.mean(launch_us)
+
+    # hipGraph replays (one captured step per input set), back to back.
+    graphs = []
+
+    for i in range(sets):
+
+        g = torch.cuda.CUDAGraph()
+
+        with torch.cuda.graph(g):
+
+            step(i)
+
+        graphs.append(g)
+
+    for i in range(3 * sets):
+
+        graphs[i % sets].replay()
+
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _queue_behind_sleep(max(60.0, steps * 0.05))
+    start.record(stream)
+
+    for i in range(steps):
+
+        graphs[i % sets].replay()
+
+    end.record(stream)
+    torch.cuda.synchronize()
+    graph_us = start.elapsed_time(end) * 1e3 / steps
+
     algorithmic = c1_algorithmic_bytes(batch, vocab)
     achieved = algorithmic / (kernel_us * 1e-6) / 1e9
 
@@ -403,13 +444,16 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox:
         "config": {
             "workload": "config 1: UnshardedFusedSingular.autoregressive B=64 V=128256 bf16, "
                         "penalties + bias + temperature + top-k/top-p/min-p + Gumbel-max, "
-                        "logprobs + top-5, update_counts",
+                        "logprobs + top-5, update_counts; one kernel launch per step",
             "rows": batch,
             "vocab": vocab,
             "input_sets_rotated": sets,
+            "algorithmic_bytes_per_step": algorithmic,
             "achieved_hbm_gbs": round(achieved, 1),
             "rows_per_s": round(batch / (kernel_us * 1e-6), 1),
-            "median_us": round(statistics.median(launch_us), 3),
+            "median_kernel_us": round(statistics.median(launch_us), 3),
+            "graph_replay_us_per_step": round(graph_us, 3),
+            "host_us_per_eager_call": round(wall * 1e6 / steps, 1),
         },
         "roofline": {
             "bound": "hbm",
@@ -424,9 +468,24 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 8, philox:
     if cpu_rows > 0:
 
         sys.path.insert(0, str(ROOT))
-        result["cpu_baseline"] = cpu_baseline_c1(base, cpu_rows)
+        result["cpu_baseline"] = cpu_baseline_c1(base, min(cpu_rows, batch))
 
     return result
+
+
+def copy_calibration(gib: float = 1.0, repeats: int = 5) -> None:
+    """A plain device copy of known size, to scale the FETCH_SIZE / WRITE_SIZE counters."""
+
+    n = int(gib * (1 << 30)) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+
+    for _ in range(repeats):
+
+        dst.copy_(src)
+
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "repeats": repeats}))
 
 
 def main(argv=None) -> int:
@@ -435,11 +494,19 @@ def main(argv=None) -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--cpu-rows", type=int, default=8,
+    parser.add_argument("--cpu-rows", type=int, default=64,
                         help="rows of config 1 timed for the CPU baseline (0 to skip)")
     parser.add_argument("--buffer-noise", action="store_true",
                         help="read Gumbel noise from the buffers instead of the Philox stream")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a 1 GiB device copy (PMC counter calibration)")
     args = parser.parse_args(argv)
+
+    if args.copy_calibration:
+
+        copy_calibration()
+
+        return 0
 
     if args.gpus != 1:
 

@@ -2,17 +2,15 @@
  * sonic_sampler.h -- C-ABI of the MI355X (gfx950) fused sampling / verification library.
  *
  * Every entry point takes a pointer to a plain argument struct (raw device pointers, element
- * strides, sizes, flags and a hipStream_t passed as void*), enqueues exactly one kernel launch
- * on that stream and returns an ss_status code. No entry point allocates device memory,
- * synchronises the host or throws, so all of them may be recorded into a hipGraph.
+ * strides, sizes, flags and a hipStream_t passed as void*), enqueues its kernel launches (two or
+ * three, back to back) on that stream and returns an ss_status code. No entry point allocates
+ * device memory, synchronises the host or throws, so all of them may be recorded into a hipGraph.
  *
  * Conventions shared by all structs:
  *   - strides are in ELEMENTS of the pointed-to type, never bytes;
  *   - the vocabulary axis is unit-stride (contiguous);
  *   - a NULL pointer means "stage / buffer absent" exactly like a `None` tensor in the reference's
- *     functional API (src/sonic_sampler/interface/functional/singular.py:75-121);
- *   - `tickets` is a caller-owned int32 array, zero-initialised once at allocation; kernels use it
- *     for per-row / per-request arrival counting and leave it zeroed again on exit.
+ *     functional API (src/sonic_sampler/interface/functional/singular.py:75-121).
  *
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   ss_topk             <- UnshardedBoundedTopK.__call__, src/sonic_sampler/interface/topk.py:98-161
@@ -92,7 +90,6 @@ typedef struct ss_topk_args {
     int32_t reserved;
     void *scratch;       /* rows * stride_scratch elements (uint32 or uint64) */
     int64_t stride_scratch;
-    int32_t *tickets;    /* >= rows int32, zeroed */
     void *values;        /* [rows, k] bf16 or fp32 */
     int32_t *indices;    /* [rows, k] */
     void *stream;        /* hipStream_t */
@@ -150,7 +147,6 @@ typedef struct ss_singular_args {
     uint16_t *probabilities; int64_t stride_probabilities; /* [slots, target_vocab] bf16 or NULL */
     /* in-flight */
     uint32_t *scratch; int64_t stride_scratch;             /* [rows, tiles * 128] */
-    int32_t *tickets;                                      /* >= rows int32, zeroed */
     void *stream;
 } ss_singular_args;
 
@@ -202,7 +198,6 @@ typedef struct ss_multistep_args {
     float *values;               /* [rows, 128] fp32 truncated log-probabilities */
     int32_t *indices;            /* [rows, 128] */
     uint32_t *scratch; int64_t stride_scratch;
-    int32_t *tickets;            /* >= rows + B int32, zeroed */
     void *stream;
 } ss_multistep_args;
 

@@ -1,12 +1,11 @@
-// Fused chain speculative verification in one launch (replaces K1 ops/prologue.py:272-472, K5
-// ops/multistep.py:76-226 and K6 ops/verify.py:244-434 of the reference).
-//
-// Grid: rows * tiles workgroups, rows = B * (gamma + 1) or cu_seqlens[B] (variable lookahead).
-//   tile stage    every workgroup: prologue over one tile of one row -> tile argmax / top-128;
-//   row stage     last workgroup of a row (row ticket): merge -> truncation -> fp32 log_softmax,
-//                 written to values / indices [row, 128] (greedy rows: the argmax in indices);
-//   request stage last row of a request to finish (request ticket): greedy or stochastic chain
-//                 verification, residual resampling, logprobs, top-Z, decode-count update.
+// Fused chain speculative verification (replaces K1 ops/prologue.py:272-472, K5
+// ops/multistep.py:76-226 and K6 ops/verify.py:244-434 of the reference), as three back-to-back
+// launches on the caller's stream; rows = B * (gamma + 1) or cu_seqlens[B] (variable lookahead).
+//   tile stage    grid rows * tiles: prologue over one tile of one row -> tile argmax / top-128;
+//   row stage     grid rows: merge -> truncation -> fp32 log_softmax, written to values /
+//                 indices [row, 128] (greedy rows: the argmax in indices[row, 0]);
+//   request stage grid B (one wavefront each): greedy or stochastic chain verification, residual
+//                 resampling, logprobs, top-Z, decode-count update.
 // Semantics follow the reference's PyTorch path (core/naive.py:497-646 `verification`,
 // :694-708 `multistep`), applied per request so that slots and variable lookahead compose.
 #include "ss_sampling.h"
@@ -48,20 +47,8 @@ __device__ __forceinline__ int find_position(const int32_t *idx, int d) {
     return p < SS_K ? p : -1;
 }
 
-template <int E, bool VEC>
-__global__ __launch_bounds__(SS_BLOCK) void multistep_kernel(ss_multistep_args a, int tiles) {
-    __shared__ SampleSmem sm;
-    const int row = blockIdx.x / tiles;
-    const int tile = blockIdx.x - row * tiles;
-    const Request rq = resolve_request(a, row);
-    const int step = row - rq.margin;
-    // Rows outside every request, or requests longer than lookahead + 1, break the layout
-    // contract; they are skipped (their outputs stay unwritten) rather than read out of bounds.
-    if (step < 0 || step >= rq.n || rq.n > a.lookahead + 1) return;
-    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
-    const uint32_t ind = a.indicators[slot];
-    const bool greedy = (ind & IND_GREEDY) != 0;
-
+__device__ __forceinline__ RowState multistep_row_state(const ss_multistep_args &a, int row,
+                                                        int step, int slot, uint32_t ind) {
     RowState rs;
     rs.ind = ind;
     rs.logits = a.logits + (int64_t)row * a.stride_logits;
@@ -78,6 +65,28 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_kernel(ss_multistep_args a
     rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.nhist = 0;
+    return rs;
+}
+
+// Rows outside every request, or requests longer than lookahead + 1, break the layout contract;
+// they are skipped (their outputs stay unwritten) rather than read out of bounds.
+__device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, const Request &rq,
+                                                int step) {
+    return step >= 0 && step < rq.n && rq.n <= a.lookahead + 1;
+}
+
+// Tile stage: grid rows * tiles.
+template <int E, bool VEC>
+__global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x / tiles;
+    const int tile = blockIdx.x - row * tiles;
+    const Request rq = resolve_request(a, row);
+    const int step = row - rq.margin;
+    if (!row_in_contract(a, rq, step)) return;
+    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
+    const uint32_t ind = a.indicators[slot];
+    RowState rs = multistep_row_state(a, row, step, slot, ind);
     if (step > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         // Step s of a request sees the drafts of steps < s as extra decode history
         // (core/naive.py:179-198, the `tril` history with timestep None).
@@ -85,18 +94,25 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_kernel(ss_multistep_args a
         if ((int)threadIdx.x < step) sm.hist[threadIdx.x] = a.drafted_tokens[rq.margin + threadIdx.x];
         __syncthreads();
     }
-
     uint32_t keys[E];
     prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
-    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
-    tile_stage<E>(sm, greedy, keys, scr, tile);
+    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
+}
 
-    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
-
-    // ---- row stage ------------------------------------------------------------------------------
+// Row stage: grid rows; merge -> truncation -> fp32 log_softmax into values / indices [row, 128]
+// (greedy rows: the argmax in indices[row, 0]).
+__global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x;
+    const Request rq = resolve_request(a, row);
+    const int step = row - rq.margin;
+    if (!row_in_contract(a, rq, step)) return;
+    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
+    const uint32_t ind = a.indicators[slot];
+    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     float *vrow = a.values + (int64_t)row * SS_K;
     int32_t *irow = a.indices + (int64_t)row * SS_K;
-    if (greedy) {
+    if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
             const int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
             if (threadIdx.x == 0) {
@@ -104,25 +120,40 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_kernel(ss_multistep_args a
                 vrow[0] = 0.0f;
             }
         }
-    } else {
-        float v0 = 0.f, v1 = 0.f;
-        int i0 = 0, i1 = 0;
-        merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
-        if (threadIdx.x < 64) {
-            truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
-                     a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
-            float m, x0, x1;
-            const float logs = logf(exp_parts(v0, v1, m, x0, x1));
-            const int e0 = 2 * threadIdx.x;
-            vrow[e0] = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
-            vrow[e0 + 1] = (v1 - m) - logs;
-            irow[e0] = i0;
-            irow[e0 + 1] = i1;
-        }
+        return;
     }
-
-    if (!arrive(a.tickets + a.rows + rq.b, rq.n, &sm.sel.flag)) return;
+    float v0 = 0.f, v1 = 0.f;
+    int i0 = 0, i1 = 0;
+    merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
     if (threadIdx.x >= 64) return;
+    truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
+             a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
+    float m, x0, x1;
+    const float logs = logf(exp_parts(v0, v1, m, x0, x1));
+    const int e0 = 2 * threadIdx.x;
+    vrow[e0] = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
+    vrow[e0 + 1] = (v1 - m) - logs;
+    irow[e0] = i0;
+    irow[e0 + 1] = i1;
+}
+
+// Request stage: grid B, one wavefront per request.
+__global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args a) {
+    const int b = blockIdx.x;
+    Request rq;
+    if (a.cu_seqlens) {
+        rq.b = b;
+        rq.margin = a.cu_seqlens[b];
+        rq.n = a.cu_seqlens[b + 1] - rq.margin;
+    } else {
+        rq.b = b;
+        rq.n = a.lookahead + 1;
+        rq.margin = b * rq.n;
+    }
+    if (rq.n < 1 || rq.n > a.lookahead + 1 || rq.margin < 0 || rq.margin + rq.n > a.rows) return;
+    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
+    const uint32_t ind = a.indicators[slot];
+    const bool greedy = (ind & IND_GREEDY) != 0;
 
     // ---- request stage (wave 0) -------------------------------------------------------------------
     const int lane = threadIdx.x;
@@ -241,12 +272,16 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((multistep_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((multistep_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((multistep_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((multistep_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((multistep_tiles_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((multistep_tiles_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((multistep_tiles_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((multistep_tiles_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
+    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
+    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
@@ -260,7 +295,7 @@ static bool aligned_ms(const void *p, int64_t stride, int bytes) {
 extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
     using namespace ss;
     if (!a || !a->logits || !a->indicators || !a->drafted_tokens || !a->out_tokens || !a->offsets ||
-        !a->values || !a->indices || !a->scratch || !a->tickets || !a->uniform)
+        !a->values || !a->indices || !a->scratch || !a->uniform)
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows < 0 || a->batch < 0 || a->vocab_size <= 0 || a->stride_logits < a->vocab_size)
         return SS_ERR_INVALID_ARGUMENT;

@@ -1,26 +1,20 @@
-// Fused single-step sampling in one launch (replaces K1 ops/prologue.py:272-472 followed by K4
-// ops/singular.py:154-358 of the reference).
+// Fused single-step sampling (replaces K1 ops/prologue.py:272-472 followed by K4
+// ops/singular.py:154-358 of the reference), as two back-to-back launches on the caller's stream.
 //
-// Grid: rows * tiles workgroups. Every workgroup runs the logit-processor prologue over one
+// Tile stage, grid rows * tiles: every workgroup runs the logit-processor prologue over one
 // vocabulary tile of one row and leaves either the tile argmax (greedy rows) or its exact top-128
-// in the row's scratch. The last workgroup of the row merges the candidates and performs the
-// selection: truncation, d2t remap, Gumbel-max over bf16(v - w), decode-count update, logprobs,
-// top-Z logprobs and the draft-probability scatter. Semantics follow the reference's PyTorch path
-// (core/naive.py:377-495 `selection`, :648-692 `preamble` / `singular`).
+// in the row's scratch. Row stage, grid rows: one workgroup per row merges the candidates and
+// performs the selection: truncation, d2t remap, Gumbel-max over bf16(v - w), decode-count update,
+// logprobs, top-Z logprobs and the draft-probability scatter. The launch boundary orders the two
+// stages across all XCDs without per-workgroup cache maintenance. Semantics follow the
+// reference's PyTorch path (core/naive.py:377-495 `selection`, :648-692 `preamble` / `singular`).
 #include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
 
 namespace ss {
 
-template <int E, bool VEC>
-__global__ __launch_bounds__(SS_BLOCK) void singular_kernel(ss_singular_args a, int tiles) {
-    __shared__ SampleSmem sm;
-    const int row = blockIdx.x / tiles;
-    const int tile = blockIdx.x - row * tiles;
-    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
-    const uint32_t ind = a.indicators[slot];
-    const bool greedy = (ind & IND_GREEDY) != 0;
-
+__device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a, int row,
+                                                       int slot, uint32_t ind) {
     RowState rs;
     rs.ind = ind;
     rs.logits = a.logits + (int64_t)row * a.stride_logits;
@@ -35,21 +29,38 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_kernel(ss_singular_args a, 
     rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.nhist = 0;
+    return rs;
+}
+
+// Tile stage: grid rows * tiles.
+template <int E, bool VEC>
+__global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x / tiles;
+    const int tile = blockIdx.x - row * tiles;
+    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
+    const uint32_t ind = a.indicators[slot];
+    RowState rs = singular_row_state(a, row, slot, ind);
     if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         rs.nhist = a.timestep;
         if ((int)threadIdx.x < rs.nhist)
             sm.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
         __syncthreads();
     }
-
     uint32_t keys[E];
     prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
-    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
-    tile_stage<E>(sm, greedy, keys, scr, tile);
+    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
+}
 
-    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
+// Row stage: grid rows; merge of the tiles' candidates and the selection.
+__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    const int row = blockIdx.x;
+    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
+    const uint32_t ind = a.indicators[slot];
+    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
 
-    if (greedy) {
+    if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
             int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
             if (a.d2t) token = a.d2t[token];
@@ -141,12 +152,14 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((singular_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((singular_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((singular_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((singular_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((singular_tiles_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((singular_tiles_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((singular_tiles_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((singular_tiles_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
+    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
@@ -159,7 +172,7 @@ static bool aligned(const void *p, int64_t stride, int bytes_per_vec) {
 
 extern "C" int ss_fused_singular(const ss_singular_args *a) {
     using namespace ss;
-    if (!a || !a->logits || !a->indicators || !a->tokens || !a->scratch || !a->tickets)
+    if (!a || !a->logits || !a->indicators || !a->tokens || !a->scratch)
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows < 0 || a->vocab_size <= 0 || a->stride_logits < a->vocab_size)
         return SS_ERR_INVALID_ARGUMENT;

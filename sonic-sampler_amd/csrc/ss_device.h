@@ -1,5 +1,5 @@
 // Device helpers shared by every kernel of the library: bf16 rounding, order-preserving keys,
-// wave64 / workgroup scans and reductions, and the cross-workgroup arrival ticket.
+// wave64 / workgroup scans and reductions.
 //
 // All kernels run with SS_BLOCK = 256 threads (four wave64 wavefronts).
 #pragma once
@@ -142,27 +142,6 @@ __device__ __forceinline__ void block_exclusive_scan(uint32_t (&v)[NV], uint32_t
         totals[i] = total;
     }
     __syncthreads();
-}
-
-// ---------------------------------------------------------------------------------------------
-// Cross-workgroup arrival ticket. Every workgroup of a group calls arrive() after writing its
-// partial results; exactly one (the last to arrive) gets `true`, after which the partial results
-// of all others are visible to it. The last arriver resets the counter so that the next launch
-// (or the next replay of a captured graph) starts from zero again.
-// ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ bool arrive(int32_t *counter, int32_t expected, int32_t *flag_smem) {
-    __threadfence();  // release this thread's global writes at agent scope
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t old = atomicAdd(counter, 1);
-        int32_t last = (old == expected - 1);
-        if (last) *counter = 0;
-        *flag_smem = last;
-    }
-    __syncthreads();
-    bool last = *flag_smem != 0;
-    if (last) __threadfence();  // acquire: later loads observe the other workgroups' writes
-    return last;
 }
 
 }  // namespace ss

@@ -47,32 +47,65 @@ __device__ __forceinline__ int tile_col(int j) {  // column offset of element j 
     return (j >> 2) * (SS_BLOCK * 4) + (int)threadIdx.x * 4 + (j & 3);
 }
 
-// One element through the processor chain. x is bf16-exact on entry and on exit.
-__device__ __forceinline__ float process_element(float x, const RowState &rs, int tcol,
-                                                 uint32_t gword, int32_t dec, int32_t ctx,
-                                                 uint32_t braw, const int32_t *hist) {
-    const uint32_t ind = rs.ind;
-    if (ind & IND_GRAMMAR) {
-        if (rs.grammar && !((gword >> (tcol & 31)) & 1u)) x = -INFINITY;
-    }
-    if ((ind & (IND_MULT | IND_FREQ | IND_PRES)) && rs.dec) {
-        // The history never counts token 0: the reference pads the history with 0 and then
-        // restores the original count of token 0 (core/naive.py:179-203).
-        if (tcol != 0) {
-            for (int h = 0; h < rs.nhist; ++h) dec += (hist[h] == tcol);
-        }
-        if ((ind & IND_MULT) && rs.ctx) {
-            if (dec + ctx > 0) x = rbf(x < 0.0f ? x * rs.rep : x / rs.rep);
-        }
-        if (ind & IND_FREQ) x = rbf(x - rbf((float)dec) * rs.freq);
-        if (ind & IND_PRES) x = rbf(x - (dec > 0 ? rs.pres : 0.0f));
-    }
-    if ((ind & IND_BIAS) && rs.bias) x = rbf(x + bf2f(braw));
-    if (ind & IND_TEMP) x = rbf(x / rs.temp);
-    return x;
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 b2v __attribute__((ext_vector_type(2)));
+
+// Rounds two fp32 values to bf16 (round-to-nearest-even, v_cvt_pk_bf16_f32) in place.
+__device__ __forceinline__ void round_pair(float &a, float &b) {
+    const f2v v = {a, b};
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v));
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
 }
 
-// Streams one tile of one row through the prologue and returns the elements' keys (0 = absent).
+template <int E>
+__device__ __forceinline__ void round_all(float (&x)[E]) {
+#pragma unroll
+    for (int j = 0; j < E; j += 2) round_pair(x[j], x[j + 1]);
+}
+
+// Divisor state of a per-row constant d: rcp = RN(1/d); `exact` is false when d is 0, infinite or
+// NaN, where the plain IEEE quotient is used instead.
+struct Divisor {
+    float d, rcp;
+    bool fast;
+};
+
+__device__ __forceinline__ Divisor make_divisor(float d) {
+    Divisor v;
+    v.d = d;
+    v.rcp = 1.0f / d;
+    v.fast = d != 0.0f && __builtin_isfinite(d) && __builtin_isfinite(v.rcp) && v.rcp != 0.0f;
+    return v;
+}
+
+// bf16(x / d) for a bf16-exact x: q0 = x * RN(1/d) is within 2 ulp of x / d and one FMA
+// correction brings it within 0.5 ulp + 2^-24 ulp. Because x and d carry 8 significant bits,
+// x / d is either exactly representable (then the corrected quotient equals it) or at least
+// ~2^-17 (relative) away from every bf16 rounding boundary, so the bf16 rounding of the result is
+// that of the correctly rounded fp32 quotient, which is what torch's `div` computes.
+__device__ __forceinline__ float div_exact_bf16(float x, const Divisor &v) {
+    if (!v.fast) return x / v.d;
+    const float q0 = x * v.rcp;
+    const float r = __builtin_fmaf(-q0, v.d, x);
+    const float q1 = __builtin_fmaf(r, v.rcp, q0);
+    return __builtin_isinf(x) ? q0 : q1;
+}
+
+// Order-preserving 16-bit key of a bf16-exact float (-0 folded onto +0).
+__device__ __forceinline__ uint32_t key_of(float x) {
+    const uint32_t u = __float_as_uint(x + 0.0f);
+    const uint32_t flip = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
+    return (u ^ flip) >> 16;
+}
+
+// Streams one tile of one row through the processor chain and returns the keys (0 = absent).
+// The chain runs processor by processor over all E elements, so every indicator test is a
+// uniform branch taken once per tile, and each processor ends with one packed bf16 rounding --
+// the rounding points of the reference's PyTorch path (core/naive.py:131-268): grammar mask,
+// multiplicative penalty (x < 0 ? x * r : x / r where context + decode counts > 0), frequency
+// penalty x - bf16(count) * f (one rounding, as torch's addcmul), presence penalty, logit bias,
+// temperature.
 // VEC: vocabulary and every row base are 4-element aligned, so a 4-column chunk is either fully
 // inside the vocabulary or fully outside, and planes load as 8 / 16-byte vectors.
 template <int E, bool VEC>
@@ -80,103 +113,146 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
                                               const int32_t *hist, uint32_t (&keys)[E]) {
     constexpr int NCH = E / 4;
     const uint32_t ind = rs.ind;
-    const bool any_proc = (ind & 0x3Fu) != 0;
     const bool use_g = (ind & IND_GRAMMAR) && rs.grammar;
     const bool use_rep = (ind & (IND_MULT | IND_FREQ | IND_PRES)) && rs.dec;
-    const bool use_ctx = use_rep && (ind & IND_MULT) && rs.ctx;
+    const bool use_mult = use_rep && (ind & IND_MULT) && rs.ctx;
     const bool use_bias = (ind & IND_BIAS) && rs.bias;
-    const bool remap = rs.d2t != nullptr && (ind & 0x1Fu);
+    const bool remap = rs.d2t != nullptr && (use_g || use_rep || use_bias);
+    const bool direct = VEC && !remap;
 
-    uint32_t lg[E];
-    int tcol[E];
-    uint32_t gw[E];
-    int32_t dc[E], cc[E];
-    uint32_t bs[E];
-
-    // Logits: 8-byte vector per chunk when aligned, streamed with non-temporal loads.
+    float x[E];
+    bool ok[E];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = col0 + tile_col(4 * c);
         if (VEC) {
-            u32x2 w = col < V ? __builtin_nontemporal_load((const u32x2 *)(rs.logits + col))
-                              : u32x2{0u, 0u};
-            lg[4 * c + 0] = w.x & 0xffffu;
-            lg[4 * c + 1] = w.x >> 16;
-            lg[4 * c + 2] = w.y & 0xffffu;
-            lg[4 * c + 3] = w.y >> 16;
+            const bool in = col < V;
+            const u32x2 w = in ? __builtin_nontemporal_load((const u32x2 *)(rs.logits + col))
+                               : u32x2{0u, 0u};
+            x[4 * c + 0] = __uint_as_float(w.x << 16);
+            x[4 * c + 1] = __uint_as_float(w.x & 0xffff0000u);
+            x[4 * c + 2] = __uint_as_float(w.y << 16);
+            x[4 * c + 3] = __uint_as_float(w.y & 0xffff0000u);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                lg[4 * c + i] = col + i < V ? (uint32_t)rs.logits[col + i] : 0xff80u;
+            for (int i = 0; i < 4; ++i) {
+                ok[4 * c + i] = col + i < V;
+                x[4 * c + i] = ok[4 * c + i] ? bf2f(rs.logits[col + i]) : 0.0f;
+            }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) tcol[4 * c + i] = col + i;
     }
-    if (any_proc) {
+
+    if (use_g || use_rep || use_bias) {
+        int tcol[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) tcol[j] = col0 + tile_col(j);
         if (remap) {
 #pragma unroll
-            for (int j = 0; j < E; ++j) tcol[j] = tcol[j] < V ? rs.d2t[tcol[j]] : 0;
+            for (int j = 0; j < E; ++j) tcol[j] = ok[j] ? rs.d2t[tcol[j]] : 0;
         }
         if (use_g) {
 #pragma unroll
             for (int j = 0; j < E; ++j) {
-                if (!remap && VEC && (j & 3)) {
-                    gw[j] = gw[j & ~3];
+                uint32_t w;
+                if (direct) {
+                    w = ok[j] ? rs.grammar[(col0 + tile_col(j & ~3)) >> 5] : 0xffffffffu;
                 } else {
-                    gw[j] = (col0 + tile_col(j) < V) ? rs.grammar[tcol[j] >> 5] : 0xffffffffu;
+                    w = ok[j] ? rs.grammar[tcol[j] >> 5] : 0xffffffffu;
                 }
+                x[j] = ((w >> (tcol[j] & 31)) & 1u) ? x[j] : -INFINITY;
             }
         }
         if (use_rep) {
+            int32_t dec[E];
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 const int col = col0 + tile_col(4 * c);
-                if (VEC && !remap) {
-                    i32x4 d = col < V ? __builtin_nontemporal_load((const i32x4 *)(rs.dec + col))
-                                      : i32x4{0, 0, 0, 0};
-                    dc[4 * c + 0] = d.x; dc[4 * c + 1] = d.y; dc[4 * c + 2] = d.z; dc[4 * c + 3] = d.w;
-                    if (use_ctx) {
-                        i32x4 q = col < V ? __builtin_nontemporal_load((const i32x4 *)(rs.ctx + col))
-                                          : i32x4{0, 0, 0, 0};
-                        cc[4 * c + 0] = q.x; cc[4 * c + 1] = q.y; cc[4 * c + 2] = q.z; cc[4 * c + 3] = q.w;
-                    }
+                if (direct) {
+                    const i32x4 d = ok[4 * c] ? __builtin_nontemporal_load((const i32x4 *)(rs.dec + col))
+                                              : i32x4{0, 0, 0, 0};
+                    dec[4 * c + 0] = d.x; dec[4 * c + 1] = d.y; dec[4 * c + 2] = d.z; dec[4 * c + 3] = d.w;
                 } else {
 #pragma unroll
+                    for (int i = 0; i < 4; ++i) dec[4 * c + i] = ok[4 * c + i] ? rs.dec[tcol[4 * c + i]] : 0;
+                }
+            }
+            if (rs.nhist > 0) {
+                // The history never counts token 0: the reference pads the history with 0 and then
+                // restores the original count of token 0 (core/naive.py:179-203).
+                for (int h = 0; h < rs.nhist; ++h) {
+                    const int t = hist[h];
+#pragma unroll
+                    for (int j = 0; j < E; ++j) dec[j] += (tcol[j] == t && t != 0) ? 1 : 0;
+                }
+            }
+            if (use_mult) {
+                const Divisor rep = make_divisor(rs.rep);
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    int32_t ctx[4];
+                    const int col = col0 + tile_col(4 * c);
+                    if (direct) {
+                        const i32x4 q = ok[4 * c] ? __builtin_nontemporal_load((const i32x4 *)(rs.ctx + col))
+                                                  : i32x4{0, 0, 0, 0};
+                        ctx[0] = q.x; ctx[1] = q.y; ctx[2] = q.z; ctx[3] = q.w;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ctx[i] = ok[4 * c + i] ? rs.ctx[tcol[4 * c + i]] : 0;
+                    }
+#pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const bool ok = col + i < V;
-                        dc[4 * c + i] = ok ? rs.dec[tcol[4 * c + i]] : 0;
-                        if (use_ctx) cc[4 * c + i] = ok ? rs.ctx[tcol[4 * c + i]] : 0;
+                        const int j = 4 * c + i;
+                        const float y = x[j] < 0.0f ? x[j] * rs.rep : div_exact_bf16(x[j], rep);
+                        x[j] = (dec[j] + ctx[i] > 0) ? y : x[j];
                     }
                 }
+                round_all(x);
+            }
+            if (ind & IND_FREQ) {
+                float cnt[E];
+#pragma unroll
+                for (int j = 0; j < E; ++j) cnt[j] = (float)dec[j];
+                round_all(cnt);
+#pragma unroll
+                for (int j = 0; j < E; ++j) x[j] = __builtin_fmaf(-cnt[j], rs.freq, x[j]);
+                round_all(x);
+            }
+            if (ind & IND_PRES) {
+#pragma unroll
+                for (int j = 0; j < E; ++j) x[j] = x[j] - (dec[j] > 0 ? rs.pres : 0.0f);
+                round_all(x);
             }
         }
         if (use_bias) {
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 const int col = col0 + tile_col(4 * c);
-                if (VEC && !remap) {
-                    u32x2 b = col < V ? __builtin_nontemporal_load((const u32x2 *)(rs.bias + col))
-                                      : u32x2{0u, 0u};
-                    bs[4 * c + 0] = b.x & 0xffffu; bs[4 * c + 1] = b.x >> 16;
-                    bs[4 * c + 2] = b.y & 0xffffu; bs[4 * c + 3] = b.y >> 16;
+                if (direct) {
+                    const u32x2 b = ok[4 * c] ? __builtin_nontemporal_load((const u32x2 *)(rs.bias + col))
+                                              : u32x2{0u, 0u};
+                    x[4 * c + 0] += __uint_as_float(b.x << 16);
+                    x[4 * c + 1] += __uint_as_float(b.x & 0xffff0000u);
+                    x[4 * c + 2] += __uint_as_float(b.y << 16);
+                    x[4 * c + 3] += __uint_as_float(b.y & 0xffff0000u);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        bs[4 * c + i] = col + i < V ? (uint32_t)rs.bias[tcol[4 * c + i]] : 0u;
+                        x[4 * c + i] += ok[4 * c + i] ? bf2f(rs.bias[tcol[4 * c + i]]) : 0.0f;
                 }
             }
+            round_all(x);
         }
+    }
+    if (ind & IND_TEMP) {
+        const Divisor t = make_divisor(rs.temp);
+#pragma unroll
+        for (int j = 0; j < E; ++j) x[j] = div_exact_bf16(x[j], t);
+        round_all(x);
     }
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const bool ok = col0 + tile_col(j) < V;
-        float x = bf2f(lg[j]);
-        if (any_proc) {
-            x = process_element(x, rs, tcol[j], use_g ? gw[j] : 0xffffffffu, use_rep ? dc[j] : 0,
-                                use_ctx ? cc[j] : 0, use_bias ? bs[j] : 0u, hist);
-        }
-        keys[j] = ok ? key16(f2bf(x)) : 0u;
-    }
+    for (int j = 0; j < E; ++j) keys[j] = ok[j] ? key_of(x[j]) : 0u;
 }
 
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose
@@ -230,32 +306,60 @@ __device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int 
     return idx < V ? idx : V - 1;
 }
 
-// Row merge: all threads call; on return wave 0 holds the row's top-128 sorted by (value desc,
-// column asc), element e = 2 * lane + i as (v_i, idx_i).
-__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, int tiles,
-                                          int block_n, int V, float &v0, float &v1, int &i0,
-                                          int &i1) {
-    constexpr int EM = 16;
-    const int ncand = tiles * SS_K;
-    const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
-    auto load = [&](int sc, uint32_t(&out)[EM]) {
-#pragma unroll
-        for (int j = 0; j < EM; ++j) {
-            const int p = order_pos<EM, 4>(sc, j);
-            out[j] = p < ncand ? (scr[p] >> 16) : 0u;
-        }
-    };
+// Selects the row's top-128 among `nsc` blocks of candidates and leaves them, in column order,
+// as (key << 8 | 127 - pos) composites and column indices in sm.cand / sm.idx.
+template <bool HELD, int EM, class Load, class Cand>
+__device__ __forceinline__ void merge_select(SampleSmem &sm, int nsc, Load load, Cand cand,
+                                             int block_n, int V) {
     uint32_t thi, margin;
     int level;
     radix_threshold<EM, 16>(sm.sel, nsc, load, (uint32_t)SS_K, thi, level, margin);
     compact<EM, 4>(sm.sel, nsc, load, thi, level, margin, [&](uint32_t pos, int sc, int j) {
         if (pos >= (uint32_t)SS_K) return;
         const int p = order_pos<EM, 4>(sc, j);
-        const uint32_t c = scr[p];
+        const uint32_t c = cand(sc, j);
         const int idx = (p / SS_K) * block_n + (int)(c & 0xffffu);
         sm.cand[pos] = ((uint64_t)(c >> 16) << 8) | (uint64_t)(127u - pos);
         sm.idx[pos] = idx < V ? idx : V - 1;  // only an absent-element sentinel can exceed V
     });
+}
+
+// Row merge: all threads call; on return wave 0 holds the row's top-128 sorted by (value desc,
+// column asc), element e = 2 * lane + i as (v_i, idx_i). Up to 4096 candidates are read once
+// with 16-byte loads and kept in registers; larger rows stream them from the scratch per pass.
+__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, int tiles,
+                                          int block_n, int V, float &v0, float &v1, int &i0,
+                                          int &i1) {
+    constexpr int EM = 16;
+    const int ncand = tiles * SS_K;
+    const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
+    if (nsc == 1) {
+        uint32_t held[EM];
+#pragma unroll
+        for (int c = 0; c < EM / 4; ++c) {
+            const int p = order_pos<EM, 4>(0, 4 * c);  // multiple of 4; ncand is a multiple of 128
+            const uint4 q = p < ncand ? *(const uint4 *)(scr + p) : make_uint4(0u, 0u, 0u, 0u);
+            held[4 * c + 0] = q.x; held[4 * c + 1] = q.y; held[4 * c + 2] = q.z; held[4 * c + 3] = q.w;
+        }
+        merge_select<true, EM>(
+            sm, 1,
+            [&](int, uint32_t(&out)[EM]) {
+#pragma unroll
+                for (int j = 0; j < EM; ++j) out[j] = held[j] >> 16;
+            },
+            [&](int, int j) { return held[j]; }, block_n, V);
+    } else {
+        merge_select<false, EM>(
+            sm, nsc,
+            [&](int sc, uint32_t(&out)[EM]) {
+#pragma unroll
+                for (int j = 0; j < EM; ++j) {
+                    const int p = order_pos<EM, 4>(sc, j);
+                    out[j] = p < ncand ? (scr[p] >> 16) : 0u;
+                }
+            },
+            [&](int sc, int j) { return scr[order_pos<EM, 4>(sc, j)]; }, block_n, V);
+    }
     __syncthreads();
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;

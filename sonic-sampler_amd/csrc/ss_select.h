@@ -70,7 +70,7 @@ __device__ __forceinline__ void find_bin(SelectSmem &sm, int nbins, uint32_t nee
 // E keys of super-chunk sc (absent elements as 0). On return the selection rule is
 //     select  <=>  (key >> level) > thi  ||  ((key >> level) == thi && rank_among_equal < margin)
 template <int E, int KEYBITS, class Loader>
-__device__ void radix_threshold(SelectSmem &sm, int nsc, Loader load, uint32_t need, uint32_t &thi,
+__device__ __forceinline__ void radix_threshold(SelectSmem &sm, int nsc, Loader load, uint32_t need, uint32_t &thi,
                                 int &level, uint32_t &margin) {
     constexpr int ND = KEYBITS == 16 ? 2 : 3;
     const int shifts[3] = {KEYBITS - 12, KEYBITS == 16 ? 0 : 8, 0};
@@ -109,7 +109,7 @@ __device__ void radix_threshold(SelectSmem &sm, int nsc, Loader load, uint32_t n
 // super-chunk sc with its output position pos in [0, need). Positions are dense and increasing in
 // order position. Elements of one thread are visited in increasing order position.
 template <int E, int CH, class Loader, class Emit>
-__device__ void compact(SelectSmem &sm, int nsc, Loader load, uint32_t thi, int level,
+__device__ __forceinline__ void compact(SelectSmem &sm, int nsc, Loader load, uint32_t thi, int level,
                         uint32_t margin, Emit emit) {
     constexpr int NCH = E / CH;
     uint32_t base_gt = 0, base_eq = 0;

@@ -1,12 +1,11 @@
-// Bounded top-k over [rows, vocab] logits in one launch (replaces K2 ops/topk/bitpack.py:99-158
-// followed by K3 ops/topk/unpack.py:312-377 of the reference).
+// Bounded top-k over [rows, vocab] logits (replaces K2 ops/topk/bitpack.py:99-158 followed by K3
+// ops/topk/unpack.py:312-377 of the reference), as two back-to-back launches.
 //
-// Grid: rows * tiles workgroups, row-major so that the tiles of a row are dispatched together.
-// Tile stage: each workgroup streams block_n logits with coalesced 8/16-byte loads, turns them into
-// order-preserving keys and writes its exact top-k (ties to the lowest column) to the scratch row
-// in column order. Merge stage: the last workgroup of a row to arrive (arrival ticket) selects the
-// row's top-k among the tiles*k candidates, sorts them by (value desc, column asc) with a wave64
-// bitonic network and writes values / indices densely as [rows, k].
+// Tile stage, grid rows * tiles: each workgroup turns block_n logits into order-preserving keys
+// and writes its exact top-k (ties to the lowest column) to the scratch row in column order.
+// Merge stage, grid rows: selects the row's top-k among the tiles * k candidates, sorts them by
+// (value desc, column asc) with a wave64 bitonic network and writes values / indices densely as
+// [rows, k].
 #include "ss_select.h"
 #include "../../include/sonic_sampler.h"
 
@@ -45,8 +44,9 @@ struct TopkTraits<true> {
     __device__ static int cand_li(Cand c) { return (int)(c & 0xffffffffu); }
 };
 
+// Tile stage: grid rows * tiles.
 template <bool F32, int E>
-__global__ __launch_bounds__(SS_BLOCK) void topk_kernel(ss_topk_args a, int tiles) {
+__global__ __launch_bounds__(SS_BLOCK) void topk_tiles_kernel(ss_topk_args a, int tiles) {
     using Tr = TopkTraits<F32>;
     using Cand = typename Tr::Cand;
     constexpr int CH = 4;
@@ -79,9 +79,21 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_kernel(ss_topk_args a, int tile
         if (pos < (uint32_t)k) scr[tile * k + (int)pos] = Tr::pack(keys[j], order_pos<E, CH>(0, j));
     });
 
-    if (!arrive(a.tickets + row, tiles, &sm.sel.flag)) return;
+}
 
-    // ---- merge stage (last workgroup of the row) ----------------------------------------------
+// Merge stage: grid rows.
+template <bool F32>
+__global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, int tiles) {
+    using Tr = TopkTraits<F32>;
+    using Cand = typename Tr::Cand;
+    constexpr int CH = 4;
+    __shared__ TopkSmem sm;
+    const int row = blockIdx.x;
+    const int V = a.vocab_size;
+    const int k = a.k;
+    const Cand *scr = (const Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+    uint32_t thi, margin;
+    int level;
     constexpr int EM = 16;
     const int ncand = tiles * k;
     const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
@@ -131,19 +143,21 @@ static int launch_topk(const ss_topk_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((topk_kernel<F32, 4>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((topk_kernel<F32, 8>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((topk_kernel<F32, 16>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((topk_kernel<F32, 32>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((topk_tiles_kernel<F32, 4>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((topk_tiles_kernel<F32, 8>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((topk_tiles_kernel<F32, 16>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((topk_tiles_kernel<F32, 32>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
+    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
 }  // namespace ss
 
 extern "C" int ss_topk(const ss_topk_args *a) {
-    if (!a || !a->logits || !a->scratch || !a->tickets || !a->values || !a->indices)
+    if (!a || !a->logits || !a->scratch || !a->values || !a->indices)
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows < 0 || a->vocab_size <= 0) return SS_ERR_INVALID_ARGUMENT;
     if (a->k < 1 || a->k > SS_MAX_K || (a->k & (a->k - 1)) != 0) return SS_ERR_INVALID_ARGUMENT;

@@ -35,7 +35,7 @@ class TopKArgs(ctypes.Structure):
     _fields_ = [
         ("logits", c_p), ("stride_logits", c_i64), ("dtype", c_i32), ("rows", c_i32),
         ("vocab_size", c_i32), ("k", c_i32), ("block_n", c_i32), ("reserved", c_i32),
-        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("values", c_p),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("values", c_p),
         ("indices", c_p), ("stream", c_p),
     ]
 
@@ -60,7 +60,7 @@ class SingularArgs(ctypes.Structure):
         ("logprobs", c_p), ("stride_logprobs", c_i64),
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("probabilities", c_p), ("stride_probabilities", c_i64),
-        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("stream", c_p),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
     ]
 
 
@@ -84,7 +84,7 @@ class MultistepArgs(ctypes.Structure):
         ("out_tokens", c_p), ("offsets", c_p), ("logprobs", c_p),
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("values", c_p), ("indices", c_p),
-        ("scratch", c_p), ("stride_scratch", c_i64), ("tickets", c_p), ("stream", c_p),
+        ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
     ]
 
 

@@ -4,9 +4,7 @@
 ``TwoStageTiling.factory`` resolves ``block_n`` from the dispatch table (or ``block_size``),
 validates the configuration with the reference's ``ValueError`` conditions and allocates the
 in-flight buffers: ``scratchpad [B * (gamma + 1), blocks * 128]`` uint32 and, for the verifier,
-``values`` / ``indices [B * (gamma + 1), 128]``. It also allocates ``tickets``, the zeroed int32
-arrival counters the single-launch kernels use (one per logit row plus one per request); the
-kernels leave them zeroed, so the buffers can be reused across calls and graph replays.
+``values`` / ``indices [B * (gamma + 1), 128]``.
 """
 
 from __future__ import annotations
@@ -169,8 +167,8 @@ def default_device(device=None) -> torch.device:
 @dataclass(eq=False, kw_only=True)
 class TwoStageTiling:
 
-    # Accepted for API compatibility; the gfx950 path is a single launch, there is no
-    # dependent launch to overlap.
+    # Accepted for API compatibility (programmatic dependent launch has no gfx950 counterpart;
+    # the stages are ordered launches on one stream).
     pdl: bool
 
     # Tile width.
@@ -184,9 +182,6 @@ class TwoStageTiling:
 
     # Tuned dispatch, when resolved from a table.
     dispatch: Optional[VocabBucket]
-
-    # Zeroed int32 arrival counters [rows + requests].
-    tickets: Tensor
 
     @classmethod
     def resolve(
@@ -244,7 +239,6 @@ class TwoStageTiling:
         with torch.device(target):
 
             scratchpad = torch.empty(total_rows, vocabulary.blocks * k, dtype=I32).view(U32)
-            tickets = torch.zeros(total_rows + batch_size, dtype=I32)
 
             values = indices = None
 
@@ -259,7 +253,6 @@ class TwoStageTiling:
             vocabulary=vocabulary,
             scratchpad=scratchpad,
             dispatch=dispatch,
-            tickets=tickets,
         )
 
         return instance, values, indices
@@ -290,8 +283,3 @@ class TwoStageTiling:
                 k_strategy = k_strategy or TopKStrategy.resolve(best)
 
         return config or TwoStageWarpConfig.default(), k_strategy or TopKStrategy(), block_size
-
-    def reset(self) -> None:
-        """Re-zeroes the arrival counters (only needed if a launch was aborted mid-flight)."""
-
-        self.tickets.zero_()

@@ -60,19 +60,6 @@ def resolve_scratchpad(logits: Tensor, block_n: int, buffer: Optional[Tensor] = 
     return (rows, vocab_blocks), (rows,), scratchpad, vocab_blocks
 
 
-def resolve_tickets(buffer: Optional[Tensor], count: int, device) -> Tensor:
-
-    if buffer is None:
-
-        return torch.zeros(count, dtype=I32, device=device)
-
-    if buffer.dtype != I32 or buffer.numel() < count or not buffer.is_contiguous():
-
-        raise ValueError(f"tickets must be a contiguous int32 tensor of >= {count} zeroed entries")
-
-    return buffer
-
-
 def conditional_stride(*data: Optional[Tensor]) -> Optional[int]:
 
     for tensor in data:

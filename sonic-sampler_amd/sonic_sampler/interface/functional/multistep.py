@@ -2,13 +2,13 @@
 ``interface/functional/multistep.py:50-461``).
 
 ``fused_multistep`` keeps the reference's keyword set and layouts (fixed-gamma ``[B, gamma + 1, V]``
-logits, or varlen ``[sum_i (gamma_i + 1), V]`` logits with ``cu_seqlens``) and launches one HIP
-kernel (``ss_fused_multistep``) that runs the prologue, the per-row top-128 and truncation, and
-the per-request verification.
+logits, or varlen ``[sum_i (gamma_i + 1), V]`` logits with ``cu_seqlens``) and calls
+``ss_fused_multistep``, which launches the tile stage (prologue + tile top-128), the row stage
+(merge, truncation, softmax) and the request stage (chain verification) back to back.
 
 Additions to the reference's keywords (all optional): ``philox_seed`` / ``philox_offset`` (Gumbel
 noise from the Philox stream instead of ``gumbel_noise``; a fresh seed is drawn when neither is
-given) and ``tickets`` (zeroed int32 arrival counters, ``rows + B`` entries).
+given).
 
 ``values`` receives the truncated fp32 log-probabilities of each row's top-128 (the reference
 stores their exponentials); ``indices`` the matching token ids.
@@ -34,7 +34,6 @@ from sonic_sampler.interface.functional.base import (
     fresh_seed,
     philox,
     resolve_scratchpad,
-    resolve_tickets,
     unit_stride,
     validate_block,
     validate_count_update,
@@ -170,7 +169,6 @@ def fused_multistep(
     # Additions.
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
-    tickets: Optional[Tensor] = None,
 ) -> Verification:
 
     validate_count_update(update_counts, decode_counts)
@@ -249,8 +247,6 @@ def fused_multistep(
             top_values = collapse_2d(verification.logprobs.top_k.logprobs)
             top_tokens = collapse_2d(verification.logprobs.top_k.tokens)
 
-    ticket_buffer = resolve_tickets(tickets, rows + batch_size, logits.device)
-
     p = _native.ptr
     s = _native.stride0
 
@@ -286,7 +282,7 @@ def fused_multistep(
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         values=p(values_buffer), indices=p(indices_buffer),
         scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        tickets=p(ticket_buffer), stream=_native.stream_of(logits),
+        stream=_native.stream_of(logits),
     )
 
     _native.check(_native.load().ss_fused_multistep(ctypes.byref(args)), "ss_fused_multistep")

@@ -1,8 +1,8 @@
 """Functional single-step sampling (reference ``interface/functional/singular.py:38-322``).
 
-``fused_singular`` keeps the reference's keyword set and buffer semantics and launches one HIP
-kernel (``ss_fused_singular``): prologue + tile top-128 on every (row, tile) workgroup, merge and
-selection on the last workgroup of each row.
+``fused_singular`` keeps the reference's keyword set and buffer semantics and calls
+``ss_fused_singular``, which launches the tile stage (prologue + tile top-128 per (row, tile)
+workgroup) and the row stage (merge + selection per row) back to back.
 
 Additions to the reference's keywords (all optional):
 
@@ -13,7 +13,6 @@ Additions to the reference's keywords (all optional):
 * ``philox_seed`` / ``philox_offset`` / ``philox_step`` -- draw the Gumbel noise from the
   counter-based Philox stream instead of ``gumbel_noise``. With neither given, a fresh seed is drawn
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
-* ``tickets`` -- the int32 arrival counters (zeroed); allocated when omitted.
 """
 
 from __future__ import annotations
@@ -35,7 +34,6 @@ from sonic_sampler.interface.functional.base import (
     fresh_seed,
     philox,
     resolve_scratchpad,
-    resolve_tickets,
     unit_stride,
     validate_block,
     validate_count_update,
@@ -109,7 +107,6 @@ def fused_singular(
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
     philox_step: int = 0,
-    tickets: Optional[Tensor] = None,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
@@ -181,8 +178,6 @@ def fused_singular(
         history = timestep if timestep is not None else min(lookahead, drafted_tokens.size(1))
         history = max(0, min(history, drafted_tokens.size(1)))
 
-    ticket_buffer = resolve_tickets(tickets, batch_size, logits.device)
-
     p = _native.ptr
     s = _native.stride0
 
@@ -213,7 +208,7 @@ def fused_singular(
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         probabilities=p(probabilities), stride_probabilities=s(probabilities),
         scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        tickets=p(ticket_buffer), stream=_native.stream_of(logits),
+        stream=_native.stream_of(logits),
     )
 
     _native.check(_native.load().ss_fused_singular(ctypes.byref(args)), "ss_fused_singular")

@@ -70,7 +70,6 @@ class UnshardedFusedMultistep(TwoStageTiling):
             values=values,
             indices=indices,
             dispatch=factory.dispatch,
-            tickets=factory.tickets,
         )
 
     def tuning(self, size: int, strategy=None, tuning: Optional[ThreeStageWarpConfig] = None):
@@ -145,5 +144,4 @@ class UnshardedFusedMultistep(TwoStageTiling):
             warp_config=config,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
-            tickets=self.tickets,
         )

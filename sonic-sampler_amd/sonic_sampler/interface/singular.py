@@ -78,7 +78,6 @@ class UnshardedFusedSingular(TwoStageTiling):
             vocabulary=factory.vocabulary,
             scratchpad=factory.scratchpad,
             dispatch=factory.dispatch,
-            tickets=factory.tickets,
         )
 
     def autoregressive(
@@ -132,7 +131,6 @@ class UnshardedFusedSingular(TwoStageTiling):
             philox_seed=philox_seed,
             philox_offset=philox_offset,
             philox_step=0,
-            tickets=self.tickets,
         )
 
     def drafting(
@@ -196,5 +194,4 @@ class UnshardedFusedSingular(TwoStageTiling):
             philox_seed=philox_seed,
             philox_offset=philox_offset,
             philox_step=timestep,
-            tickets=self.tickets,
         )

@@ -85,7 +85,6 @@ class UnshardedBoundedTopK(TwoStageTiling):
             values=values,
             indices=indices,
             dispatch=factory.dispatch,
-            tickets=factory.tickets,
         )
 
         instance._wide = None
@@ -163,7 +162,7 @@ class UnshardedBoundedTopK(TwoStageTiling):
             logits=flat.data_ptr(), stride_logits=flat.stride(0), dtype=dtype, rows=n_rows,
             vocab_size=flat.size(-1), k=self.k, block_n=block_n, reserved=0,
             scratch=scratch.data_ptr(), stride_scratch=scratch.stride(0),
-            tickets=self.tickets.data_ptr(), values=values.data_ptr(),
+            values=values.data_ptr(),
             indices=self.indices.data_ptr(), stream=_native.stream_of(flat),
         )
 

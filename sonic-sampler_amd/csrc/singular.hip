@@ -28,6 +28,7 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
     rs.pres = (ind & IND_PRES) && a.presence ? bf2f(a.presence[slot]) : 0.0f;
     rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
     if (!a.temperature) rs.ind &= ~IND_TEMP;
+    rs.vt = a.target_vocab > 0 ? a.target_vocab : a.vocab_size;
     rs.nhist = 0;
     return rs;
 }

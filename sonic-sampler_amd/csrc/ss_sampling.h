@@ -40,6 +40,7 @@ struct RowState {
     const int32_t *dec;
     const uint16_t *bias;
     float rep, freq, pres, temp;
+    int vt;     // width of the counts / bias / grammar rows (target vocabulary)
     int nhist;  // drafted tokens of the history staged in SampleSmem::hist
 };
 
@@ -64,8 +65,8 @@ __device__ __forceinline__ void round_all(float (&x)[E]) {
     for (int j = 0; j < E; j += 2) round_pair(x[j], x[j + 1]);
 }
 
-// Divisor state of a per-row constant d: rcp = RN(1/d); `exact` is false when d is 0, infinite or
-// NaN, where the plain IEEE quotient is used instead.
+// Divisor state of a per-row constant d: rcp = RN(1/d); `fast` is false when d is 0, infinite
+// or NaN, where the plain IEEE quotient is used instead.
 struct Divisor {
     float d, rcp;
     bool fast;
@@ -79,17 +80,13 @@ __device__ __forceinline__ Divisor make_divisor(float d) {
     return v;
 }
 
-// bf16(x / d) for a bf16-exact x: q0 = x * RN(1/d) is within 2 ulp of x / d and one FMA
-// correction brings it within 0.5 ulp + 2^-24 ulp. Because x and d carry 8 significant bits,
-// x / d is either exactly representable (then the corrected quotient equals it) or at least
-// ~2^-17 (relative) away from every bf16 rounding boundary, so the bf16 rounding of the result is
-// that of the correctly rounded fp32 quotient, which is what torch's `div` computes.
-__device__ __forceinline__ float div_exact_bf16(float x, const Divisor &v) {
-    if (!v.fast) return x / v.d;
-    const float q0 = x * v.rcp;
-    const float r = __builtin_fmaf(-q0, v.d, x);
-    const float q1 = __builtin_fmaf(r, v.rcp, q0);
-    return __builtin_isinf(x) ? q0 : q1;
+// x / d for bf16 x and d, valid as the input of a bf16 rounding. Both carry 8 significant bits, so
+// x / d is either exact with at most 8 significant bits (a bf16 value) or at least 2^-17 (relative)
+// away from every bf16 rounding boundary, since a boundary needs 9 significant bits. x * RN(1/d)
+// is within 2^-23 of x / d, so its bf16 rounding equals that of torch's correctly rounded fp32
+// quotient.
+__device__ __forceinline__ float div_bf16(float x, const Divisor &v) {
+    return v.fast ? x * v.rcp : x / v.d;
 }
 
 // Order-preserving 16-bit key of a bf16-exact float (-0 folded onto +0).
@@ -99,6 +96,16 @@ __device__ __forceinline__ uint32_t key_of(float x) {
     return (u ^ flip) >> 16;
 }
 
+// Raw buffer view of one row: loads past `bytes` return 0 without faulting, so every load below is
+// unconditional. Descriptor word 3 for gfx9-family raw buffers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const void *p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                             0x00020000);
+}
+
+constexpr int NT = 2;  // non-temporal: each plane is read once
+
 // Streams one tile of one row through the processor chain and returns the keys (0 = absent).
 // The chain runs processor by processor over all E elements, so every indicator test is a
 // uniform branch taken once per tile, and each processor ends with one packed bf16 rounding --
@@ -106,8 +113,8 @@ __device__ __forceinline__ uint32_t key_of(float x) {
 // multiplicative penalty (x < 0 ? x * r : x / r where context + decode counts > 0), frequency
 // penalty x - bf16(count) * f (one rounding, as torch's addcmul), presence penalty, logit bias,
 // temperature.
-// VEC: vocabulary and every row base are 4-element aligned, so a 4-column chunk is either fully
-// inside the vocabulary or fully outside, and planes load as 8 / 16-byte vectors.
+// VEC: the vocabulary is a multiple of 4 and every row base is aligned for 8 / 16-byte vector
+// loads, so a 4-column chunk is either fully inside the vocabulary or fully outside.
 template <int E, bool VEC>
 __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
                                               const int32_t *hist, uint32_t (&keys)[E]) {
@@ -119,27 +126,30 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     const bool use_bias = (ind & IND_BIAS) && rs.bias;
     const bool remap = rs.d2t != nullptr && (use_g || use_rep || use_bias);
     const bool direct = VEC && !remap;
+    const int lane4 = (int)threadIdx.x * 4;  // column offset of this thread inside a chunk
 
     float x[E];
     bool ok[E];
+    const __amdgpu_buffer_rsrc_t lg = row_buffer(rs.logits, (int64_t)V * 2);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int col = col0 + tile_col(4 * c);
+        const int base = col0 + c * (SS_BLOCK * 4);  // uniform
         if (VEC) {
-            const bool in = col < V;
-            const u32x2 w = in ? __builtin_nontemporal_load((const u32x2 *)(rs.logits + col))
-                               : u32x2{0u, 0u};
+            const u32x2 w = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(lg, lane4 * 2, base * 2, NT));
             x[4 * c + 0] = __uint_as_float(w.x << 16);
             x[4 * c + 1] = __uint_as_float(w.x & 0xffff0000u);
             x[4 * c + 2] = __uint_as_float(w.y << 16);
             x[4 * c + 3] = __uint_as_float(w.y & 0xffff0000u);
+            const bool in = base + lane4 < V;
 #pragma unroll
             for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                ok[4 * c + i] = col + i < V;
-                x[4 * c + i] = ok[4 * c + i] ? bf2f(rs.logits[col + i]) : 0.0f;
+                const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(lg, (lane4 + i) * 2, base * 2, NT);
+                x[4 * c + i] = __uint_as_float(h << 16);
+                ok[4 * c + i] = base + lane4 + i < V;
             }
         }
     }
@@ -149,33 +159,41 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
 #pragma unroll
         for (int j = 0; j < E; ++j) tcol[j] = col0 + tile_col(j);
         if (remap) {
+            const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)V * 4);
 #pragma unroll
-            for (int j = 0; j < E; ++j) tcol[j] = ok[j] ? rs.d2t[tcol[j]] : 0;
+            for (int j = 0; j < E; ++j) tcol[j] = __builtin_amdgcn_raw_buffer_load_b32(m, tcol[j] * 4, 0, 0);
         }
         if (use_g) {
+            const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
 #pragma unroll
             for (int j = 0; j < E; ++j) {
                 uint32_t w;
                 if (direct) {
-                    w = ok[j] ? rs.grammar[(col0 + tile_col(j & ~3)) >> 5] : 0xffffffffu;
+                    // the four columns of a chunk share one 32-bit word
+                    w = (j & 3) ? keys[j & ~3]
+                                : __builtin_amdgcn_raw_buffer_load_b32(
+                                      g, ((col0 + tile_col(j)) >> 5) * 4, 0, 0);
+                    keys[j] = w;  // keys[] doubles as the word cache until the keys are formed
                 } else {
-                    w = ok[j] ? rs.grammar[tcol[j] >> 5] : 0xffffffffu;
+                    w = __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
                 }
                 x[j] = ((w >> (tcol[j] & 31)) & 1u) ? x[j] : -INFINITY;
             }
         }
         if (use_rep) {
             int32_t dec[E];
+            const __amdgpu_buffer_rsrc_t d = row_buffer(rs.dec, (int64_t)rs.vt * 4);
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const int col = col0 + tile_col(4 * c);
+                const int base = col0 + c * (SS_BLOCK * 4);
                 if (direct) {
-                    const i32x4 d = ok[4 * c] ? __builtin_nontemporal_load((const i32x4 *)(rs.dec + col))
-                                              : i32x4{0, 0, 0, 0};
-                    dec[4 * c + 0] = d.x; dec[4 * c + 1] = d.y; dec[4 * c + 2] = d.z; dec[4 * c + 3] = d.w;
+                    const i32x4 q = __builtin_bit_cast(
+                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(d, lane4 * 4, base * 4, NT));
+                    dec[4 * c + 0] = q.x; dec[4 * c + 1] = q.y; dec[4 * c + 2] = q.z; dec[4 * c + 3] = q.w;
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) dec[4 * c + i] = ok[4 * c + i] ? rs.dec[tcol[4 * c + i]] : 0;
+                    for (int i = 0; i < 4; ++i)
+                        dec[4 * c + i] = __builtin_amdgcn_raw_buffer_load_b32(d, tcol[4 * c + i] * 4, 0, 0);
                 }
             }
             if (rs.nhist > 0) {
@@ -189,22 +207,24 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             }
             if (use_mult) {
                 const Divisor rep = make_divisor(rs.rep);
+                const __amdgpu_buffer_rsrc_t q = row_buffer(rs.ctx, (int64_t)rs.vt * 4);
 #pragma unroll
                 for (int c = 0; c < NCH; ++c) {
                     int32_t ctx[4];
-                    const int col = col0 + tile_col(4 * c);
+                    const int base = col0 + c * (SS_BLOCK * 4);
                     if (direct) {
-                        const i32x4 q = ok[4 * c] ? __builtin_nontemporal_load((const i32x4 *)(rs.ctx + col))
-                                                  : i32x4{0, 0, 0, 0};
-                        ctx[0] = q.x; ctx[1] = q.y; ctx[2] = q.z; ctx[3] = q.w;
+                        const i32x4 v = __builtin_bit_cast(
+                            i32x4, __builtin_amdgcn_raw_buffer_load_b128(q, lane4 * 4, base * 4, NT));
+                        ctx[0] = v.x; ctx[1] = v.y; ctx[2] = v.z; ctx[3] = v.w;
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) ctx[i] = ok[4 * c + i] ? rs.ctx[tcol[4 * c + i]] : 0;
+                        for (int i = 0; i < 4; ++i)
+                            ctx[i] = __builtin_amdgcn_raw_buffer_load_b32(q, tcol[4 * c + i] * 4, 0, 0);
                     }
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int j = 4 * c + i;
-                        const float y = x[j] < 0.0f ? x[j] * rs.rep : div_exact_bf16(x[j], rep);
+                        const float y = x[j] < 0.0f ? x[j] * rs.rep : div_bf16(x[j], rep);
                         x[j] = (dec[j] + ctx[i] > 0) ? y : x[j];
                     }
                 }
@@ -226,20 +246,23 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             }
         }
         if (use_bias) {
+            const __amdgpu_buffer_rsrc_t b = row_buffer(rs.bias, (int64_t)rs.vt * 2);
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const int col = col0 + tile_col(4 * c);
+                const int base = col0 + c * (SS_BLOCK * 4);
                 if (direct) {
-                    const u32x2 b = ok[4 * c] ? __builtin_nontemporal_load((const u32x2 *)(rs.bias + col))
-                                              : u32x2{0u, 0u};
-                    x[4 * c + 0] += __uint_as_float(b.x << 16);
-                    x[4 * c + 1] += __uint_as_float(b.x & 0xffff0000u);
-                    x[4 * c + 2] += __uint_as_float(b.y << 16);
-                    x[4 * c + 3] += __uint_as_float(b.y & 0xffff0000u);
+                    const u32x2 w = __builtin_bit_cast(
+                        u32x2, __builtin_amdgcn_raw_buffer_load_b64(b, lane4 * 2, base * 2, NT));
+                    x[4 * c + 0] += __uint_as_float(w.x << 16);
+                    x[4 * c + 1] += __uint_as_float(w.x & 0xffff0000u);
+                    x[4 * c + 2] += __uint_as_float(w.y << 16);
+                    x[4 * c + 3] += __uint_as_float(w.y & 0xffff0000u);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        x[4 * c + i] += ok[4 * c + i] ? bf2f(rs.bias[tcol[4 * c + i]]) : 0.0f;
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[4 * c + i] * 2, 0, 0);
+                        x[4 * c + i] += __uint_as_float(h << 16);
+                    }
                 }
             }
             round_all(x);
@@ -248,7 +271,7 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     if (ind & IND_TEMP) {
         const Divisor t = make_divisor(rs.temp);
 #pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = div_exact_bf16(x[j], t);
+        for (int j = 0; j < E; ++j) x[j] = div_bf16(x[j], t);
         round_all(x);
     }
 #pragma unroll

@@ -1,9 +1,13 @@
-"""The kernels' division x / d (reciprocal + one FMA correction) rounds to the same bf16 as torch's
-IEEE fp32 division for bf16 operands -- the claim that lets the prologue avoid full IEEE divides.
+"""The kernels' division x / d = x * RN(1/d) rounds to the same bf16 as torch's IEEE fp32 division
+for bf16 operands -- the claim that lets the prologue replace every per-element divide by one
+multiply (the reciprocal is computed once per row).
 
-The device formula is restated here in exact rational arithmetic (every fp32 operation rounded
-once, FMA rounded once) and compared with torch's fp32 division followed by the bf16 cast, the
-reference's `logits / scales` and `logits.div_(temperature)` (core/naive.py:218, :266).
+Why it holds: x and d carry 8 significant bits, so x / d is either exact with at most 8 bits (a bf16
+value) or at least 2^-17 (relative) away from every bf16 rounding boundary (a boundary needs 9
+bits); x * RN(1/d) is within 2^-23 of x / d. The device formula is restated here in exact rational
+arithmetic (every fp32 operation rounded once) and compared with torch's fp32 division followed by
+the bf16 cast, the reference's `logits / scales` and `logits.div_(temperature)`
+(core/naive.py:218, :266).
 """
 
 from __future__ import annotations
@@ -31,11 +35,8 @@ def rn32(value: Fraction) -> float:
 def kernel_div(x: float, d: float) -> float:
 
     rcp = rn32(Fraction(1) / Fraction(d))
-    q0 = rn32(Fraction(x) * Fraction(rcp))
-    r = rn32(Fraction(x) - Fraction(q0) * Fraction(d))
-    q1 = rn32(Fraction(r) * Fraction(rcp) + Fraction(q0))
 
-    return q1
+    return rn32(Fraction(x) * Fraction(rcp))
 
 
 def bf16(v: float) -> float:
@@ -61,7 +62,7 @@ def test_random_operands():
 
     rng = random.Random(0)
 
-    for _ in range(6000):
+    for _ in range(20000):
 
         x = random_bf16(rng, -20, 20)
         d = abs(random_bf16(rng, -6, 6))
@@ -75,7 +76,7 @@ def test_quotients_near_bf16_midpoints():
 
     rng = random.Random(1)
 
-    for _ in range(4000):
+    for _ in range(20000):
 
         d = abs(random_bf16(rng, -3, 3))
         m = (2 * rng.randrange(128, 256) + 1) * 2.0 ** (rng.randrange(-8, 8) - 8)   # 9-bit odd

@@ -1,10 +1,12 @@
 """Benchmark of the fused sampling / verification path on one MI355X.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]`` prints one JSON line with the
-headline metric of BASELINE.json: fused decode-sample microseconds per step and achieved HBM GB/s
-at B=64, V=128256 bf16 (config 1, ``UnshardedFusedSingular.autoregressive``), plus ``roofline``
-(measured live with HIP events on the launch stream) and ``cpu_baseline`` (the CPU restatement of
-the reference's PyTorch path from ``oracle/``, timed on a bounded sample of the same workload).
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints one JSON line with the headline
+metric: fused decode-sample microseconds per step and achieved HBM GB/s at B=64, V=128256 bf16
+(config 1, ``UnshardedFusedSingular.autoregressive``), plus ``roofline`` for the dominant kernel
+(the tile kernel, timed live with HIP events on the launch stream; HBM traffic per launch from the
+committed FETCH_SIZE / WRITE_SIZE summary in ``profiles/``) and ``cpu_baseline`` (the CPU
+restatement of the reference's PyTorch path from ``oracle/``, timed on a bounded sample of the
+same workload).
 
 The module also defines the synthetic workloads of all five configurations; the parity tests
 import them. Logits follow one generator: x ~ N(0, 3^2) plus 1-16 spikes of U[10, 20] per row,
@@ -303,6 +305,49 @@ def c1_algorithmic_bytes(batch: int, vocab: int, top_logprobs: int = 5) -> int:
     return streamed + gathers + outputs
 
 
+def c1_tile_bytes(batch: int, vocab: int) -> int:
+    """Algorithmic HBM bytes of one tile-kernel launch at config 1: every element's logit,
+    context count, decode count and bias, read once."""
+
+    return batch * vocab * C1_BYTES_PER_ELEMENT
+
+
+TILE_KERNEL = "singular_tiles_kernel<16, true>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "singular_tiles_c1_traffic.txt"
+
+
+def measured_traffic(kernel: str, batch: int, vocab: int) -> Optional[int]:
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE / WRITE_SIZE summary
+    (counter KiB scaled by the copy-kernel calibration factor), or None when the summary is absent
+    or was taken on another workload."""
+
+    if not TRAFFIC_SUMMARY.exists():
+
+        return None
+
+    fields = {}
+
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+
+        key, sep, value = line.partition(":")
+
+        if sep and key.strip() and not key.startswith("#"):
+
+            fields[key.strip()] = value.strip()
+
+    try:
+
+        if fields["kernel"] != kernel or int(fields["rows"]) != batch or int(fields["vocab"]) != vocab:
+
+            return None
+
+        return int(fields["traffic_bytes_per_launch"])
+
+    except (KeyError, ValueError):
+
+        return None
+
+
 def cpu_baseline_c1(workload: SingularWorkload, rows: int) -> dict:
     """The CPU restatement of the reference's PyTorch path on `rows` rows of config 1."""
 
@@ -340,13 +385,14 @@ def cpu_baseline_c1(workload: SingularWorkload, rows: int) -> dict:
 
 def _queue_behind_sleep(ms: float = 60.0) -> None:
     """Keeps the GPU busy while the host enqueues the timed launches, so that they run back to
-    back and each event pair brackets exactly one kernel."""
+    back and each event pair brackets exactly the launches between its two records."""
 
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
 def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox: bool = True) -> dict:
 
+    from sonic_sampler import _native
     from sonic_sampler.interface import UnshardedFusedSingular
 
     device = torch.device("cuda:0")
@@ -365,12 +411,13 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
-    def step(i: int):
+    def step(i: int, stage_event=None):
 
         logits, buffers = inputs[i % sets]
 
         return sampler.autoregressive(logits, buffers, update_counts=True, logprobs=True,
-                                      philox_seed=1234 if philox else None, philox_offset=i)
+                                      philox_seed=1234 if philox else None, philox_offset=i,
+                                      stage_event=stage_event)
 
     for i in range(warmup):
 
@@ -378,22 +425,31 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
 
     torch.cuda.synchronize()
 
-    # Eager launches: per-launch kernel time from event pairs on the launch stream.
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+    # Eager launches queued back to back: per-step time from event pairs on the launch stream,
+    # and the tile kernel's own time from the event the library records between its launches.
+    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+
+    for _, mid, _ in events:
+
+        _native.event_handle(mid)
+
+    torch.cuda.synchronize()
     _queue_behind_sleep(max(60.0, steps * 0.3))
     wall0 = time.perf_counter()
 
     for i in range(steps):
 
         events[i][0].record(stream)
-        step(i)
-        events[i][1].record(stream)
+        step(i, events[i][1])
+        events[i][2].record(stream)
 
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    launch_us = [a.elapsed_time(b) * 1e3 for a, b in events]
+    launch_us = [a.elapsed_time(c) * 1e3 for a, _, c in events]
+    tile_us = [a.elapsed_time(b) * 1e3 for a, b, _ in events]
+    row_us = [b.elapsed_time(c) * 1e3 for _, b, c in events]
     kernel_us = statistics.mean(launch_us)
+    tile_kernel_us = statistics.mean(tile_us)
 
     # hipGraph replays (one captured step per input set), back to back.
     graphs = []
@@ -426,7 +482,9 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     graph_us = start.elapsed_time(end) * 1e3 / steps
 
     algorithmic = c1_algorithmic_bytes(batch, vocab)
-    achieved = algorithmic / (kernel_us * 1e-6) / 1e9
+    tile_bytes = c1_tile_bytes(batch, vocab)
+    achieved = tile_bytes / (tile_kernel_us * 1e-6) / 1e9
+    traffic = measured_traffic(TILE_KERNEL, batch, vocab)
 
     result = {
         "metric": "fused decode-sample us/step + achieved HBM GB/s, B=64 V=128256 bf16",
@@ -444,24 +502,28 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
         "config": {
             "workload": "config 1: UnshardedFusedSingular.autoregressive B=64 V=128256 bf16, "
                         "penalties + bias + temperature + top-k/top-p/min-p + Gumbel-max, "
-                        "logprobs + top-5, update_counts; one kernel launch per step",
+                        "logprobs + top-5, update_counts; one tile launch + one row launch per step",
             "rows": batch,
             "vocab": vocab,
             "input_sets_rotated": sets,
             "algorithmic_bytes_per_step": algorithmic,
-            "achieved_hbm_gbs": round(achieved, 1),
+            "step_hbm_gbs": round(algorithmic / (kernel_us * 1e-6) / 1e9, 1),
             "rows_per_s": round(batch / (kernel_us * 1e-6), 1),
-            "median_kernel_us": round(statistics.median(launch_us), 3),
+            "median_step_us": round(statistics.median(launch_us), 3),
+            "tile_kernel_us": round(tile_kernel_us, 3),
+            "row_kernel_us": round(statistics.mean(row_us), 3),
             "graph_replay_us_per_step": round(graph_us, 3),
             "host_us_per_eager_call": round(wall * 1e6 / steps, 1),
         },
         "roofline": {
+            "kernel": TILE_KERNEL,
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "algorithmic_bytes": tile_bytes,
+            "traffic": traffic,
         },
     }
 
@@ -474,7 +536,8 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
 
 
 def copy_calibration(gib: float = 1.0, repeats: int = 5) -> None:
-    """A plain device copy of known size, to scale the FETCH_SIZE / WRITE_SIZE counters."""
+    """A plain elementwise device copy of known size (reads and writes `gib` GiB once each), to
+    scale the FETCH_SIZE / WRITE_SIZE counters."""
 
     n = int(gib * (1 << 30)) // 4
     src = torch.ones(n, dtype=torch.float32, device="cuda:0")
@@ -482,7 +545,7 @@ def copy_calibration(gib: float = 1.0, repeats: int = 5) -> None:
 
     for _ in range(repeats):
 
-        dst.copy_(src)
+        torch.mul(src, 1.0, out=dst)
 
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "repeats": repeats}))

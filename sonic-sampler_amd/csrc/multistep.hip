@@ -59,10 +59,14 @@ __device__ __forceinline__ RowState multistep_row_state(const ss_multistep_args 
     rs.ctx = a.context_counts ? a.context_counts + (int64_t)slot * a.stride_context : nullptr;
     rs.dec = a.decode_counts ? a.decode_counts + (int64_t)slot * a.stride_decode : nullptr;
     rs.bias = a.logit_bias ? a.logit_bias + (int64_t)slot * a.stride_bias : nullptr;
-    rs.rep = (ind & IND_MULT) && a.repetition ? bf2f(a.repetition[slot]) : 1.0f;
-    rs.freq = (ind & IND_FREQ) && a.frequency ? bf2f(a.frequency[slot]) : 0.0f;
-    rs.pres = (ind & IND_PRES) && a.presence ? bf2f(a.presence[slot]) : 0.0f;
-    rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
+    const float rep = param_bf16(a.repetition, a.indicators, slot, 1.0f);
+    const float freq = param_bf16(a.frequency, a.indicators, slot, 0.0f);
+    const float pres = param_bf16(a.presence, a.indicators, slot, 0.0f);
+    const float temp = param_bf16(a.temperature, a.indicators, slot, 1.0f);
+    rs.rep = (ind & IND_MULT) ? rep : 1.0f;
+    rs.freq = (ind & IND_FREQ) ? freq : 0.0f;
+    rs.pres = (ind & IND_PRES) ? pres : 0.0f;
+    rs.temp = (ind & IND_TEMP) ? temp : 1.0f;
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.vt = a.vocab_size;
     rs.nhist = 0;
@@ -77,16 +81,18 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
 }
 
 // Tile stage: grid rows * tiles.
-template <int E, bool VEC>
+template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x / tiles;
     const int tile = blockIdx.x - row * tiles;
+    u32x2 lw[E / 4];
+    if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
     const Request rq = resolve_request(a, row);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
     const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
-    const uint32_t ind = a.indicators[slot];
+    const uint32_t ind = uniform_u16(a.indicators, slot);
     RowState rs = multistep_row_state(a, row, step, slot, ind);
     if (step > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         // Step s of a request sees the drafts of steps < s as extra decode history
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
         __syncthreads();
     }
     uint32_t keys[E];
-    prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
+    prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
 }
 
@@ -268,18 +274,19 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
     }
 }
 
-template <bool VEC>
+template <int MODE>
 static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((multistep_tiles_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((multistep_tiles_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((multistep_tiles_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((multistep_tiles_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    if (a->stage_event && hipEventRecord((hipEvent_t)a->stage_event, s) != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, *a);
@@ -314,5 +321,6 @@ extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
                      aligned_ms(a->decode_counts, a->stride_decode, 16) &&
                      aligned_ms(a->context_counts, a->stride_context, 16) &&
                      aligned_ms(a->logit_bias, a->stride_bias, 8);
-    return vec ? launch_multistep<true>(a, tiles) : launch_multistep<false>(a, tiles);
+    if (!vec) return launch_multistep<MODE_SCALAR>(a, tiles);
+    return launch_multistep<MODE_DIRECT>(a, tiles);
 }

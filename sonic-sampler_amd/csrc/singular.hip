@@ -23,10 +23,14 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
     rs.ctx = a.context_counts ? a.context_counts + (int64_t)slot * a.stride_context : nullptr;
     rs.dec = a.decode_counts ? a.decode_counts + (int64_t)slot * a.stride_decode : nullptr;
     rs.bias = a.logit_bias ? a.logit_bias + (int64_t)slot * a.stride_bias : nullptr;
-    rs.rep = (ind & IND_MULT) && a.repetition ? bf2f(a.repetition[slot]) : 1.0f;
-    rs.freq = (ind & IND_FREQ) && a.frequency ? bf2f(a.frequency[slot]) : 0.0f;
-    rs.pres = (ind & IND_PRES) && a.presence ? bf2f(a.presence[slot]) : 0.0f;
-    rs.temp = (ind & IND_TEMP) && a.temperature ? bf2f(a.temperature[slot]) : 1.0f;
+    const float rep = param_bf16(a.repetition, a.indicators, slot, 1.0f);
+    const float freq = param_bf16(a.frequency, a.indicators, slot, 0.0f);
+    const float pres = param_bf16(a.presence, a.indicators, slot, 0.0f);
+    const float temp = param_bf16(a.temperature, a.indicators, slot, 1.0f);
+    rs.rep = (ind & IND_MULT) ? rep : 1.0f;
+    rs.freq = (ind & IND_FREQ) ? freq : 0.0f;
+    rs.pres = (ind & IND_PRES) ? pres : 0.0f;
+    rs.temp = (ind & IND_TEMP) ? temp : 1.0f;
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.vt = a.target_vocab > 0 ? a.target_vocab : a.vocab_size;
     rs.nhist = 0;
@@ -34,13 +38,15 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 }
 
 // Tile stage: grid rows * tiles.
-template <int E, bool VEC>
+template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x / tiles;
     const int tile = blockIdx.x - row * tiles;
+    u32x2 lw[E / 4];
+    if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
     const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
-    const uint32_t ind = a.indicators[slot];
+    const uint32_t ind = uniform_u16(a.indicators, slot);
     RowState rs = singular_row_state(a, row, slot, ind);
     if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         rs.nhist = a.timestep;
@@ -49,7 +55,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
         __syncthreads();
     }
     uint32_t keys[E];
-    prologue_keys<E, VEC>(rs, tile * a.block_n, a.vocab_size, sm.hist, keys);
+    prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
 }
 
@@ -148,18 +154,19 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
     if (lane == 0) a.tokens[(int64_t)row * a.stride_tokens] = token;
 }
 
-template <bool VEC>
+template <int MODE>
 static int launch_singular(const ss_singular_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((singular_tiles_kernel<4, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((singular_tiles_kernel<8, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((singular_tiles_kernel<16, VEC>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((singular_tiles_kernel<32, VEC>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((singular_tiles_kernel<4, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((singular_tiles_kernel<8, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((singular_tiles_kernel<16, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((singular_tiles_kernel<32, MODE>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    if (a->stage_event && hipEventRecord((hipEvent_t)a->stage_event, s) != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
@@ -193,5 +200,6 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
                      (!direct || (aligned(a->decode_counts, a->stride_decode, 16) &&
                                   aligned(a->context_counts, a->stride_context, 16) &&
                                   aligned(a->logit_bias, a->stride_bias, 8)));
-    return vec ? launch_singular<true>(a, tiles) : launch_singular<false>(a, tiles);
+    if (!vec) return launch_singular<MODE_SCALAR>(a, tiles);
+    return direct ? launch_singular<MODE_DIRECT>(a, tiles) : launch_singular<MODE_GATHER_VEC>(a, tiles);
 }

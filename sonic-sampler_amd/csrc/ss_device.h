@@ -30,19 +30,19 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
 // ---------------------------------------------------------------------------------------------
-// Order-preserving unsigned keys. A larger key means a larger value; -0 is folded onto +0 so that
-// equal values compare equal, as they do in torch's sort. Key 0 is never produced by a non-NaN
-// value and serves as the "absent element" sentinel.
-// ---------------------------------------------------------------------------------------------
+// Order-preserving unsigned keys. A larger key means a larger value, and -0 and +0 share a key,
+// so that equal values compare equal, as they do in torch's sort. 16-bit keys: a non-negative
+// bf16 h maps to h | 0x8000, a negative one to its 16-bit two's complement negation (-0 = 0x8000
+// lands on 0x8000 itself, the key of +0). Key 0 is never produced and serves as the "absent
+// element" sentinel.
 __device__ __forceinline__ uint32_t key16(uint32_t h) {
     h &= 0xffffu;
-    if ((h & 0x7fffu) == 0) h = 0;
-    return (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+    return (h & 0x8000u) ? ((0x10000u - h) & 0xffffu) : (h | 0x8000u);
 }
 
 __device__ __forceinline__ uint32_t unkey16(uint32_t k) {
     k &= 0xffffu;
-    return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+    return (k & 0x8000u) ? (k & 0x7fffu) : ((0x10000u - k) & 0xffffu);
 }
 
 __device__ __forceinline__ uint32_t key32(uint32_t u) {

@@ -89,12 +89,8 @@ __device__ __forceinline__ float div_bf16(float x, const Divisor &v) {
     return v.fast ? x * v.rcp : x / v.d;
 }
 
-// Order-preserving 16-bit key of a bf16-exact float (-0 folded onto +0).
-__device__ __forceinline__ uint32_t key_of(float x) {
-    const uint32_t u = __float_as_uint(x + 0.0f);
-    const uint32_t flip = (uint32_t)((int32_t)u >> 31) | 0x80000000u;
-    return (u ^ flip) >> 16;
-}
+// Order-preserving 16-bit key (key16) of a bf16-exact float.
+__device__ __forceinline__ uint32_t key_of(float x) { return key16(__float_as_uint(x) >> 16); }
 
 // Raw buffer view of one row: loads past `bytes` return 0 without faulting, so every load below is
 // unconditional. Descriptor word 3 for gfx9-family raw buffers.
@@ -106,27 +102,226 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(const void *p, int6
 
 constexpr int NT = 2;  // non-temporal: each plane is read once
 
-// Streams one tile of one row through the processor chain and returns the keys (0 = absent).
-// The chain runs processor by processor over all E elements, so every indicator test is a
-// uniform branch taken once per tile, and each processor ends with one packed bf16 rounding --
-// the rounding points of the reference's PyTorch path (core/naive.py:131-268): grammar mask,
-// multiplicative penalty (x < 0 ? x * r : x / r where context + decode counts > 0), frequency
-// penalty x - bf16(count) * f (one rounding, as torch's addcmul), presence penalty, logit bias,
-// temperature.
-// VEC: the vocabulary is a multiple of 4 and every row base is aligned for 8 / 16-byte vector
-// loads, so a 4-column chunk is either fully inside the vocabulary or fully outside.
-template <int E, bool VEC>
-__device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
-                                              const int32_t *hist, uint32_t (&keys)[E]) {
+typedef short s2v __attribute__((ext_vector_type(2)));
+typedef unsigned short u2v __attribute__((ext_vector_type(2)));
+
+// key16 of the two bf16 halves of `u` at once, with packed 16-bit integer operations.
+__device__ __forceinline__ uint32_t packed_keys(uint32_t u) {
+    const uint32_t m = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, u) >> (s2v){15, 15});
+    const uint32_t neg = __builtin_bit_cast(uint32_t, (u2v){0, 0} - __builtin_bit_cast(u2v, u));
+    return (neg & m) | ((u | 0x80008000u) & ~m);
+}
+
+// bf16 rounding of one value (round-to-nearest-even).
+__device__ __forceinline__ float rnd(float a) {
+    float b = a;
+    round_pair(a, b);
+    return a;
+}
+
+// Processor constants of one row, uniform over the workgroup.
+struct Chain {
+    bool mult, freq, pres, bias, temp;
+    float rep, fr, pr;
+    Divisor rdiv, tdiv;
+};
+
+// The whole processor chain on one element, rounding to bf16 after every processor as the
+// reference's PyTorch path does (core/naive.py:131-268): multiplicative penalty (x < 0 ? x * r :
+// x / r where context + decode counts > 0), frequency penalty x - bf16(count) * f (one rounding,
+// as torch's addcmul), presence penalty, logit bias, temperature.
+__device__ __forceinline__ float chain(const Chain &k, float x, int32_t dec, int32_t ctx, float b) {
+    if (k.mult && dec + ctx > 0) x = rnd(x < 0.0f ? x * k.rep : div_bf16(x, k.rdiv));
+    if (k.freq) x = rnd(__builtin_fmaf(-rnd((float)dec), k.fr, x));
+    if (k.pres) x = rnd(x - (dec > 0 ? k.pr : 0.0f));
+    if (k.bias) x = rnd(x + b);
+    if (k.temp) x = rnd(div_bf16(x, k.tdiv));
+    return x;
+}
+
+// Keys of E elements from their (grammar-masked) logits x, decode counts, context counts and
+// bias bits. Most elements of a row have zero counts and zero bias; for them every penalty and the
+// bias are the identity and the chain reduces to the temperature division, which runs for all
+// elements with one multiply each. Elements with a nonzero count or bias (or every element, when a
+// non-finite frequency penalty turns 0 * f into NaN) then run the full chain one element position
+// at a time, so a wave pays for it only at the positions where one of its lanes holds one.
+template <int E>
+__device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, const float (&x)[E],
+                                            const bool (&ok)[E], const int32_t (&dec)[E],
+                                            const int32_t (&ctx)[E], const uint32_t (&bb)[E],
+                                            uint32_t (&keys)[E]) {
+#pragma unroll
+    for (int j = 0; j < E; j += 2) {
+        float y0 = x[j], y1 = x[j + 1];
+        if (k.temp) {
+            y0 = div_bf16(y0, k.tdiv);
+            y1 = div_bf16(y1, k.tdiv);
+        }
+        const f2v v = {y0, y1};
+        const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
+        keys[j] = ok[j] ? (kk & 0xffffu) : 0u;
+        keys[j + 1] = ok[j + 1] ? (kk >> 16) : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
+        if (exc && ok[j]) keys[j] = key_of(chain(k, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
+    }
+}
+
+// Processor flags of one row.
+struct Uses {
+    bool g, rep, mult, bias, remap;
+};
+
+__device__ __forceinline__ Uses row_uses(const RowState &rs) {
+    Uses u;
+    u.g = (rs.ind & IND_GRAMMAR) && rs.grammar;
+    u.rep = (rs.ind & (IND_MULT | IND_FREQ | IND_PRES)) && rs.dec;
+    u.mult = u.rep && (rs.ind & IND_MULT) && rs.ctx;
+    u.bias = (rs.ind & IND_BIAS) && rs.bias;
+    u.remap = rs.d2t != nullptr && (u.g || u.rep || u.bias);
+    return u;
+}
+
+__device__ __forceinline__ Chain row_chain(const RowState &rs, const Uses &u, bool &all_exc) {
+    Chain k;
+    k.mult = u.mult;
+    k.freq = u.rep && (rs.ind & IND_FREQ);
+    k.pres = u.rep && (rs.ind & IND_PRES);
+    k.bias = u.bias;
+    k.temp = (rs.ind & IND_TEMP) != 0;
+    k.rep = rs.rep;
+    k.fr = rs.freq;
+    k.pr = rs.pres;
+    k.rdiv = make_divisor(rs.rep);
+    k.tdiv = make_divisor(rs.temp);
+    all_exc = k.freq && !__builtin_isfinite(rs.freq);
+    return k;
+}
+
+// The logits of one tile as 4-column words (VEC layout). They depend on the row only, so the
+// kernels issue them first, before the request state that decides how the other planes are read.
+template <int E>
+__device__ __forceinline__ void load_logits_vec(const uint16_t *lrow, int col0, int V,
+                                                u32x2 (&lw)[E / 4]) {
+    const __amdgpu_buffer_rsrc_t lg = row_buffer(lrow, (int64_t)V * 2);
+    const int lane4 = (int)threadIdx.x * 4;
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c)
+        lw[c] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(lg, lane4 * 2, (col0 + c * (SS_BLOCK * 4)) * 2, NT));
+}
+
+// Reads at workgroup-uniform addresses through the constant address space, which the compiler
+// serves with scalar loads: they wait on the scalar counter, never on the vector loads already in
+// flight. Only for data no kernel of the launch writes.
+typedef const __attribute__((address_space(4))) uint32_t *const_u32p;
+
+__device__ __forceinline__ int32_t uniform_i32(const int32_t *p, int idx) {
+    return (int32_t)*(const_u32p)(uintptr_t)(p + idx);
+}
+
+// p[idx] of a 16-bit array, read as the aligned dword holding it (a dword never crosses a page,
+// so the 2 bytes beside the element are always mapped).
+__device__ __forceinline__ uint32_t uniform_u16(const uint16_t *p, int idx) {
+    const uintptr_t addr = (uintptr_t)(p + idx);
+    const uint32_t w = *(const_u32p)(addr & ~(uintptr_t)3);
+    return (addr & 2) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Per-request bf16 parameter p[slot] as fp32, or `dflt` when p is NULL. `any` is a valid array of
+// the same length, read instead of a NULL p so that the reads of a request issue unbranched.
+__device__ __forceinline__ float param_bf16(const uint16_t *p, const uint16_t *any, int slot,
+                                            float dflt) {
+    const uint32_t h = uniform_u16(p ? p : any, slot);
+    return p ? bf2f(h) : dflt;
+}
+
+// Direct layout (no d2t remap, vocabulary a multiple of 4, 8 / 16-byte aligned rows): the side
+// planes of one tile -- grammar words, decode and context counts, bias -- as loaded words.
+template <int E>
+struct Planes {
+    u32x2 bw[E / 4];
+    i32x4 dw[E / 4], cw[E / 4];
+    uint32_t gw[E / 4];
+};
+
+// Issues every side-plane load of the tile before any loaded word is consumed. A plane that is
+// off reads through an empty buffer, which returns zeros without touching memory.
+template <int E>
+__device__ __forceinline__ void issue_planes(const RowState &rs, const Uses &u, bool on, int col0,
+                                             Planes<E> &pl) {
+    const int lane4 = (int)threadIdx.x * 4;
+    const bool g = on && u.g, rep = on && u.rep, mult = on && u.mult, bias = on && u.bias;
+    const __amdgpu_buffer_rsrc_t gb =
+        row_buffer(g ? rs.grammar : nullptr, g ? (int64_t)((rs.vt + 31) >> 5) * 4 : 0);
+    const __amdgpu_buffer_rsrc_t db = row_buffer(rep ? rs.dec : nullptr, rep ? (int64_t)rs.vt * 4 : 0);
+    const __amdgpu_buffer_rsrc_t cb = row_buffer(mult ? rs.ctx : nullptr, mult ? (int64_t)rs.vt * 4 : 0);
+    const __amdgpu_buffer_rsrc_t bb = row_buffer(bias ? rs.bias : nullptr, bias ? (int64_t)rs.vt * 2 : 0);
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        const int base = col0 + c * (SS_BLOCK * 4);  // uniform, a multiple of 32
+        pl.dw[c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(db, lane4 * 4, base * 4, NT));
+        pl.cw[c] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(cb, lane4 * 4, base * 4, NT));
+        pl.bw[c] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(bb, lane4 * 2, base * 2, NT));
+        pl.gw[c] = __builtin_amdgcn_raw_buffer_load_b32(gb, (lane4 >> 5) * 4, (base >> 5) * 4, 0);
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, int col0, int V,
+                                            const int32_t *hist, const u32x2 (&lw)[E / 4],
+                                            const Planes<E> &pl, uint32_t (&keys)[E]) {
     constexpr int NCH = E / 4;
-    const uint32_t ind = rs.ind;
-    const bool use_g = (ind & IND_GRAMMAR) && rs.grammar;
-    const bool use_rep = (ind & (IND_MULT | IND_FREQ | IND_PRES)) && rs.dec;
-    const bool use_mult = use_rep && (ind & IND_MULT) && rs.ctx;
-    const bool use_bias = (ind & IND_BIAS) && rs.bias;
-    const bool remap = rs.d2t != nullptr && (use_g || use_rep || use_bias);
-    const bool direct = VEC && !remap;
-    const int lane4 = (int)threadIdx.x * 4;  // column offset of this thread inside a chunk
+    const int lane4 = (int)threadIdx.x * 4;
+    bool all_exc;
+    const Chain k = row_chain(rs, u, all_exc);
+    float x[E];
+    bool ok[E];
+    int32_t dec[E], ctx[E];
+    uint32_t bbits[E];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int base = col0 + c * (SS_BLOCK * 4);
+        const bool in = base + lane4 < V;
+        x[4 * c + 0] = __uint_as_float(lw[c].x << 16);
+        x[4 * c + 1] = __uint_as_float(lw[c].x & 0xffff0000u);
+        x[4 * c + 2] = __uint_as_float(lw[c].y << 16);
+        x[4 * c + 3] = __uint_as_float(lw[c].y & 0xffff0000u);
+        dec[4 * c + 0] = pl.dw[c].x; dec[4 * c + 1] = pl.dw[c].y; dec[4 * c + 2] = pl.dw[c].z; dec[4 * c + 3] = pl.dw[c].w;
+        ctx[4 * c + 0] = pl.cw[c].x; ctx[4 * c + 1] = pl.cw[c].y; ctx[4 * c + 2] = pl.cw[c].z; ctx[4 * c + 3] = pl.cw[c].w;
+        bbits[4 * c + 0] = pl.bw[c].x << 16;
+        bbits[4 * c + 1] = pl.bw[c].x & 0xffff0000u;
+        bbits[4 * c + 2] = pl.bw[c].y << 16;
+        bbits[4 * c + 3] = pl.bw[c].y & 0xffff0000u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ok[4 * c + i] = in;
+            if (u.g && !((pl.gw[c] >> ((lane4 & 31) + i)) & 1u)) x[4 * c + i] = -INFINITY;
+        }
+    }
+    if (u.rep && rs.nhist > 0) {
+        // The history never counts token 0: the reference pads the history with 0 and then
+        // restores the original count of token 0 (core/naive.py:179-203).
+        for (int h = 0; h < rs.nhist; ++h) {
+            const int t = hist[h];
+#pragma unroll
+            for (int j = 0; j < E; ++j) dec[j] += (col0 + tile_col(j) == t && t != 0) ? 1 : 0;
+        }
+    }
+    finish_keys<E>(k, all_exc, x, ok, dec, ctx, bbits, keys);
+}
+
+// General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
+template <int E, bool VEC>
+__device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, int col0, int V,
+                                            const int32_t *hist, const u32x2 (&lw)[E / 4],
+                                            uint32_t (&keys)[E]) {
+    constexpr int NCH = E / 4;
+    const int lane4 = (int)threadIdx.x * 4;
+    bool all_exc;
+    const Chain k = row_chain(rs, u, all_exc);
 
     float x[E];
     bool ok[E];
@@ -135,8 +330,7 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     for (int c = 0; c < NCH; ++c) {
         const int base = col0 + c * (SS_BLOCK * 4);  // uniform
         if (VEC) {
-            const u32x2 w = __builtin_bit_cast(
-                u32x2, __builtin_amdgcn_raw_buffer_load_b64(lg, lane4 * 2, base * 2, NT));
+            const u32x2 w = lw[c];
             x[4 * c + 0] = __uint_as_float(w.x << 16);
             x[4 * c + 1] = __uint_as_float(w.x & 0xffff0000u);
             x[4 * c + 2] = __uint_as_float(w.y << 16);
@@ -154,128 +348,80 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
         }
     }
 
-    if (use_g || use_rep || use_bias) {
+    int32_t dec[E], ctx[E];
+    uint32_t bbits[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        dec[j] = 0;
+        ctx[j] = 0;
+        bbits[j] = 0;
+    }
+    if (u.g || u.rep || u.bias) {
         int tcol[E];
 #pragma unroll
         for (int j = 0; j < E; ++j) tcol[j] = col0 + tile_col(j);
-        if (remap) {
+        if (u.remap) {
             const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)V * 4);
 #pragma unroll
             for (int j = 0; j < E; ++j) tcol[j] = __builtin_amdgcn_raw_buffer_load_b32(m, tcol[j] * 4, 0, 0);
         }
-        if (use_g) {
+        if (u.g) {
             const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
 #pragma unroll
             for (int j = 0; j < E; ++j) {
-                uint32_t w;
-                if (direct) {
-                    // the four columns of a chunk share one 32-bit word
-                    w = (j & 3) ? keys[j & ~3]
-                                : __builtin_amdgcn_raw_buffer_load_b32(
-                                      g, ((col0 + tile_col(j)) >> 5) * 4, 0, 0);
-                    keys[j] = w;  // keys[] doubles as the word cache until the keys are formed
-                } else {
-                    w = __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
-                }
+                const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
                 x[j] = ((w >> (tcol[j] & 31)) & 1u) ? x[j] : -INFINITY;
             }
         }
-        if (use_rep) {
-            int32_t dec[E];
+        if (u.rep) {
             const __amdgpu_buffer_rsrc_t d = row_buffer(rs.dec, (int64_t)rs.vt * 4);
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int base = col0 + c * (SS_BLOCK * 4);
-                if (direct) {
-                    const i32x4 q = __builtin_bit_cast(
-                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(d, lane4 * 4, base * 4, NT));
-                    dec[4 * c + 0] = q.x; dec[4 * c + 1] = q.y; dec[4 * c + 2] = q.z; dec[4 * c + 3] = q.w;
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        dec[4 * c + i] = __builtin_amdgcn_raw_buffer_load_b32(d, tcol[4 * c + i] * 4, 0, 0);
-                }
-            }
+            for (int j = 0; j < E; ++j) dec[j] = __builtin_amdgcn_raw_buffer_load_b32(d, tcol[j] * 4, 0, 0);
             if (rs.nhist > 0) {
-                // The history never counts token 0: the reference pads the history with 0 and then
-                // restores the original count of token 0 (core/naive.py:179-203).
+                // The history never counts token 0 (core/naive.py:179-203).
                 for (int h = 0; h < rs.nhist; ++h) {
                     const int t = hist[h];
 #pragma unroll
                     for (int j = 0; j < E; ++j) dec[j] += (tcol[j] == t && t != 0) ? 1 : 0;
                 }
             }
-            if (use_mult) {
-                const Divisor rep = make_divisor(rs.rep);
-                const __amdgpu_buffer_rsrc_t q = row_buffer(rs.ctx, (int64_t)rs.vt * 4);
-#pragma unroll
-                for (int c = 0; c < NCH; ++c) {
-                    int32_t ctx[4];
-                    const int base = col0 + c * (SS_BLOCK * 4);
-                    if (direct) {
-                        const i32x4 v = __builtin_bit_cast(
-                            i32x4, __builtin_amdgcn_raw_buffer_load_b128(q, lane4 * 4, base * 4, NT));
-                        ctx[0] = v.x; ctx[1] = v.y; ctx[2] = v.z; ctx[3] = v.w;
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            ctx[i] = __builtin_amdgcn_raw_buffer_load_b32(q, tcol[4 * c + i] * 4, 0, 0);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int j = 4 * c + i;
-                        const float y = x[j] < 0.0f ? x[j] * rs.rep : div_bf16(x[j], rep);
-                        x[j] = (dec[j] + ctx[i] > 0) ? y : x[j];
-                    }
-                }
-                round_all(x);
-            }
-            if (ind & IND_FREQ) {
-                float cnt[E];
-#pragma unroll
-                for (int j = 0; j < E; ++j) cnt[j] = (float)dec[j];
-                round_all(cnt);
-#pragma unroll
-                for (int j = 0; j < E; ++j) x[j] = __builtin_fmaf(-cnt[j], rs.freq, x[j]);
-                round_all(x);
-            }
-            if (ind & IND_PRES) {
-#pragma unroll
-                for (int j = 0; j < E; ++j) x[j] = x[j] - (dec[j] > 0 ? rs.pres : 0.0f);
-                round_all(x);
-            }
         }
-        if (use_bias) {
+        if (u.mult) {
+            const __amdgpu_buffer_rsrc_t q = row_buffer(rs.ctx, (int64_t)rs.vt * 4);
+#pragma unroll
+            for (int j = 0; j < E; ++j) ctx[j] = __builtin_amdgcn_raw_buffer_load_b32(q, tcol[j] * 4, 0, 0);
+        }
+        if (u.bias) {
             const __amdgpu_buffer_rsrc_t b = row_buffer(rs.bias, (int64_t)rs.vt * 2);
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int base = col0 + c * (SS_BLOCK * 4);
-                if (direct) {
-                    const u32x2 w = __builtin_bit_cast(
-                        u32x2, __builtin_amdgcn_raw_buffer_load_b64(b, lane4 * 2, base * 2, NT));
-                    x[4 * c + 0] += __uint_as_float(w.x << 16);
-                    x[4 * c + 1] += __uint_as_float(w.x & 0xffff0000u);
-                    x[4 * c + 2] += __uint_as_float(w.y << 16);
-                    x[4 * c + 3] += __uint_as_float(w.y & 0xffff0000u);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[4 * c + i] * 2, 0, 0);
-                        x[4 * c + i] += __uint_as_float(h << 16);
-                    }
-                }
-            }
-            round_all(x);
+            for (int j = 0; j < E; ++j)
+                bbits[j] = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << 16;
         }
     }
-    if (ind & IND_TEMP) {
-        const Divisor t = make_divisor(rs.temp);
-#pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = div_bf16(x[j], t);
-        round_all(x);
+    finish_keys<E>(k, all_exc, x, ok, dec, ctx, bbits, keys);
+}
+
+// Memory layouts of the prologue, fixed per launch by the host:
+//   MODE_DIRECT      no d2t, vocabulary a multiple of 4, 8 / 16-byte aligned rows: vector loads
+//                    of every plane, all issued before any is consumed;
+//   MODE_GATHER_VEC  d2t given: vector logit loads, per-element gathers through the target vocab;
+//   MODE_SCALAR      anything else: per-element loads throughout.
+enum { MODE_DIRECT = 0, MODE_GATHER_VEC = 1, MODE_SCALAR = 2 };
+
+// Streams one tile of one row through the processor chain and returns the keys (0 = absent).
+// `lw` holds the tile's logits from load_logits_vec unless MODE is MODE_SCALAR.
+template <int E, int MODE>
+__device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
+                                              const int32_t *hist, const u32x2 (&lw)[E / 4],
+                                              uint32_t (&keys)[E]) {
+    const Uses u = row_uses(rs);
+    if constexpr (MODE == MODE_DIRECT) {
+        Planes<E> pl;
+        issue_planes<E>(rs, u, true, col0, pl);
+        direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
+    } else {
+        gather_keys<E, MODE == MODE_GATHER_VEC>(rs, u, col0, V, hist, lw, keys);
     }
-#pragma unroll
-    for (int j = 0; j < E; ++j) keys[j] = ok[j] ? key_of(x[j]) : 0u;
 }
 
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose

@@ -61,6 +61,7 @@ class SingularArgs(ctypes.Structure):
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("probabilities", c_p), ("stride_probabilities", c_i64),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
+        ("stage_event", c_p),
     ]
 
 
@@ -85,6 +86,7 @@ class MultistepArgs(ctypes.Structure):
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("values", c_p), ("indices", c_p),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
+        ("stage_event", c_p),
     ]
 
 
@@ -166,6 +168,20 @@ def stride0(tensor: torch.Tensor | None) -> int:
 def stream_of(tensor: torch.Tensor) -> int:
 
     return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def event_handle(event: "torch.cuda.Event | None") -> int | None:
+    """The hipEvent_t behind a torch event (created on first use), or None."""
+
+    if event is None:
+
+        return None
+
+    if not event.cuda_event:
+
+        event.record()
+
+    return event.cuda_event
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:

@@ -13,6 +13,8 @@ Additions to the reference's keywords (all optional):
 * ``philox_seed`` / ``philox_offset`` / ``philox_step`` -- draw the Gumbel noise from the
   counter-based Philox stream instead of ``gumbel_noise``. With neither given, a fresh seed is drawn
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
+* ``stage_event`` -- a ``torch.cuda.Event`` recorded on the stream between the tile launch and the
+  row launch (per-stage timing).
 """
 
 from __future__ import annotations
@@ -107,6 +109,7 @@ def fused_singular(
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
     philox_step: int = 0,
+    stage_event: Optional[torch.cuda.Event] = None,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
@@ -208,7 +211,7 @@ def fused_singular(
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         probabilities=p(probabilities), stride_probabilities=s(probabilities),
         scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        stream=_native.stream_of(logits),
+        stream=_native.stream_of(logits), stage_event=_native.event_handle(stage_event),
     )
 
     _native.check(_native.load().ss_fused_singular(ctypes.byref(args)), "ss_fused_singular")

@@ -92,6 +92,7 @@ class UnshardedFusedSingular(TwoStageTiling):
         tuning: Optional[TwoStageWarpConfig] = None,
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
+        stage_event=None,
     ) -> Selection:
         """One decode step over `buffers.flags.target` with `gumbel.target[:, 0]` noise.
 
@@ -130,6 +131,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             warp_config=config,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
+            stage_event=stage_event,
             philox_step=0,
         )
 
@@ -148,6 +150,7 @@ class UnshardedFusedSingular(TwoStageTiling):
         tuning: Optional[TwoStageWarpConfig] = None,
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
+        stage_event=None,
     ) -> Selection:
         """One draft step over `buffers.flags.draft` with `gumbel.draft[:, timestep]` noise.
 
@@ -193,5 +196,6 @@ class UnshardedFusedSingular(TwoStageTiling):
             timestep=timestep,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
+            stage_event=stage_event,
             philox_step=timestep,
         )

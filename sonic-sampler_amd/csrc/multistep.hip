@@ -314,6 +314,8 @@ extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
     if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
         return SS_ERR_INVALID_ARGUMENT;
+    // candidate lists move as 16-byte vectors
+    if ((uintptr_t)a->scratch % 16 != 0 || a->stride_scratch % 4 != 0) return SS_ERR_INVALID_ARGUMENT;
     if (a->max_top_logprobs < 0 || a->max_top_logprobs > SS_MAX_K) return SS_ERR_INVALID_ARGUMENT;
     if (!a->philox.enabled && !a->gumbel) return SS_ERR_INVALID_ARGUMENT;
     if (a->rows == 0 || a->batch == 0) return SS_OK;

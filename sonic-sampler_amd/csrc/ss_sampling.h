@@ -23,6 +23,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct SampleSmem {
     SelectSmem sel;
+    uint32_t surv[2 * SS_K];   // tile stage: candidates that pass the lower bound
+    uint32_t runs[4][SS_K];    // row merge: the waves' sorted samples
+    int32_t col[4 * SS_K];     // row merge: column of each sample slot
+    int32_t flag;
     uint64_t cand[SS_K];
     int32_t idx[SS_K];
     int32_t hist[64];
@@ -425,11 +429,20 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
 }
 
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose
-// maximum picks the lowest column among equal maxima. Other rows store their exact top-128 as
-// (key << 16) | column offset, in column order, at scratch[tile * 128 ...].
+// maximum picks the lowest column among equal maxima. Other rows store their exact top-128 as the
+// same composites, sorted in descending order (0 for absent entries), at scratch[tile * 128 ...].
+//
+// The top-128 is found without a full selection over the tile: the 32nd-largest per-thread
+// maximum of each wave bounds the tile's 128th-largest key from below (each of the four waves has
+// 32 threads holding a key at least that large), so only keys at or above the smallest of the
+// four bounds can be in the top-128. Those survivors -- about 4% of a 4096-wide tile of
+// unstructured logits -- are gathered in LDS and one wave sorts them. Tiles whose survivors
+// exceed 256 (heavily tied keys) take the exact radix selection of the 128 instead.
 template <int E>
 __device__ __forceinline__ void tile_stage(SampleSmem &sm, bool greedy, const uint32_t (&keys)[E],
                                            uint32_t *scr, int tile) {
+    const int lane = lane_id();
+    const int wave = (int)threadIdx.x >> 6;
     if (greedy) {
         uint32_t best = 0;
 #pragma unroll
@@ -438,7 +451,7 @@ __device__ __forceinline__ void tile_stage(SampleSmem &sm, bool greedy, const ui
             best = best > c ? best : c;
         }
         best = wave_max_u32(best);
-        if (lane_id() == 0) sm.red[threadIdx.x >> 6] = best;
+        if (lane == 0) sm.red[wave] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
             uint32_t b = sm.red[0];
@@ -447,16 +460,56 @@ __device__ __forceinline__ void tile_stage(SampleSmem &sm, bool greedy, const ui
         }
         return;
     }
-    auto load = [&](int, uint32_t(&out)[E]) {
+    uint32_t m = 0;
 #pragma unroll
-        for (int j = 0; j < E; ++j) out[j] = keys[j];
-    };
-    uint32_t thi, margin;
-    int level;
-    radix_threshold<E, 16>(sm.sel, 1, load, (uint32_t)SS_K, thi, level, margin);
-    compact<E, 4>(sm.sel, 1, load, thi, level, margin, [&](uint32_t pos, int, int j) {
-        if (pos < (uint32_t)SS_K) scr[tile * SS_K + (int)pos] = (keys[j] << 16) | (uint32_t)tile_col(j);
-    });
+    for (int j = 0; j < E; ++j) m = max(m, keys[j]);
+    uint32_t bound = 0;  // the largest t with at least 32 lanes holding m >= t
+#pragma unroll
+    for (int b = 15; b >= 0; --b) {
+        const uint32_t c = bound | (1u << b);
+        if (__popcll(__ballot(m >= c)) >= 32) bound = c;
+    }
+    if (lane == 0) sm.red[wave] = bound;
+    __syncthreads();
+    uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
+    lo = lo ? lo : 1u;  // never admit absent elements
+    uint32_t n = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) n += keys[j] >= lo;
+    uint32_t off[1] = {n}, tot[1];
+    block_exclusive_scan<1>(off, tot, sm.sel.scan);
+    uint32_t count = tot[0];
+    if (count <= 2 * SS_K) {
+        uint32_t pos = off[0];
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            if (keys[j] >= lo) sm.surv[pos++] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
+        }
+    } else {
+        auto load = [&](int, uint32_t(&out)[E]) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) out[j] = keys[j];
+        };
+        uint32_t thi, margin;
+        int level;
+        radix_threshold<E, 16>(sm.sel, 1, load, (uint32_t)SS_K, thi, level, margin);
+        compact<E, 4>(sm.sel, 1, load, thi, level, margin, [&](uint32_t pos, int, int j) {
+            if (pos < (uint32_t)SS_K)
+                sm.surv[pos] = keys[j] ? (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j)) : 0u;
+        });
+        count = SS_K;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t e = 4u * (uint32_t)lane + (uint32_t)r;
+            v[r] = e < count ? sm.surv[e] : 0u;
+        }
+        wave_sort256_desc(v);
+        if (lane < SS_K / 4) *(uint4 *)(scr + tile * SS_K + 4 * lane) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
 }
 
 // Greedy merge over the tiles' maxima (wave 0): the largest value, lowest column on ties.
@@ -487,18 +540,19 @@ __device__ __forceinline__ void merge_select(SampleSmem &sm, int nsc, Load load,
         if (pos >= (uint32_t)SS_K) return;
         const int p = order_pos<EM, 4>(sc, j);
         const uint32_t c = cand(sc, j);
-        const int idx = (p / SS_K) * block_n + (int)(c & 0xffffu);
+        const int idx = (p / SS_K) * block_n + (int)(0xffffu - (c & 0xffffu));
         sm.cand[pos] = ((uint64_t)(c >> 16) << 8) | (uint64_t)(127u - pos);
         sm.idx[pos] = idx < V ? idx : V - 1;  // only an absent-element sentinel can exceed V
     });
 }
 
-// Row merge: all threads call; on return wave 0 holds the row's top-128 sorted by (value desc,
-// column asc), element e = 2 * lane + i as (v_i, idx_i). Up to 4096 candidates are read once
-// with 16-byte loads and kept in registers; larger rows stream them from the scratch per pass.
-__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, int tiles,
-                                          int block_n, int V, float &v0, float &v1, int &i0,
-                                          int &i1) {
+// Exact row merge by radix selection over every candidate (any tile order). All threads call; on
+// return wave 0 holds the row's top-128 sorted by (value desc, column asc), element
+// e = 2 * lane + i as (v_i, idx_i). Up to 4096 candidates are read once with 16-byte loads and
+// kept in registers; larger rows stream them from the scratch per pass.
+__device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *scr, int tiles,
+                                                int block_n, int V, float &v0, float &v1, int &i0,
+                                                int &i1) {
     constexpr int EM = 16;
     const int ncand = tiles * SS_K;
     const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
@@ -538,6 +592,88 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, i
         v1 = bf2f(unkey16((uint32_t)(c1 >> 8)));
         i0 = sm.idx[127 - (int)(c0 & 0x7fu)];
         i1 = sm.idx[127 - (int)(c1 & 0x7fu)];
+    }
+}
+
+// Row merge over the tiles' sorted candidate lists. All threads call; on return wave 0 holds the
+// row's top-128 sorted by (value desc, column asc), element e = 2 * lane + i as (v_i, idx_i).
+//
+// Only the first kp = min(128, 512 / tiles) entries of every list are merged: 512 sample slots,
+// slot s = list * kp + position, as composites (key << 16) | (0xffff - s), whose order is the
+// (value desc, column asc) order because lists are in tile order and equal keys of one list are
+// in column order. Each wave sorts 128 slots, and two rounds of bitonic merges keep the top-128
+// of the four runs. The result is exact unless some list holds more than kp of the row's top-128,
+// i.e. unless a list's first unmerged entry beats the 128th merged one; that case (rare: 17 of the
+// top-128 in one of 32 tiles) falls back to the radix merge over every candidate.
+__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, int tiles,
+                                          int block_n, int V, float &v0, float &v1, int &i0,
+                                          int &i1) {
+    const int lane = lane_id();
+    const int wave = (int)threadIdx.x >> 6;
+    const int kp = min(SS_K, (4 * SS_K) / tiles);
+    const int ns = tiles * kp;  // <= 512
+    uint32_t c[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int s = (int)threadIdx.x + r * SS_BLOCK;
+        uint32_t comp = 0;
+        if (s < ns) {
+            const int list = s / kp;
+            const uint32_t raw = scr[list * SS_K + (s - list * kp)];
+            if (raw) {
+                const int idx = list * block_n + (int)(0xffffu - (raw & 0xffffu));
+                sm.col[s] = idx < V ? idx : V - 1;
+                comp = (raw & 0xffff0000u) | (0xffffu - (uint32_t)s);
+            }
+        }
+        c[r] = comp;
+    }
+    wave_bitonic128_desc<2>(c[0], c[1]);
+    sm.runs[wave][2 * lane] = c[0];
+    sm.runs[wave][2 * lane + 1] = c[1];
+    __syncthreads();
+    if (wave < 2) {
+        // top-128 of runs (2w, 2w+1): the elementwise maximum against the reversed second run is
+        // a bitonic sequence holding them
+        const uint32_t *a = sm.runs[2 * wave], *b = sm.runs[2 * wave + 1];
+        uint32_t x0 = max(a[2 * lane], b[127 - 2 * lane]);
+        uint32_t x1 = max(a[2 * lane + 1], b[126 - 2 * lane]);
+        wave_bitonic128_desc<128>(x0, x1);
+        sm.runs[2 * wave][2 * lane] = x0;
+        sm.runs[2 * wave][2 * lane + 1] = x1;
+    }
+    __syncthreads();
+    uint32_t f0 = 0, f1 = 0;
+    if (wave == 0) {
+        f0 = max(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
+        f1 = max(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
+        wave_bitonic128_desc<128>(f0, f1);
+        // exactness check: no list's first unmerged entry may beat the 128th merged element
+        const uint32_t last = __shfl(f1, 63, 64);
+        const uint32_t klast = last >> 16;
+        const int ilast = last ? sm.col[0xffffu - (last & 0xffffu)] : V;
+        bool beat = false;
+        if (kp < SS_K) {
+            for (int t = lane; t < tiles; t += 64) {
+                const uint32_t nx = scr[t * SS_K + kp];
+                const uint32_t kn = nx >> 16;
+                const int in = t * block_n + (int)(0xffffu - (nx & 0xffffu));
+                beat |= nx != 0u && (kn > klast || (kn == klast && in < ilast));
+            }
+        }
+        const bool any = __ballot(beat) != 0;
+        if (lane == 0) sm.flag = any ? 1 : 0;
+    }
+    __syncthreads();
+    if (sm.flag) {
+        merge_row_radix(sm, scr, tiles, block_n, V, v0, v1, i0, i1);
+        return;
+    }
+    if (wave == 0) {
+        v0 = bf2f(unkey16(f0 >> 16));
+        v1 = bf2f(unkey16(f1 >> 16));
+        i0 = f0 ? sm.col[0xffffu - (f0 & 0xffffu)] : V - 1;
+        i1 = f1 ? sm.col[0xffffu - (f1 & 0xffffu)] : V - 1;
     }
 }
 

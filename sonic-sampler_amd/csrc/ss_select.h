@@ -157,35 +157,74 @@ __device__ __forceinline__ int order_pos(int sc, int j) {
     return sc * (SS_BLOCK * E) + (j / CH) * (SS_BLOCK * CH) + (int)threadIdx.x * CH + (j % CH);
 }
 
-// Sorts 128 64-bit composites held by wave 0 (two per lane: element 2*lane + i) in descending
-// order with a bitonic network over lanes. Composites must be distinct for a deterministic order.
-__device__ __forceinline__ void wave_sort128_desc(uint64_t &a0, uint64_t &a1) {
+// One merge size of a bitonic network over 128 values held by one wave, two per lane (element
+// 2 * lane + i in a_i), ordering each run of SIZE elements descending or ascending by the run's
+// parity, as the descending network needs.
+template <int SIZE, typename T>
+__device__ __forceinline__ void bitonic128_size(T &a0, T &a1) {
     const int lane = lane_id();
-    // element index e = 2 * lane + i
+    const bool desc = ((2 * lane) & SIZE) == 0;  // the same for both elements of the lane
 #pragma unroll
-    for (int size = 2; size <= 128; size <<= 1) {
+    for (int dist = SIZE >> 1; dist > 1; dist >>= 1) {
+        const int ld = dist >> 1;  // lane distance
+        const T p0 = __shfl_xor(a0, ld, 64);
+        const T p1 = __shfl_xor(a1, ld, 64);
+        const bool keep_hi = ((lane & ld) == 0) == desc;  // lower element index keeps the max
+        const T h0 = a0 > p0 ? a0 : p0, l0 = a0 > p0 ? p0 : a0;
+        const T h1 = a1 > p1 ? a1 : p1, l1 = a1 > p1 ? p1 : a1;
+        a0 = keep_hi ? h0 : l0;
+        a1 = keep_hi ? h1 : l1;
+    }
+    // partner inside the lane: elements 2 * lane and 2 * lane + 1
+    const T lo = a0 < a1 ? a0 : a1, hi = a0 < a1 ? a1 : a0;
+    a0 = desc ? hi : lo;
+    a1 = desc ? lo : hi;
+}
+
+// Bitonic network sorting 128 values held by one wave (two per lane) in descending order, from
+// merge size FIRST: 2 sorts arbitrary input; 128 only runs the final merge, which sorts any
+// bitonic sequence. Values must be distinct for a deterministic order.
+template <int FIRST = 2, typename T>
+__device__ __forceinline__ void wave_bitonic128_desc(T &a0, T &a1) {
+    if constexpr (FIRST <= 128) {
+        bitonic128_size<FIRST>(a0, a1);
+        wave_bitonic128_desc<FIRST * 2>(a0, a1);
+    }
+}
+
+// Sorts 128 64-bit composites held by one wave (element 2 * lane + i) in descending order.
+__device__ __forceinline__ void wave_sort128_desc(uint64_t &a0, uint64_t &a1) {
+    wave_bitonic128_desc<2>(a0, a1);
+}
+
+// Sorts 256 32-bit values held by one wave (element e = 4 * lane + r in v[r]) in descending
+// order with a bitonic network: in-lane exchanges for element distances 1 and 2, lane shuffles
+// for the larger ones.
+__device__ __forceinline__ void wave_sort256_desc(uint32_t (&v)[4]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 256; size <<= 1) {
 #pragma unroll
         for (int dist = size >> 1; dist > 0; dist >>= 1) {
-            if (dist == 1) {
-                // partner inside the lane: elements 2*lane and 2*lane+1
-                const int e0 = 2 * lane;
-                const bool desc = ((e0 & size) == 0);
-                const uint64_t lo = a0 < a1 ? a0 : a1, hi = a0 < a1 ? a1 : a0;
-                a0 = desc ? hi : lo;
-                a1 = desc ? lo : hi;
-            } else {
-                const int ld = dist >> 1;  // lane distance
-                const uint64_t p0 = __shfl_xor(a0, ld, 64);
-                const uint64_t p1 = __shfl_xor(a1, ld, 64);
-                const bool lower = (lane & ld) == 0;  // this lane holds the lower element index
+            if (dist < 4) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int e = 2 * lane + i;
-                    const bool desc = ((e & size) == 0);
-                    uint64_t mine = i ? a1 : a0, other = i ? p1 : p0;
-                    const uint64_t hi = mine > other ? mine : other, lo = mine > other ? other : mine;
-                    const uint64_t res = (lower == desc) ? hi : lo;
-                    if (i) a1 = res; else a0 = res;
+                for (int r = 0; r < 4; ++r) {
+                    const int p = r ^ dist;
+                    if (p > r) {
+                        const bool desc = ((4 * lane + r) & size) == 0;
+                        const uint32_t hi = max(v[r], v[p]), lo = min(v[r], v[p]);
+                        v[r] = desc ? hi : lo;
+                        v[p] = desc ? lo : hi;
+                    }
+                }
+            } else {
+                const int ld = dist >> 2;  // lane distance
+                const bool lower = (lane & ld) == 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t o = __shfl_xor(v[r], ld, 64);
+                    const bool desc = ((4 * lane + r) & size) == 0;
+                    v[r] = (lower == desc) ? max(v[r], o) : min(v[r], o);
                 }
             }
         }

@@ -160,3 +160,42 @@ def test_config4_drafting_full_size():
     # every selected token is grammar-admissible and in the d2t image
     image = set(work.d2t.tolist())
     assert all(int(t) in image for t in selection.tokens[:, 0].cpu())
+
+
+@pytest.mark.parametrize("seed", [20, 21])
+def test_concentrated_and_tied_rows(seed):
+    """Rows that defeat the sampled merge (one tile holding most of the top-128) or the tile
+    stage's lower bound (long runs of equal keys) take the exact radix paths; results must not
+    change."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    rows, vocab, block = 16, 65536, 2048
+    g = torch.Generator().manual_seed(seed)
+    logits = spiked_logits(rows, vocab, seed=300 + seed).float()
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0:    # 60 large values inside one tile
+            tile = int(torch.randint(0, vocab // block, (1,), generator=g))
+            cols = tile * block + torch.randperm(block, generator=g)[:60]
+            logits[r, cols] = 25.0 + torch.rand(60, generator=g) * 5.0
+        elif kind == 1:  # every logit equal
+            logits[r] = 0.5
+        elif kind == 2:  # a handful of distinct values
+            logits[r] = torch.randint(-3, 4, (vocab,), generator=g).float()
+    logits = logits.to(torch.bfloat16)
+    host = SamplingBuffers.random(size=rows, timesteps=1, vocab_size=vocab, device="cpu", seed=seed,
+                                  max_top_logprobs=8)
+    buffers = to_device(host, DEV)
+    print(f"concentrated / tied rows seed={seed}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=8,
+                                                block_size=block, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=8)
+    check_singular(selection, expected, logprobs=True)

@@ -59,6 +59,37 @@ __device__ __forceinline__ uint32_t unkey32(uint32_t k) {
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// The value of lane (lane ^ LD) for LD in {1, 2, 4, 8, 16, 32}: DPP lane permutations within a
+// 16-lane row (quad_perm for 1 and 2, row shifts for 4, row rotation by 8 for 8) and the gfx950
+// row swaps for 16 and 32. Register-to-register, no LDS round trip.
+template <int LD>
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t v) {
+    static_assert(LD == 1 || LD == 2 || LD == 4 || LD == 8 || LD == 16 || LD == 32, "lane distance");
+    const int x = (int)v;
+    if constexpr (LD == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (LD == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (LD == 4) {
+        const int up = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0xf, false);    // row_shl:4, lane + 4
+        const int down = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xf, 0xf, false);  // row_shr:4, lane - 4
+        return (uint32_t)((__lane_id() & 4) ? down : up);
+    } else if constexpr (LD == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(x, x, 0x128, 0xf, 0xf, false);  // row_ror:8
+    } else if constexpr (LD == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? p[0] : p[1];
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? p[0] : p[1];
+    }
+}
+
+template <int LD>
+__device__ __forceinline__ uint64_t xor_lanes(uint64_t v) {
+    return ((uint64_t)xor_lanes<LD>((uint32_t)(v >> 32)) << 32) | xor_lanes<LD>((uint32_t)v);
+}
+
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
     const int lane = lane_id();
 #pragma unroll

@@ -157,6 +157,28 @@ __device__ __forceinline__ int order_pos(int sc, int j) {
     return sc * (SS_BLOCK * E) + (j / CH) * (SS_BLOCK * CH) + (int)threadIdx.x * CH + (j % CH);
 }
 
+// One compare-exchange step at lane distance LD of a bitonic network whose merge runs have the
+// direction `desc`; every element of the lane pairs with the same element of lane (lane ^ LD).
+template <int LD, int N, typename T>
+__device__ __forceinline__ void bitonic_lane_step(T (&a)[N], bool desc) {
+    const bool keep_hi = ((lane_id() & LD) == 0) == desc;  // the lower lane keeps the max
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const T p = xor_lanes<LD>(a[i]);
+        const T hi = a[i] > p ? a[i] : p, lo = a[i] > p ? p : a[i];
+        a[i] = keep_hi ? hi : lo;
+    }
+}
+
+// The lane-distance steps LD, LD / 2, ..., 1 of one merge size.
+template <int LD, int N, typename T>
+__device__ __forceinline__ void bitonic_lane_steps(T (&a)[N], bool desc) {
+    if constexpr (LD >= 1) {
+        bitonic_lane_step<LD>(a, desc);
+        bitonic_lane_steps<LD / 2>(a, desc);
+    }
+}
+
 // One merge size of a bitonic network over 128 values held by one wave, two per lane (element
 // 2 * lane + i in a_i), ordering each run of SIZE elements descending or ascending by the run's
 // parity, as the descending network needs.
@@ -164,19 +186,10 @@ template <int SIZE, typename T>
 __device__ __forceinline__ void bitonic128_size(T &a0, T &a1) {
     const int lane = lane_id();
     const bool desc = ((2 * lane) & SIZE) == 0;  // the same for both elements of the lane
-#pragma unroll
-    for (int dist = SIZE >> 1; dist > 1; dist >>= 1) {
-        const int ld = dist >> 1;  // lane distance
-        const T p0 = __shfl_xor(a0, ld, 64);
-        const T p1 = __shfl_xor(a1, ld, 64);
-        const bool keep_hi = ((lane & ld) == 0) == desc;  // lower element index keeps the max
-        const T h0 = a0 > p0 ? a0 : p0, l0 = a0 > p0 ? p0 : a0;
-        const T h1 = a1 > p1 ? a1 : p1, l1 = a1 > p1 ? p1 : a1;
-        a0 = keep_hi ? h0 : l0;
-        a1 = keep_hi ? h1 : l1;
-    }
+    T a[2] = {a0, a1};
+    bitonic_lane_steps<SIZE / 4>(a, desc);
     // partner inside the lane: elements 2 * lane and 2 * lane + 1
-    const T lo = a0 < a1 ? a0 : a1, hi = a0 < a1 ? a1 : a0;
+    const T lo = a[0] < a[1] ? a[0] : a[1], hi = a[0] < a[1] ? a[1] : a[0];
     a0 = desc ? hi : lo;
     a1 = desc ? lo : hi;
 }
@@ -197,38 +210,39 @@ __device__ __forceinline__ void wave_sort128_desc(uint64_t &a0, uint64_t &a1) {
     wave_bitonic128_desc<2>(a0, a1);
 }
 
-// Sorts 256 32-bit values held by one wave (element e = 4 * lane + r in v[r]) in descending
-// order with a bitonic network: in-lane exchanges for element distances 1 and 2, lane shuffles
-// for the larger ones.
-__device__ __forceinline__ void wave_sort256_desc(uint32_t (&v)[4]) {
+// One merge size of the 256-element network of wave_sort256_desc.
+template <int SIZE>
+__device__ __forceinline__ void bitonic256_size(uint32_t (&v)[4]) {
     const int lane = lane_id();
+    if constexpr (SIZE >= 8) {
+        bitonic_lane_steps<SIZE / 8>(v, ((4 * lane) & SIZE) == 0);
+    }
 #pragma unroll
-    for (int size = 2; size <= 256; size <<= 1) {
+    for (int dist = (SIZE >= 4 ? 2 : 1); dist > 0; dist >>= 1) {
 #pragma unroll
-        for (int dist = size >> 1; dist > 0; dist >>= 1) {
-            if (dist < 4) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int p = r ^ dist;
-                    if (p > r) {
-                        const bool desc = ((4 * lane + r) & size) == 0;
-                        const uint32_t hi = max(v[r], v[p]), lo = min(v[r], v[p]);
-                        v[r] = desc ? hi : lo;
-                        v[p] = desc ? lo : hi;
-                    }
-                }
-            } else {
-                const int ld = dist >> 2;  // lane distance
-                const bool lower = (lane & ld) == 0;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t o = __shfl_xor(v[r], ld, 64);
-                    const bool desc = ((4 * lane + r) & size) == 0;
-                    v[r] = (lower == desc) ? max(v[r], o) : min(v[r], o);
-                }
+        for (int r = 0; r < 4; ++r) {
+            const int p = r ^ dist;
+            if (p > r) {
+                const bool desc = ((4 * lane + r) & SIZE) == 0;
+                const uint32_t hi = max(v[r], v[p]), lo = min(v[r], v[p]);
+                v[r] = desc ? hi : lo;
+                v[p] = desc ? lo : hi;
             }
         }
     }
 }
+
+template <int SIZE = 2>
+__device__ __forceinline__ void bitonic256_from(uint32_t (&v)[4]) {
+    if constexpr (SIZE <= 256) {
+        bitonic256_size<SIZE>(v);
+        bitonic256_from<SIZE * 2>(v);
+    }
+}
+
+// Sorts 256 32-bit values held by one wave (element e = 4 * lane + r in v[r]) in descending
+// order with a bitonic network: in-lane exchanges for element distances 1 and 2, lane
+// permutations for the larger ones.
+__device__ __forceinline__ void wave_sort256_desc(uint32_t (&v)[4]) { bitonic256_from<2>(v); }
 
 }  // namespace ss

@@ -1,0 +1,217 @@
+"""Host-side surface on the CPU: indicator derivation, buffer layouts, dispatch resolution and the
+functional entry points' argument errors (raised before any device work). Each block cites the
+reference module whose behaviour it checks (the reference ships no tests of its own)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from sonic_sampler.core.flags import Flags, Indicator, SamplingMode, ScopedIndicators
+from sonic_sampler.core.buffer import SamplingBuffers
+from sonic_sampler.interface.base import TwoStageTiling, resolve_dispatch
+from sonic_sampler.interface.dispatch import DispatchSummary
+from sonic_sampler.ops.base import MAX_K, next_power_of_2
+
+
+# ------------------------------------------------------------------------------------------------
+# Indicators (reference core/flags.py:150-184)
+# ------------------------------------------------------------------------------------------------
+
+def test_greedy_is_top_k_one_and_masks_stochastic_bits():
+
+    bits = Indicator.from_params(temperature=0.7, top_k=1, top_p=0.9, min_p=0.1, top_k_logprobs=5,
+                                 greedy_draft=True)
+
+    assert Indicator.GREEDY in bits
+    assert Indicator.TEMPERATURE in bits
+    for masked in (Indicator.TOP_K, Indicator.TOP_P, Indicator.MIN_P, Indicator.TOP_K_LOGPROBS,
+                   Indicator.STOCHASTIC_VERIFY_GREEDY_DRAFT):
+        assert masked not in bits
+
+
+@pytest.mark.parametrize("top_k, expected", [(0, False), (1, False), (2, True), (127, True), (128, False),
+                                             (1000, False)])
+def test_top_k_bit_only_strictly_inside_the_bound(top_k, expected):
+
+    assert (Indicator.TOP_K in Indicator.from_params(top_k=top_k)) is expected
+
+
+@pytest.mark.parametrize("field, value, bit", [
+    ("multiplicative", 1.1, Indicator.MULTIPLICATIVE),
+    ("frequency", 0.2, Indicator.FREQUENCY),
+    ("presence", -0.3, Indicator.PRESENCE),
+    ("temperature", 0.5, Indicator.TEMPERATURE),
+    ("top_p", 0.9, Indicator.TOP_P),
+    ("min_p", 0.05, Indicator.MIN_P),
+    ("top_k_logprobs", 5, Indicator.TOP_K_LOGPROBS),
+])
+def test_each_parameter_sets_its_bit(field, value, bit):
+
+    assert bit in Indicator.from_params(**{field: value})
+    assert Indicator.from_params() & bit == 0
+
+
+def test_neutral_parameters_give_no_bits():
+
+    assert int(Indicator.from_params()) == 0
+    assert int(Indicator.from_params(top_p=1.0, min_p=0.0, top_k=MAX_K)) == 0
+
+
+def test_greedy_resolution_and_modes():
+
+    full = Indicator.maximal()
+
+    assert full.greedy() & Indicator.stochastic() == 0
+    assert Indicator.GREEDY in full.greedy()
+    assert full.resolve(SamplingMode.MINIMAL) == Indicator.GREEDY
+    assert Indicator.GRAMMAR not in full.resolve(SamplingMode.NON_GRAMMAR)
+    assert Indicator.GREEDY not in full
+    assert int(Indicator.all()) == 0xFFF
+
+
+def test_flags_pack_target_and_draft_contiguously():
+
+    target = [Indicator.from_params(top_k=1), Indicator.from_params(temperature=0.5), Indicator.GRAMMAR]
+    draft = [Indicator.GREEDY, Indicator.GREEDY, Indicator.BIAS]
+    flags = Flags.from_scoped(ScopedIndicators.from_values(3, 4, target, draft), device="cpu")
+
+    assert flags.packed.shape == (3, 2)
+    assert flags.packed.stride() == (1, 3)
+    assert flags.target.is_contiguous() and flags.draft.is_contiguous()
+    assert flags.target.tolist() == [int(t) for t in target]
+    assert flags.draft.tolist() == [int(d) for d in draft]
+    assert not flags.all_greedy
+
+
+# ------------------------------------------------------------------------------------------------
+# Buffers (reference core/buffer.py:784-817, :938-986)
+# ------------------------------------------------------------------------------------------------
+
+def test_default_buffers_are_neutral():
+
+    size, steps, vocab = 3, 4, 1000
+    buffers = SamplingBuffers.default(size, steps, vocab, device="cpu", noise=False)
+
+    assert buffers.grammar.shape == (size, steps, (vocab + 31) // 32)
+    assert buffers.grammar.dtype == torch.uint32
+    assert torch.all(buffers.grammar.view(torch.int32) == -1)       # every token allowed
+    assert buffers.bias.shape == (size, vocab) and not buffers.bias.float().any()
+    assert torch.all(buffers.temperature.float() == 1.0)
+    assert torch.all(buffers.top_k == MAX_K)
+    assert torch.all(buffers.top_p.float() == 1.0)
+    assert not buffers.min_p.float().any()
+    counts = buffers.repetition.counts
+    assert counts.context.shape == counts.decode.shape == (size, vocab)
+    assert counts.decode.dtype == torch.int32
+    assert buffers.weights.gumbel.target.shape == (size, steps, vocab)
+    assert buffers.flags.packed.shape == (size, 2)
+
+
+def test_random_buffers_are_reproducible_and_honour_indicators():
+
+    a = SamplingBuffers.random(4, 2, 512, device="cpu", seed=5)
+    b = SamplingBuffers.random(4, 2, 512, device="cpu", seed=5)
+
+    assert torch.equal(a.flags.packed, b.flags.packed)
+    assert torch.equal(a.temperature, b.temperature)
+    assert torch.equal(a.repetition.counts.decode, b.repetition.counts.decode)
+
+    for row, word in enumerate(a.flags.target.tolist()):
+
+        bits = Indicator(word)
+        if Indicator.TEMPERATURE not in bits:
+            assert float(a.temperature[row]) == 1.0
+        if Indicator.MIN_P not in bits:
+            assert float(a.min_p[row]) == 0.0
+
+
+# ------------------------------------------------------------------------------------------------
+# Dispatch and tiling (reference interface/dispatch.py:105-268, interface/base.py:155-276)
+# ------------------------------------------------------------------------------------------------
+
+def test_dispatch_table_for_gfx950():
+
+    table = DispatchSummary.load(k=MAX_K, arch="gfx950")
+
+    assert table is not None
+    assert table.vocab.get(size=128256).block_n == 4096
+    assert table.vocab.get(size=32000).block_n == 2048
+    assert table.vocab.get(size=151936).block_n == 4096
+
+
+@pytest.mark.parametrize("k, block, message", [
+    (256, None, "maximum supported top-k"),
+    (48, None, "power of 2"),
+    (128, 3000, "block_size"),
+])
+def test_dispatch_errors(k, block, message):
+
+    with pytest.raises(ValueError, match=message):
+
+        resolve_dispatch(k, 32000, block, "gfx950")
+
+
+def test_tiling_buffers():
+
+    tiling, values, indices = TwoStageTiling.factory(vocab_size=128256, batch_size=8, lookahead=3,
+                                                     arch="gfx950", device="cpu")
+
+    assert tiling.block_n == 4096
+    assert tiling.vocabulary.blocks == 32
+    assert tiling.scratchpad.shape == (8 * 4, 32 * MAX_K)
+    assert tiling.scratchpad.dtype == torch.uint32
+    assert values.shape == indices.shape == (32, MAX_K)
+
+
+def test_single_tile_vocabulary_is_rejected():
+
+    with pytest.raises(ValueError, match="greater than 1"):
+
+        TwoStageTiling.factory(vocab_size=1000, block_size=1024, device="cpu")
+
+
+def test_next_power_of_2():
+
+    assert [next_power_of_2(n) for n in (1, 2, 3, 5, 128, 129)] == [1, 2, 4, 8, 128, 256]
+
+
+# ------------------------------------------------------------------------------------------------
+# Functional argument errors (reference interface/functional/*.py ValueError conditions)
+# ------------------------------------------------------------------------------------------------
+
+def test_fused_singular_argument_errors():
+
+    from sonic_sampler.interface.functional.singular import fused_singular
+
+    logits = torch.zeros(2, 8192, dtype=torch.bfloat16)
+    flags = torch.zeros(2, dtype=torch.uint16)
+
+    with pytest.raises(ValueError, match="bfloat16"):
+        fused_singular(logits.float(), flags, block_n=1024)
+    with pytest.raises(ValueError):
+        fused_singular(logits, flags, block_n=1000)
+    with pytest.raises(ValueError, match="top logprobs"):
+        fused_singular(logits, flags, block_n=1024, max_top_logprobs=129)
+    with pytest.raises(ValueError, match="sharded"):
+        fused_singular(logits, flags, block_n=1024, world_size=2)
+    with pytest.raises(ValueError):
+        fused_singular(logits, flags, block_n=1024, update_counts=True)   # counts required
+
+
+def test_fused_multistep_layout_errors():
+
+    from sonic_sampler.interface.functional.multistep import fused_multistep
+
+    flags = torch.zeros(2, dtype=torch.uint16)
+    drafted = torch.zeros(2, 5, dtype=torch.int32)
+
+    with pytest.raises(ValueError, match="lookahead"):
+        fused_multistep(torch.zeros(10, 8192, dtype=torch.bfloat16), flags, drafted, block_n=1024)
+    with pytest.raises(ValueError, match="multiple"):
+        fused_multistep(torch.zeros(11, 8192, dtype=torch.bfloat16), flags, drafted, block_n=1024, lookahead=4)
+    with pytest.raises(ValueError, match="varlen"):
+        fused_multistep(torch.zeros(2, 5, 8192, dtype=torch.bfloat16), flags, drafted, block_n=1024,
+                        cu_seqlens=torch.tensor([0, 5, 10], dtype=torch.int32))
+    with pytest.raises(ValueError, match="63"):
+        fused_multistep(torch.zeros(2, 65, 8192, dtype=torch.bfloat16), flags, drafted, block_n=1024)

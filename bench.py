@@ -312,7 +312,7 @@ def c1_tile_bytes(batch: int, vocab: int) -> int:
     return batch * vocab * C1_BYTES_PER_ELEMENT
 
 
-TILE_KERNEL = "singular_tiles_kernel<16, true>"
+TILE_KERNEL = "singular_tiles_kernel<16, 0>"
 TRAFFIC_SUMMARY = ROOT / "profiles" / "singular_tiles_c1_traffic.txt"
 
 
@@ -411,13 +411,13 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
 
-    def step(i: int, stage_event=None):
+    def step(i: int, tile_events=None):
 
         logits, buffers = inputs[i % sets]
 
         return sampler.autoregressive(logits, buffers, update_counts=True, logprobs=True,
                                       philox_seed=1234 if philox else None, philox_offset=i,
-                                      stage_event=stage_event)
+                                      tile_events=tile_events)
 
     for i in range(warmup):
 
@@ -425,31 +425,41 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
 
     torch.cuda.synchronize()
 
-    # Eager launches queued back to back: per-step time from event pairs on the launch stream,
-    # and the tile kernel's own time from the event the library records between its launches.
-    events = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
-
-    for _, mid, _ in events:
-
-        _native.event_handle(mid)
-
-    torch.cuda.synchronize()
+    # Eager launches queued back to back: per-step time from event pairs on the launch stream.
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
     _queue_behind_sleep(max(60.0, steps * 0.3))
     wall0 = time.perf_counter()
 
     for i in range(steps):
 
         events[i][0].record(stream)
-        step(i, events[i][1])
-        events[i][2].record(stream)
+        step(i)
+        events[i][1].record(stream)
 
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    launch_us = [a.elapsed_time(c) * 1e3 for a, _, c in events]
-    tile_us = [a.elapsed_time(b) * 1e3 for a, b, _ in events]
-    row_us = [b.elapsed_time(c) * 1e3 for _, b, c in events]
+    launch_us = [a.elapsed_time(b) * 1e3 for a, b in events]
     kernel_us = statistics.mean(launch_us)
-    tile_kernel_us = statistics.mean(tile_us)
+
+    # The tile kernel alone, from events its own dispatch records at its start and end (a second
+    # pass: recording them adds a little to each step, so the step time above runs without them).
+    tile_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(steps)]
+
+    for pair in tile_events:
+
+        _native.event_pair(pair)
+
+    torch.cuda.synchronize()
+    _queue_behind_sleep(max(60.0, steps * 0.3))
+
+    for i in range(steps):
+
+        step(i, tile_events[i])
+
+    torch.cuda.synchronize()
+    tile_kernel_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
 
     # hipGraph replays (one captured step per input set), back to back.
     graphs = []
@@ -511,7 +521,6 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
             "rows_per_s": round(batch / (kernel_us * 1e-6), 1),
             "median_step_us": round(statistics.median(launch_us), 3),
             "tile_kernel_us": round(tile_kernel_us, 3),
-            "row_kernel_us": round(statistics.mean(row_us), 3),
             "graph_replay_us_per_step": round(graph_us, 3),
             "host_us_per_eager_call": round(wall * 1e6 / steps, 1),
         },
@@ -533,6 +542,176 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
         result["cpu_baseline"] = cpu_baseline_c1(base, min(cpu_rows, batch))
 
     return result
+
+
+def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
+    """Eager event timing (launches queued back to back) and hipGraph replay timing of `step(i)`."""
+
+    stream = torch.cuda.current_stream()
+
+    for i in range(warmup):
+
+        step(i)
+
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    _queue_behind_sleep(max(60.0, steps * 0.3))
+
+    for i in range(steps):
+
+        events[i][0].record(stream)
+        step(i)
+        events[i][1].record(stream)
+
+    torch.cuda.synchronize()
+    eager = [a.elapsed_time(b) * 1e3 for a, b in events]
+    graphs = []
+
+    for i in range(sets):
+
+        g = torch.cuda.CUDAGraph()
+
+        with torch.cuda.graph(g):
+
+            step(i)
+
+        graphs.append(g)
+
+    for i in range(3 * sets):
+
+        graphs[i % sets].replay()
+
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _queue_behind_sleep(max(60.0, steps * 0.05))
+    start.record(stream)
+
+    for i in range(steps):
+
+        graphs[i % sets].replay()
+
+    end.record(stream)
+    torch.cuda.synchronize()
+
+    return {"eager_us": statistics.mean(eager), "median_eager_us": statistics.median(eager),
+            "graph_us": start.elapsed_time(end) * 1e3 / steps}
+
+
+CONFIG_NAMES = {
+    0: "config 0: UnshardedBoundedTopK B=8 V=32000 fp32 k=32",
+    2: "config 2: UnshardedFusedMultistep greedy gamma=4 B=128 V=151936 bf16, logprobs",
+    3: "config 3: UnshardedFusedMultistep stochastic varlen gamma<=7 B=64 V=128256 bf16, draft "
+       "probabilities, top-20 logprobs",
+    4: "config 4: UnshardedFusedSingular.drafting t=3 of gamma=4, 256 of 512 slots, d2t 32000->262144, "
+       "grammar, probabilities",
+}
+
+
+def run_config(config: int, steps: int, warmup: int, sets: int = 3) -> dict:
+    """Timing of one of the other configurations (their parity is covered by the GPU tests)."""
+
+    from sonic_sampler.interface import UnshardedBoundedTopK, UnshardedFusedMultistep, UnshardedFusedSingular
+
+    device = torch.device("cuda:0")
+
+    if config == 0:
+
+        inputs = [c0_inputs(seed=1000 + 100 * i)[0].to(device) for i in range(sets)]
+        topk = UnshardedBoundedTopK.initialize(vocab_size=32000, batch_size=8, k=32, device=device)
+        step = lambda i: topk(inputs[i % sets])  # noqa: E731
+        rows, algorithmic = 8, 8 * 32000 * 4 + 8 * 32 * 8
+
+    elif config in (2, 3):
+
+        makers = {2: c2_workload, 3: c3_workload}
+        works = [makers[config](seed=1000 + config + 100 * i) for i in range(sets)]
+        batch = len(works[0].cu_seqlens) - 1
+        verifier = UnshardedFusedMultistep.initialize(vocab_size=works[0].vocab, lookahead=works[0].lookahead,
+                                                      batch_size=batch, max_top_logprobs=works[0].max_top_logprobs,
+                                                      device=device)
+        staged = []
+
+        for w in works:
+
+            buffers = to_device(w.buffers, device)
+            probs = w.probabilities.to(device) if w.probabilities is not None else None
+
+            if w.varlen:
+
+                logits, tokens = w.logits.to(device), w.drafted.to(device)
+                cu = torch.tensor(w.cu_seqlens, dtype=I32, device=device)
+
+            else:
+
+                n = w.lookahead + 1
+                logits, tokens, cu = w.logits.view(batch, n, -1).to(device), w.drafted.view(batch, n).to(device), None
+
+            staged.append((logits, tokens, buffers, probs, cu))
+
+        def step(i):
+
+            logits, tokens, buffers, probs, cu = staged[i % sets]
+
+            return verifier(logits, tokens, buffers, probabilities=probs, logprobs=True, cu_seqlens=cu,
+                            philox_seed=None)
+
+        rows = works[0].logits.size(0)
+        algorithmic = rows * works[0].vocab * 2
+
+    elif config == 4:
+
+        works = [c4_workload(seed=1004 + 100 * i) for i in range(sets)]
+        w0 = works[0]
+        rows = w0.logits.size(0)
+        sampler = UnshardedFusedSingular.initialize(vocab_size=w0.vocab, batch_size=rows, lookahead=4,
+                                                    max_top_logprobs=5, device=device)
+        staged = []
+
+        for w in works:
+
+            probs = torch.zeros(w.buffers.layout.rows, w.target_vocab, dtype=BF16, device=device)
+            staged.append((w.logits.to(device), to_device(w.buffers, device), w.tokens.to(device), probs,
+                           w.slot_mapping.to(device), w.d2t.to(device)))
+
+        def step(i):
+
+            logits, buffers, tokens, probs, slots, d2t = staged[i % sets]
+
+            return sampler.drafting(logits, buffers, timestep=w0.timestep, tokens=tokens, probabilities=probs,
+                                    slot_mapping=slots, d2t_mapping=d2t, target_vocab=w0.target_vocab,
+                                    in_place=True)
+
+        words = w0.target_vocab // 32
+        algorithmic = rows * w0.vocab * 2 + rows * words * 4 + w0.vocab * 4 + 2 * rows * 128 * 2
+
+    else:
+
+        raise ValueError(f"unknown config {config}")
+
+    t = _time_steps(step, steps, warmup, sets)
+    us = t["eager_us"]
+
+    return {
+        "metric": f"config {config} us/step + achieved HBM GB/s",
+        "value": round(us, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "higher_is_better": False,
+        "dtype": "fp32" if config == 0 else "bf16",
+        "data": "synthetic (spiked N(0,3^2) logits, configuration generators of bench.py)",
+        "config": {
+            "workload": CONFIG_NAMES[config],
+            "rows": rows,
+            "algorithmic_bytes_per_step": algorithmic,
+            "achieved_hbm_gbs": round(algorithmic / (us * 1e-6) / 1e9, 1),
+            "rows_per_s": round(rows / (us * 1e-6), 1),
+            "median_step_us": round(t["median_eager_us"], 3),
+            "graph_replay_us_per_step": round(t["graph_us"], 3),
+        },
+    }
 
 
 def copy_calibration(gib: float = 1.0, repeats: int = 5) -> None:
@@ -563,6 +742,8 @@ def main(argv=None) -> int:
                         help="read Gumbel noise from the buffers instead of the Philox stream")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a 1 GiB device copy (PMC counter calibration)")
+    parser.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4],
+                        help="configuration to time (1, the headline, by default)")
     args = parser.parse_args(argv)
 
     if args.copy_calibration:
@@ -577,6 +758,12 @@ def main(argv=None) -> int:
               "shards by batch with no exchange, so N GPUs run N independent copies)", file=sys.stderr)
 
         return 2
+
+    if args.config != 1:
+
+        print(json.dumps(run_config(args.config, args.steps, args.warmup)), flush=True)
+
+        return 0
 
     result = run_bench(args.steps, args.warmup, cpu_rows=args.cpu_rows, philox=not args.buffer_noise)
     print(json.dumps(result), flush=True)

@@ -148,7 +148,9 @@ typedef struct ss_singular_args {
     /* in-flight */
     uint32_t *scratch; int64_t stride_scratch;             /* [rows, tiles * 128] */
     void *stream;
-    void *stage_event;   /* hipEvent_t recorded between the tile and row launches, or NULL */
+    /* timing: hipEvent_t pair recorded by the tile kernel's own dispatch (start, end), or NULL */
+    void *tile_start;
+    void *tile_end;
 } ss_singular_args;
 
 int ss_fused_singular(const ss_singular_args *args);
@@ -200,7 +202,9 @@ typedef struct ss_multistep_args {
     int32_t *indices;            /* [rows, 128] */
     uint32_t *scratch; int64_t stride_scratch;
     void *stream;
-    void *stage_event;   /* hipEvent_t recorded between the tile and row launches, or NULL */
+    /* timing: hipEvent_t pair recorded by the tile kernel's own dispatch (start, end), or NULL */
+    void *tile_start;
+    void *tile_end;
 } ss_multistep_args;
 
 int ss_fused_multistep(const ss_multistep_args *args);

@@ -10,10 +10,11 @@ Contents:
   (``src/sonic_sampler/core/naive.py`` of tachyontrails/sonic-sampler) in torch CPU operations with
   the same dtypes and rounding points, composed per row so that slot mapping, d2t indirection,
   variable lookahead and decode-count updates are covered (the reference's ``NaiveSampler`` has
-  none of these; hazard list in DESIGN.md);
+  none of these);
 * ``oracle.topk`` -- bounded top-k as a stable descending sort;
 * ``oracle.philox`` -- Philox4x32-10 in numpy and the Gumbel transform of the noise stream.
 
-Each function cites the reference file:line it restates. How each is pinned (golden vectors,
-closed forms, brute force) is listed in ``tests/test_oracle.py`` and DESIGN.md.
+Each function cites the reference file:line it restates. How each is pinned (known-answer
+vectors, closed forms, brute force, agreement with the reference's batch formulation) is in
+``tests/test_oracle.py``.
 """

@@ -8,6 +8,7 @@
 //                 resampling, logprobs, top-Z, decode-count update.
 // Semantics follow the reference's PyTorch path (core/naive.py:497-646 `verification`,
 // :694-708 `multistep`), applied per request so that slots and variable lookahead compose.
+#include "ss_launch.h"
 #include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
 
@@ -279,14 +280,13 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    if (a->stage_event && hipEventRecord((hipEvent_t)a->stage_event, s) != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, *a);

@@ -8,6 +8,7 @@
 // logprobs, top-Z logprobs and the draft-probability scatter. The launch boundary orders the two
 // stages across all XCDs without per-workgroup cache maintenance. Semantics follow the
 // reference's PyTorch path (core/naive.py:377-495 `selection`, :648-692 `preamble` / `singular`).
+#include "ss_launch.h"
 #include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
 
@@ -159,14 +160,13 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((singular_tiles_kernel<4, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((singular_tiles_kernel<8, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((singular_tiles_kernel<16, MODE>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((singular_tiles_kernel<32, MODE>), grid, block, 0, s, *a, tiles); break;
+        case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    if (a->stage_event && hipEventRecord((hipEvent_t)a->stage_event, s) != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }

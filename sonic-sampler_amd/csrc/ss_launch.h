@@ -1,0 +1,21 @@
+// Host-side launch helper shared by the fused entry points.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+namespace ss {
+
+// Launches `kernel`; with a (start, end) event pair, the events are recorded by the dispatch
+// itself (hipExtLaunchKernelGGL), so they time exactly this kernel and add no packets to the
+// stream between it and its neighbours.
+template <class Kernel, class... Args>
+inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, hipStream_t stream, void *start,
+                         void *end, Args... args) {
+    if (start && end)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (hipEvent_t)start, (hipEvent_t)end, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+}
+
+}  // namespace ss

@@ -61,7 +61,7 @@ class SingularArgs(ctypes.Structure):
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("probabilities", c_p), ("stride_probabilities", c_i64),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
-        ("stage_event", c_p),
+        ("tile_start", c_p), ("tile_end", c_p),
     ]
 
 
@@ -86,7 +86,7 @@ class MultistepArgs(ctypes.Structure):
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("values", c_p), ("indices", c_p),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
-        ("stage_event", c_p),
+        ("tile_start", c_p), ("tile_end", c_p),
     ]
 
 
@@ -182,6 +182,18 @@ def event_handle(event: "torch.cuda.Event | None") -> int | None:
         event.record()
 
     return event.cuda_event
+
+
+def event_pair(events) -> tuple:
+    """(start, end) hipEvent_t handles of a pair of torch events, or (None, None)."""
+
+    if events is None:
+
+        return None, None
+
+    start, end = events
+
+    return event_handle(start), event_handle(end)
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:

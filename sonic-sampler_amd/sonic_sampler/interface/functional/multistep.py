@@ -8,8 +8,8 @@ logits, or varlen ``[sum_i (gamma_i + 1), V]`` logits with ``cu_seqlens``) and c
 
 Additions to the reference's keywords (all optional): ``philox_seed`` / ``philox_offset`` (Gumbel
 noise from the Philox stream instead of ``gumbel_noise``; a fresh seed is drawn when neither is
-given); ``stage_event`` (a ``torch.cuda.Event`` recorded between the tile launch and the row
-launch, for per-stage timing).
+given); ``tile_events`` (a pair of timing ``torch.cuda.Event`` recorded by the tile kernel's own
+dispatch at its start and end).
 
 ``values`` receives the truncated fp32 log-probabilities of each row's top-128 (the reference
 stores their exponentials); ``indices`` the matching token ids.
@@ -18,7 +18,7 @@ stores their exponentials); ``indices`` the matching token ids.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -170,7 +170,7 @@ def fused_multistep(
     # Additions.
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
-    stage_event: Optional[torch.cuda.Event] = None,
+    tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
 ) -> Verification:
 
     validate_count_update(update_counts, decode_counts)
@@ -284,8 +284,9 @@ def fused_multistep(
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         values=p(values_buffer), indices=p(indices_buffer),
         scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        stream=_native.stream_of(logits), stage_event=_native.event_handle(stage_event),
+        stream=_native.stream_of(logits),
     )
+    args.tile_start, args.tile_end = _native.event_pair(tile_events)
 
     _native.check(_native.load().ss_fused_multistep(ctypes.byref(args)), "ss_fused_multistep")
 

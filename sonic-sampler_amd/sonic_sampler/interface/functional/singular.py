@@ -13,14 +13,14 @@ Additions to the reference's keywords (all optional):
 * ``philox_seed`` / ``philox_offset`` / ``philox_step`` -- draw the Gumbel noise from the
   counter-based Philox stream instead of ``gumbel_noise``. With neither given, a fresh seed is drawn
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
-* ``stage_event`` -- a ``torch.cuda.Event`` recorded on the stream between the tile launch and the
-  row launch (per-stage timing).
+* ``tile_events`` -- a pair of timing ``torch.cuda.Event`` recorded by the tile kernel's own
+  dispatch at its start and end (per-kernel timing without extra stream packets).
 """
 
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -109,7 +109,7 @@ def fused_singular(
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
     philox_step: int = 0,
-    stage_event: Optional[torch.cuda.Event] = None,
+    tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
@@ -211,8 +211,9 @@ def fused_singular(
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         probabilities=p(probabilities), stride_probabilities=s(probabilities),
         scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        stream=_native.stream_of(logits), stage_event=_native.event_handle(stage_event),
+        stream=_native.stream_of(logits),
     )
+    args.tile_start, args.tile_end = _native.event_pair(tile_events)
 
     _native.check(_native.load().ss_fused_singular(ctypes.byref(args)), "ss_fused_singular")
 

@@ -97,7 +97,7 @@ class UnshardedFusedMultistep(TwoStageTiling):
         cu_seqlens: Optional[Tensor] = None,
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
-        stage_event=None,
+        tile_events=None,
     ) -> Verification:
         """Verifies the drafts in `tokens` against target `logits`.
 
@@ -145,5 +145,5 @@ class UnshardedFusedMultistep(TwoStageTiling):
             warp_config=config,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
-            stage_event=stage_event,
+            tile_events=tile_events,
         )

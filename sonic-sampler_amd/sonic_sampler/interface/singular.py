@@ -92,7 +92,7 @@ class UnshardedFusedSingular(TwoStageTiling):
         tuning: Optional[TwoStageWarpConfig] = None,
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
-        stage_event=None,
+        tile_events=None,
     ) -> Selection:
         """One decode step over `buffers.flags.target` with `gumbel.target[:, 0]` noise.
 
@@ -131,7 +131,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             warp_config=config,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
-            stage_event=stage_event,
+            tile_events=tile_events,
             philox_step=0,
         )
 
@@ -150,7 +150,7 @@ class UnshardedFusedSingular(TwoStageTiling):
         tuning: Optional[TwoStageWarpConfig] = None,
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
-        stage_event=None,
+        tile_events=None,
     ) -> Selection:
         """One draft step over `buffers.flags.draft` with `gumbel.draft[:, timestep]` noise.
 
@@ -196,6 +196,6 @@ class UnshardedFusedSingular(TwoStageTiling):
             timestep=timestep,
             philox_seed=philox_seed,
             philox_offset=philox_offset,
-            stage_event=stage_event,
+            tile_events=tile_events,
             philox_step=timestep,
         )

@@ -84,7 +84,7 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
 // Tile stage: grid rows * tiles.
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
-    __shared__ SampleSmem sm;
+    __shared__ TileSmem sm;
     const int row = blockIdx.x / tiles;
     const int tile = blockIdx.x - row * tiles;
     u32x2 lw[E / 4];

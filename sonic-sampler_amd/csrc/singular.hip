@@ -41,7 +41,7 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 // Tile stage: grid rows * tiles.
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles) {
-    __shared__ SampleSmem sm;
+    __shared__ TileSmem sm;
     const int row = blockIdx.x / tiles;
     const int tile = blockIdx.x - row * tiles;
     u32x2 lw[E / 4];

@@ -33,6 +33,16 @@ struct SampleSmem {
     uint32_t red[SS_WAVES];
 };
 
+// Workgroup memory of the tile kernels.
+struct TileSmem {
+    uint32_t scan[SS_WAVES * 8];
+    uint32_t red[SS_WAVES];
+    uint32_t surv[2 * SS_K];    // candidates at or above the tile's lower bound
+    uint32_t run64[4 * 64];     // merge tree: every wave's sorted 64
+    uint32_t run128[2 * SS_K];  // merge tree: the sorted 128-runs of waves 0 and 1
+    int32_t hist[64];           // drafted tokens that extend the decode history
+};
+
 // Request state of one logit row, uniform over the workgroup. Row pointers are already offset to
 // the request's slot (and timestep for the grammar).
 struct RowState {
@@ -428,18 +438,36 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     }
 }
 
+// Workgroup-wide sum of one count per thread. All threads call.
+__device__ __forceinline__ uint32_t block_count(uint32_t n, uint32_t *red) {
+    n = wave_sum(n);
+    if (lane_id() == 0) red[threadIdx.x >> 6] = n;
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < SS_WAVES; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose
 // maximum picks the lowest column among equal maxima. Other rows store their exact top-128 as the
 // same composites, sorted in descending order (0 for absent entries), at scratch[tile * 128 ...].
 //
-// The top-128 is found without a full selection over the tile: the 32nd-largest per-thread
-// maximum of each wave bounds the tile's 128th-largest key from below (each of the four waves has
-// 32 threads holding a key at least that large), so only keys at or above the smallest of the
-// four bounds can be in the top-128. Those survivors -- about 4% of a 4096-wide tile of
-// unstructured logits -- are gathered in LDS and one wave sorts them. Tiles whose survivors
-// exceed 256 (heavily tied keys) take the exact radix selection of the 128 instead.
+// The top-128 is found without a selection over the whole tile. Lower bound: per wave, the
+// largest t such that the lanes' largest and second-largest keys include at least 32 keys >= t,
+// so the wave holds at least 32 keys >= t; with lo the smallest of the four wave bounds, the tile
+// holds at least 128 keys >= lo. The survivors (keys >= lo: about 160 of a 4096-wide tile of
+// unstructured logits) are compacted into LDS and sorted by a merge tree: every wave sorts 64 of
+// them, waves 0-1 merge pairs into sorted 128-runs, wave 0 keeps the top-128 of the two runs.
+//
+// A tile with more than 256 survivors (long runs of equal keys) finds the exact 128th key T by
+// bisection on workgroup counts, then the column cut C of its ties, and keeps the elements with
+// key > T or key == T and column < C: exactly the first 128 of the stable descending order. The
+// cut is expressed through the same (T, C) test the normal path uses with T = lo - 1, C = 0, so
+// both share one compaction.
 template <int E>
-__device__ __forceinline__ void tile_stage(SampleSmem &sm, bool greedy, const uint32_t (&keys)[E],
+__device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint32_t (&keys)[E],
                                            uint32_t *scr, int tile) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
@@ -460,55 +488,98 @@ __device__ __forceinline__ void tile_stage(SampleSmem &sm, bool greedy, const ui
         }
         return;
     }
-    uint32_t m = 0;
+    uint32_t m1 = 0, m2 = 0;  // the lane's largest and second-largest key
 #pragma unroll
-    for (int j = 0; j < E; ++j) m = max(m, keys[j]);
-    uint32_t bound = 0;  // the largest t with at least 32 lanes holding m >= t
+    for (int j = 0; j < E; ++j) {
+        m2 = max(m2, min(m1, keys[j]));
+        m1 = max(m1, keys[j]);
+    }
+    uint32_t bound = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {
         const uint32_t c = bound | (1u << b);
-        if (__popcll(__ballot(m >= c)) >= 32) bound = c;
+        if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= 32) bound = c;
     }
     if (lane == 0) sm.red[wave] = bound;
     __syncthreads();
-    uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
-    lo = lo ? lo : 1u;  // never admit absent elements
+    const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
+    uint32_t T = lo ? lo - 1 : 0u;  // key 0 (absent) never survives
+    int C = 0;
     uint32_t n = 0;
 #pragma unroll
-    for (int j = 0; j < E; ++j) n += keys[j] >= lo;
+    for (int j = 0; j < E; ++j) n += keys[j] > T;
     uint32_t off[1] = {n}, tot[1];
-    block_exclusive_scan<1>(off, tot, sm.sel.scan);
+    block_exclusive_scan<1>(off, tot, sm.scan);
     uint32_t count = tot[0];
-    if (count <= 2 * SS_K) {
-        uint32_t pos = off[0];
+    if (count > 2 * SS_K) {
+        uint32_t t = 0;  // the largest t with at least 128 keys >= t
+#pragma unroll 1
+        for (int b = 15; b >= 0; --b) {
+            const uint32_t c = t | (1u << b);
+            uint32_t k = 0;
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-            if (keys[j] >= lo) sm.surv[pos++] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
+            for (int j = 0; j < E; ++j) k += keys[j] >= c;
+            if (block_count(k, sm.red) >= (uint32_t)SS_K) t = c;
         }
-    } else {
-        auto load = [&](int, uint32_t(&out)[E]) {
+        T = t;
+        uint32_t k = 0;
 #pragma unroll
-            for (int j = 0; j < E; ++j) out[j] = keys[j];
-        };
-        uint32_t thi, margin;
-        int level;
-        radix_threshold<E, 16>(sm.sel, 1, load, (uint32_t)SS_K, thi, level, margin);
-        compact<E, 4>(sm.sel, 1, load, thi, level, margin, [&](uint32_t pos, int, int j) {
-            if (pos < (uint32_t)SS_K)
-                sm.surv[pos] = keys[j] ? (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j)) : 0u;
-        });
-        count = SS_K;
+        for (int j = 0; j < E; ++j) k += keys[j] > T;
+        const uint32_t need = (uint32_t)SS_K - block_count(k, sm.red);
+        int clo = 0, chi = SS_BLOCK * E;  // the smallest column with `need` ties at or before it
+#pragma unroll 1
+        while (clo < chi) {
+            const int mid = (clo + chi) >> 1;
+            uint32_t q = 0;
+#pragma unroll
+            for (int j = 0; j < E; ++j) q += (keys[j] == T) & (tile_col(j) <= mid);
+            if (block_count(q, sm.red) >= need) chi = mid; else clo = mid + 1;
+        }
+        C = clo + 1;
+        n = 0;
+#pragma unroll
+        for (int j = 0; j < E; ++j) n += (keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C));
+        off[0] = n;
+        block_exclusive_scan<1>(off, tot, sm.scan);
+        count = tot[0];
+    }
+    uint32_t pos = off[0];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        if ((keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C)))
+            sm.surv[pos++] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
     }
     __syncthreads();
-    if (wave == 0) {
-        uint32_t v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t e = 4u * (uint32_t)lane + (uint32_t)r;
-            v[r] = e < count ? sm.surv[e] : 0u;
+    {
+        const uint32_t e = 64u * (uint32_t)wave + (uint32_t)lane;
+        uint32_t v = e < count ? sm.surv[e] : 0u;
+        if (count > 64u * (uint32_t)wave) wave_sort64_desc(v);
+        sm.run64[e] = v;
+    }
+    __syncthreads();
+    if (wave < 2) {
+        // runs 2w and 2w+1, the second reversed, form a bitonic sequence of 128
+        const uint32_t *A = sm.run64 + 128 * wave, *B = A + 64;
+        uint32_t a0 = lane < 32 ? A[2 * lane] : B[127 - 2 * lane];
+        uint32_t a1 = lane < 32 ? A[2 * lane + 1] : B[126 - 2 * lane];
+        if (count > 128u * (uint32_t)wave + 64u) wave_bitonic128_desc<128>(a0, a1);
+        if (count <= (uint32_t)SS_K) {
+            if (wave == 0) *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(a0, a1);
+        } else {
+            sm.run128[SS_K * wave + 2 * lane] = a0;
+            sm.run128[SS_K * wave + 2 * lane + 1] = a1;
         }
-        wave_sort256_desc(v);
-        if (lane < SS_K / 4) *(uint4 *)(scr + tile * SS_K + 4 * lane) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    if (count > (uint32_t)SS_K) {
+        __syncthreads();
+        if (wave == 0) {
+            // the elementwise maximum against the reversed second run is a bitonic sequence
+            // holding the top-128 of both
+            uint32_t c0 = max(sm.run128[2 * lane], sm.run128[SS_K + 127 - 2 * lane]);
+            uint32_t c1 = max(sm.run128[2 * lane + 1], sm.run128[SS_K + 126 - 2 * lane]);
+            wave_bitonic128_desc<128>(c0, c1);
+            *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(c0, c1);
+        }
     }
 }
 

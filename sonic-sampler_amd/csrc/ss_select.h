@@ -240,6 +240,19 @@ __device__ __forceinline__ void bitonic256_from(uint32_t (&v)[4]) {
     }
 }
 
+// Sorts 64 values held by one wave (one per lane, element = lane) in descending order.
+__device__ __forceinline__ void wave_sort64_desc(uint32_t &v) {
+    const int lane = lane_id();
+    uint32_t a[1] = {v};
+    bitonic_lane_steps<1>(a, (lane & 2) == 0);
+    bitonic_lane_steps<2>(a, (lane & 4) == 0);
+    bitonic_lane_steps<4>(a, (lane & 8) == 0);
+    bitonic_lane_steps<8>(a, (lane & 16) == 0);
+    bitonic_lane_steps<16>(a, (lane & 32) == 0);
+    bitonic_lane_steps<32>(a, true);
+    v = a[0];
+}
+
 // Sorts 256 32-bit values held by one wave (element e = 4 * lane + r in v[r]) in descending
 // order with a bitonic network: in-lane exchanges for element distances 1 and 2, lane
 // permutations for the larger ones.

@@ -1,7 +1,7 @@
 // Fused chain speculative verification (replaces K1 ops/prologue.py:272-472, K5
 // ops/multistep.py:76-226 and K6 ops/verify.py:244-434 of the reference), as three back-to-back
 // launches on the caller's stream; rows = B * (gamma + 1) or cu_seqlens[B] (variable lookahead).
-//   tile stage    grid rows * tiles: prologue over one tile of one row -> tile argmax / top-128;
+//   tile stage    grid (tiles, rows): prologue over one tile of one row -> tile argmax / top-128;
 //   row stage     grid rows: merge -> truncation -> fp32 log_softmax, written to values /
 //                 indices [row, 128] (greedy rows: the argmax in indices[row, 0]);
 //   request stage grid B (one wavefront each): greedy or stochastic chain verification, residual
@@ -81,12 +81,12 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
     return step >= 0 && step < rq.n && rq.n <= a.lookahead + 1;
 }
 
-// Tile stage: grid rows * tiles.
+// Tile stage: grid (tiles, rows).
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
     __shared__ TileSmem sm;
-    const int row = blockIdx.x / tiles;
-    const int tile = blockIdx.x - row * tiles;
+    const int row = blockIdx.y;
+    const int tile = blockIdx.x;
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
     const Request rq = resolve_request(a, row);
@@ -277,7 +277,8 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
 
 template <int MODE>
 static int launch_multistep(const ss_multistep_args *a, int tiles) {
-    dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
+    // x: the tiles of a row, y: rows; the linear dispatch order is row-major as (row, tile)
+    dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
         case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
@@ -311,6 +312,7 @@ extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
     if (!a->cu_seqlens && a->rows != a->batch * (a->lookahead + 1)) return SS_ERR_INVALID_ARGUMENT;
     if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
         return SS_ERR_UNSUPPORTED;
+    if (a->rows > 65535) return SS_ERR_UNSUPPORTED;  // rows are the tile grid's y dimension
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
     if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
         return SS_ERR_INVALID_ARGUMENT;

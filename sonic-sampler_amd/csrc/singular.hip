@@ -1,7 +1,7 @@
 // Fused single-step sampling (replaces K1 ops/prologue.py:272-472 followed by K4
 // ops/singular.py:154-358 of the reference), as two back-to-back launches on the caller's stream.
 //
-// Tile stage, grid rows * tiles: every workgroup runs the logit-processor prologue over one
+// Tile stage, grid (tiles, rows): every workgroup runs the logit-processor prologue over one
 // vocabulary tile of one row and leaves either the tile argmax (greedy rows) or its exact top-128
 // in the row's scratch. Row stage, grid rows: one workgroup per row merges the candidates and
 // performs the selection: truncation, d2t remap, Gumbel-max over bf16(v - w), decode-count update,
@@ -38,12 +38,12 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
     return rs;
 }
 
-// Tile stage: grid rows * tiles.
+// Tile stage: grid (tiles, rows).
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles) {
     __shared__ TileSmem sm;
-    const int row = blockIdx.x / tiles;
-    const int tile = blockIdx.x - row * tiles;
+    const int row = blockIdx.y;
+    const int tile = blockIdx.x;
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
     const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
@@ -157,7 +157,8 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
 
 template <int MODE>
 static int launch_singular(const ss_singular_args *a, int tiles) {
-    dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
+    // x: the tiles of a row, y: rows; the linear dispatch order is row-major as (row, tile)
+    dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
         case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
@@ -186,6 +187,7 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
         return SS_ERR_INVALID_ARGUMENT;
     if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
         return SS_ERR_UNSUPPORTED;
+    if (a->rows > 65535) return SS_ERR_UNSUPPORTED;  // rows are the tile grid's y dimension
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
     if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
         return SS_ERR_INVALID_ARGUMENT;

@@ -153,33 +153,85 @@ __device__ __forceinline__ float chain(const Chain &k, float x, int32_t dec, int
     return x;
 }
 
+// Branch-free form of `chain` for rows whose divisors have exact reciprocals (Divisor::fast):
+// every processor is applied, the ones that are off with neutral parameters (factor 1, penalty
+// 0, bias 0, temperature 1). Rounding a bf16-exact value to bf16 is the identity, so the result
+// equals that of the gated chain.
+struct FastChain {
+    bool mult;
+    float rep, rrcp, fr, pr, trcp;
+};
+
+__device__ __forceinline__ FastChain fast_chain(const Chain &k) {
+    FastChain f;
+    f.mult = k.mult;
+    f.rep = k.rep;
+    f.rrcp = k.rdiv.rcp;
+    f.fr = k.freq ? k.fr : 0.0f;
+    f.pr = k.pres ? k.pr : 0.0f;
+    f.trcp = k.temp ? k.tdiv.rcp : 1.0f;
+    return f;
+}
+
+__device__ __forceinline__ float chain_fast(const FastChain &k, float x, int32_t dec, int32_t ctx,
+                                            float b) {
+    const float xm = rnd(x < 0.0f ? x * k.rep : x * k.rrcp);
+    x = (k.mult && dec + ctx > 0) ? xm : x;
+    x = rnd(__builtin_fmaf(-rnd((float)dec), k.fr, x));
+    x = rnd(x - (dec > 0 ? k.pr : 0.0f));
+    x = rnd(x + b);
+    return rnd(x * k.trcp);
+}
+
 // Keys of E elements from their (grammar-masked) logits x, decode counts, context counts and
 // bias bits. Most elements of a row have zero counts and zero bias; for them every penalty and the
 // bias are the identity and the chain reduces to the temperature division, which runs for all
 // elements with one multiply each. Elements with a nonzero count or bias (or every element, when a
 // non-finite frequency penalty turns 0 * f into NaN) then run the full chain one element position
-// at a time, so a wave pays for it only at the positions where one of its lanes holds one.
+// at a time, so a wave pays for it only at the positions where one of its lanes holds one. Every
+// decision that is uniform over the row (divisor form, partial tile) is taken once, outside the
+// per-element code. `ok` marks elements inside the vocabulary; it can be false only when
+// `partial` is set.
 template <int E>
-__device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, const float (&x)[E],
-                                            const bool (&ok)[E], const int32_t (&dec)[E],
-                                            const int32_t (&ctx)[E], const uint32_t (&bb)[E],
-                                            uint32_t (&keys)[E]) {
+__device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial,
+                                            const float (&x)[E], const bool (&ok)[E],
+                                            const int32_t (&dec)[E], const int32_t (&ctx)[E],
+                                            const uint32_t (&bb)[E], uint32_t (&keys)[E]) {
+    float y[E];
+    if (k.temp && k.tdiv.fast) {
 #pragma unroll
-    for (int j = 0; j < E; j += 2) {
-        float y0 = x[j], y1 = x[j + 1];
-        if (k.temp) {
-            y0 = div_bf16(y0, k.tdiv);
-            y1 = div_bf16(y1, k.tdiv);
-        }
-        const f2v v = {y0, y1};
-        const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
-        keys[j] = ok[j] ? (kk & 0xffffu) : 0u;
-        keys[j + 1] = ok[j + 1] ? (kk >> 16) : 0u;
+        for (int j = 0; j < E; ++j) y[j] = x[j] * k.tdiv.rcp;
+    } else if (k.temp) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) y[j] = x[j] / k.tdiv.d;
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) y[j] = x[j];
     }
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
-        if (exc && ok[j]) keys[j] = key_of(chain(k, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
+    for (int j = 0; j < E; j += 2) {
+        const f2v v = {y[j], y[j + 1]};
+        const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
+        keys[j] = kk & 0xffffu;
+        keys[j + 1] = kk >> 16;
+    }
+    if (partial) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) keys[j] = ok[j] ? keys[j] : 0u;
+    }
+    if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
+        const FastChain f = fast_chain(k);
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
+            if (exc && ok[j]) keys[j] = key_of(chain_fast(f, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
+            if (exc && ok[j]) keys[j] = key_of(chain(k, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
+        }
     }
 }
 
@@ -310,10 +362,14 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
         bbits[4 * c + 2] = pl.bw[c].y << 16;
         bbits[4 * c + 3] = pl.bw[c].y & 0xffff0000u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ok[4 * c + i] = in;
-            if (u.g && !((pl.gw[c] >> ((lane4 & 31) + i)) & 1u)) x[4 * c + i] = -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
+    }
+    if (u.g) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                x[4 * c + i] = ((pl.gw[c] >> ((lane4 & 31) + i)) & 1u) ? x[4 * c + i] : -INFINITY;
     }
     if (u.rep && rs.nhist > 0) {
         // The history never counts token 0: the reference pads the history with 0 and then
@@ -324,7 +380,7 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
             for (int j = 0; j < E; ++j) dec[j] += (col0 + tile_col(j) == t && t != 0) ? 1 : 0;
         }
     }
-    finish_keys<E>(k, all_exc, x, ok, dec, ctx, bbits, keys);
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bbits, keys);
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
@@ -412,7 +468,7 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                 bbits[j] = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << 16;
         }
     }
-    finish_keys<E>(k, all_exc, x, ok, dec, ctx, bbits, keys);
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bbits, keys);
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:

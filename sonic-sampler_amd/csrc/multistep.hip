@@ -21,10 +21,20 @@ struct Request {
 __device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, int row) {
     Request r;
     if (a.cu_seqlens) {
+        // Every wave searches on its own: each round tests 64 evenly spaced pivots of (lo, hi), so
+        // one round of loads resolves up to 64 requests and two up to 4096 (cu_seqlens is
+        // non-decreasing, so the pivots at or below `row` are a prefix of the lanes).
+        const int lane = lane_id();
         int lo = 0, hi = a.batch;  // invariant: cu[lo] <= row < cu[hi]
         while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (a.cu_seqlens[mid] <= row) lo = mid; else hi = mid;
+            const int step = (hi - lo + 63) >> 6;
+            const int p = lo + lane * step;
+            const bool le = p < hi && a.cu_seqlens[p] <= row;
+            const uint64_t m = __ballot(le);  // lane 0 (pivot lo) is set unless cu[0] > row
+            if (!m) break;
+            const int k = 63 - __clzll((long long)m);
+            lo += k * step;
+            hi = min(lo + step, hi);
         }
         r.b = lo;
         r.margin = a.cu_seqlens[lo];
@@ -112,12 +122,17 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
 __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
+    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    RowSamples smp;
+    load_samples(scr, tiles, smp);  // depends on the row only: issued first
     const Request rq = resolve_request(a, row);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
-    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
-    const uint32_t ind = a.indicators[slot];
-    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, rq.b) : rq.b;
+    const uint32_t ind = uniform_u16(a.indicators, slot);
+    const int32_t topk = a.top_k ? uniform_i32(a.top_k, slot) : SS_K;
+    const float topp = a.top_p ? bf2f(uniform_u16(a.top_p, slot)) : 1.0f;
+    const float minp = a.min_p ? bf2f(uniform_u16(a.min_p, slot)) : 0.0f;
     float *vrow = a.values + (int64_t)row * SS_K;
     int32_t *irow = a.indices + (int64_t)row * SS_K;
     if (ind & IND_GREEDY) {
@@ -132,10 +147,9 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     }
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
-    merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
     if (threadIdx.x >= 64) return;
-    truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
-             a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
+    truncate(ind, topk, topp, minp, v0, v1);
     float m, x0, x1;
     const float logs = logf(exp_parts(v0, v1, m, x0, x1));
     const int e0 = 2 * threadIdx.x;
@@ -229,7 +243,7 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
             w1 = bf2f(g[c1]);
         }
         const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
-        token = __shfl((sel & 1) ? c1 : c0, sel >> 1, 64);
+        token = lane_i32((sel & 1) ? c1 : c0, sel >> 1);
 
         if (a.return_logprobs && a.logprobs) {
             for (int i = 0; i <= j; ++i) {
@@ -244,7 +258,7 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
                     a.logprobs[rq.margin + i] = (uint16_t)f2bf(vals[(int64_t)i * SS_K + pos]);
             }
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                int lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
+                int lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
                 lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
                 for (int i = 0; i <= j; ++i) {
                     const int64_t o = (int64_t)(rq.margin + i) * a.stride_top;

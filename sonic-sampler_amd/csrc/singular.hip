@@ -64,9 +64,14 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
 __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
-    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
-    const uint32_t ind = a.indicators[slot];
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    RowSamples smp;
+    load_samples(scr, tiles, smp);  // depends on the row only: issued first
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
+    const uint32_t ind = uniform_u16(a.indicators, slot);
+    const int32_t topk = a.top_k ? uniform_i32(a.top_k, slot) : SS_K;
+    const float topp = a.top_p ? bf2f(uniform_u16(a.top_p, slot)) : 1.0f;
+    const float minp = a.min_p ? bf2f(uniform_u16(a.min_p, slot)) : 0.0f;
 
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
@@ -86,13 +91,12 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
 
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
-    merge_row(sm, scr, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
     if (threadIdx.x >= 64) return;
 
     const int lane = threadIdx.x;
     const int e0 = 2 * lane, e1 = e0 + 1;
-    truncate(ind, a.top_k ? a.top_k[slot] : SS_K, a.top_p ? bf2f(a.top_p[slot]) : 1.0f,
-             a.min_p ? bf2f(a.min_p[slot]) : 0.0f, v0, v1);
+    truncate(ind, topk, topp, minp, v0, v1);
     if (a.d2t) {
         i0 = a.d2t[i0];
         i1 = a.d2t[i1];
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
         w1 = bf2f(g[i1]);
     }
     const int sel = wave_argmax_first(rbf(v0 - w0), rbf(v1 - w1));
-    const int token = __shfl((sel & 1) ? i1 : i0, sel >> 1, 64);
+    const int token = lane_i32((sel & 1) ? i1 : i0, sel >> 1);
 
     if (lane == 0 && a.update_counts && a.decode_counts) {
         int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
@@ -135,10 +139,10 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
             o1 = v1 - lse;
         }
         if (want_lp) {
-            const float osel = __shfl((sel & 1) ? o1 : o0, sel >> 1, 64);
+            const float osel = lane_f32((sel & 1) ? o1 : o0, sel >> 1);
             if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                int lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
+                int lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
                 lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
                 const int64_t o = (int64_t)row * a.stride_top;
                 if (e0 < lim) {

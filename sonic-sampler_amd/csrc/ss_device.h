@@ -90,58 +90,118 @@ __device__ __forceinline__ uint64_t xor_lanes(uint64_t v) {
     return ((uint64_t)xor_lanes<LD>((uint32_t)(v >> 32)) << 32) | xor_lanes<LD>((uint32_t)v);
 }
 
+// DPP move with a compile-time control word; lanes whose source is outside the pattern (or whose
+// row is masked off) read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)u);
+    const uint64_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+
+// DPP controls: row_shr:n shifts within each 16-lane row; row_bcast:15 / row_bcast:31 carry lane
+// 15 of each row into the next row, and lane 31 into rows 2 and 3; wave_shr:1 shifts by one lane
+// across the whole wave.
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114,
+              DPP_ROW_SHR8 = 0x118, DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143,
+              DPP_WAVE_SHR1 = 0x138;
+
+// Inclusive prefix sum over the wave's lanes: four in-row shift-and-add steps, then the row
+// carries. Register-to-register, no LDS.
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        uint32_t n = __shfl_up(v, off, 64);
-        if (lane >= off) v += n;
-    }
-    return v;
-}
-
-__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        uint64_t o = __shfl_xor(v, off, 64);
-        v = v > o ? v : o;
-    }
-    return v;
-}
-
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += dpp_u32<DPP_ROW_SHR1>(v);
+    v += dpp_u32<DPP_ROW_SHR2>(v);
+    v += dpp_u32<DPP_ROW_SHR4>(v);
+    v += dpp_u32<DPP_ROW_SHR8>(v);
+    v += dpp_u32<DPP_ROW_BCAST15, 0xa>(v);
+    v += dpp_u32<DPP_ROW_BCAST31, 0xc>(v);
     return v;
 }
 
 __device__ __forceinline__ double wave_inclusive_sum_f64(double v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        double n = __shfl_up(v, off, 64);
-        if (lane >= off) v += n;
-    }
+    v += dpp_f64<DPP_ROW_SHR1>(v);
+    v += dpp_f64<DPP_ROW_SHR2>(v);
+    v += dpp_f64<DPP_ROW_SHR4>(v);
+    v += dpp_f64<DPP_ROW_SHR8>(v);
+    v += dpp_f64<DPP_ROW_BCAST15, 0xa>(v);
+    v += dpp_f64<DPP_ROW_BCAST31, 0xc>(v);
     return v;
 }
+
+// The value of lane - 1 (0 in lane 0).
+__device__ __forceinline__ double shift_up1_f64(double v) { return dpp_f64<DPP_WAVE_SHR1>(v); }
+
+// Reductions by xor butterfly (distances 32, 16, ..., 1); every lane ends with the result.
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+    v += xor_lanes<32>(v);
+    v += xor_lanes<16>(v);
+    v += xor_lanes<8>(v);
+    v += xor_lanes<4>(v);
+    v += xor_lanes<2>(v);
+    v += xor_lanes<1>(v);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, xor_lanes<32>(v));
+    v = max(v, xor_lanes<16>(v));
+    v = max(v, xor_lanes<8>(v));
+    v = max(v, xor_lanes<4>(v));
+    v = max(v, xor_lanes<2>(v));
+    v = max(v, xor_lanes<1>(v));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_u64(v, xor_lanes<32>(v));
+    v = max_u64(v, xor_lanes<16>(v));
+    v = max_u64(v, xor_lanes<8>(v));
+    v = max_u64(v, xor_lanes<4>(v));
+    v = max_u64(v, xor_lanes<2>(v));
+    v = max_u64(v, xor_lanes<1>(v));
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, __uint_as_float(xor_lanes<32>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xor_lanes<16>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xor_lanes<8>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xor_lanes<4>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xor_lanes<2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(xor_lanes<1>(__float_as_uint(v))));
+    return v;
+}
+
+// Sum by the butterfly of a __shfl_xor loop over distances 32, 16, ..., 1, so every lane adds
+// in the same order as that loop would.
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += __uint_as_float(xor_lanes<32>(__float_as_uint(v)));
+    v += __uint_as_float(xor_lanes<16>(__float_as_uint(v)));
+    v += __uint_as_float(xor_lanes<8>(__float_as_uint(v)));
+    v += __uint_as_float(xor_lanes<4>(__float_as_uint(v)));
+    v += __uint_as_float(xor_lanes<2>(__float_as_uint(v)));
+    v += __uint_as_float(xor_lanes<1>(__float_as_uint(v)));
+    return v;
+}
+
+// Value of lane `src` (uniform) in every lane, through the scalar unit.
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int src) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, __builtin_amdgcn_readfirstlane(src));
+}
+
+__device__ __forceinline__ float lane_f32(float v, int src) {
+    return __uint_as_float(lane_u32(__float_as_uint(v), src));
+}
+
+__device__ __forceinline__ int lane_i32(int v, int src) { return (int)lane_u32((uint32_t)v, src); }
 
 // ---------------------------------------------------------------------------------------------
 // Workgroup-wide exclusive prefix sum of NV independent 32-bit lanes of data per thread, in

@@ -722,8 +722,32 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
     }
 }
 
-// Row merge over the tiles' sorted candidate lists. All threads call; on return wave 0 holds the
-// row's top-128 sorted by (value desc, column asc), element e = 2 * lane + i as (v_i, idx_i).
+// The merge inputs of one row, read at the start of a row kernel so that their latency overlaps
+// the reads of the request state: every thread's two sample slots of merge_row, and for wave 0
+// the first unmerged entry of list t = lane (lists from 64 on are read inside the merge).
+struct RowSamples {
+    uint32_t raw[2];
+    uint32_t next;
+};
+
+__device__ __forceinline__ int merge_prefix(int tiles) { return min(SS_K, (4 * SS_K) / tiles); }
+
+__device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, RowSamples &smp) {
+    const int kp = merge_prefix(tiles);
+    const int ns = tiles * kp;  // <= 512
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int s = (int)threadIdx.x + r * SS_BLOCK;
+        const int list = s / kp;
+        smp.raw[r] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
+    }
+    const int t = (int)threadIdx.x;
+    smp.next = (t < 64 && t < tiles && kp < SS_K) ? scr[t * SS_K + kp] : 0u;
+}
+
+// Row merge over the tiles' sorted candidate lists, from the samples of load_samples. All threads
+// call; on return wave 0 holds the row's top-128 sorted by (value desc, column asc), element
+// e = 2 * lane + i as (v_i, idx_i).
 //
 // Only the first kp = min(128, 512 / tiles) entries of every list are merged: 512 sample slots,
 // slot s = list * kp + position, as composites (key << 16) | (0xffff - s), whose order is the
@@ -732,21 +756,20 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
 // of the four runs. The result is exact unless some list holds more than kp of the row's top-128,
 // i.e. unless a list's first unmerged entry beats the 128th merged one; that case (rare: 17 of the
 // top-128 in one of 32 tiles) falls back to the radix merge over every candidate.
-__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, int tiles,
-                                          int block_n, int V, float &v0, float &v1, int &i0,
-                                          int &i1) {
+__device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
+                                          const RowSamples &smp, int tiles, int block_n, int V,
+                                          float &v0, float &v1, int &i0, int &i1) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
-    const int kp = min(SS_K, (4 * SS_K) / tiles);
-    const int ns = tiles * kp;  // <= 512
+    const int kp = merge_prefix(tiles);
     uint32_t c[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int s = (int)threadIdx.x + r * SS_BLOCK;
         uint32_t comp = 0;
-        if (s < ns) {
+        {
             const int list = s / kp;
-            const uint32_t raw = scr[list * SS_K + (s - list * kp)];
+            const uint32_t raw = smp.raw[r];  // 0 past the last slot
             if (raw) {
                 const int idx = list * block_n + (int)(0xffffu - (raw & 0xffffu));
                 sm.col[s] = idx < V ? idx : V - 1;
@@ -776,13 +799,13 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, i
         f1 = max(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
         wave_bitonic128_desc<128>(f0, f1);
         // exactness check: no list's first unmerged entry may beat the 128th merged element
-        const uint32_t last = __shfl(f1, 63, 64);
+        const uint32_t last = lane_u32(f1, 63);
         const uint32_t klast = last >> 16;
         const int ilast = last ? sm.col[0xffffu - (last & 0xffffu)] : V;
         bool beat = false;
         if (kp < SS_K) {
             for (int t = lane; t < tiles; t += 64) {
-                const uint32_t nx = scr[t * SS_K + kp];
+                const uint32_t nx = t < 64 ? smp.next : scr[t * SS_K + kp];
                 const uint32_t kn = nx >> 16;
                 const int in = t * block_n + (int)(0xffffu - (nx & 0xffffu));
                 beat |= nx != 0u && (kn > klast || (kn == klast && in < ilast));
@@ -806,7 +829,7 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr, i
 
 // exp(v - m) for both elements of the lane and the wave-wide sum. m is element 0 (the maximum).
 __device__ __forceinline__ float exp_parts(float v0, float v1, float &m, float &x0, float &x1) {
-    m = __shfl(v0, 0, 64);
+    m = lane_f32(v0, 0);
     x0 = expf(v0 - m);
     x1 = expf(v1 - m);
     return wave_sum_f32(x0 + x1);
@@ -830,8 +853,7 @@ __device__ __forceinline__ void truncate(uint32_t ind, int32_t topk, float topp,
         const float inv = 1.0f / s;
         const float p0 = x0 * inv, p1 = x1 * inv;
         const double inc = wave_inclusive_sum_f64((double)p0 + (double)p1);
-        double exc = __shfl_up(inc, 1, 64);
-        if (lane_id() == 0) exc = 0.0;
+        const double exc = shift_up1_f64(inc);  // 0 in lane 0
         const double c0 = exc + (double)p0, c1 = c0 + (double)p1;
         if (e0 > 0 && (float)c0 > topp) v0 = -INFINITY;
         if ((float)c1 > topp) v1 = -INFINITY;
@@ -842,7 +864,7 @@ __device__ __forceinline__ void truncate(uint32_t ind, int32_t topk, float topp,
         const float s = exp_parts(v0, v1, m, x0, x1);
         const float inv = 1.0f / s;
         const float s0 = rbf(x0 * inv), s1 = rbf(x1 * inv);
-        const float lower = rbf(minp * __shfl(s0, 0, 64));
+        const float lower = rbf(minp * lane_f32(s0, 0));
         if (s0 < lower) v0 = -INFINITY;
         if (s1 < lower) v1 = -INFINITY;
     }

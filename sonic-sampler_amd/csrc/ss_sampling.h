@@ -35,12 +35,11 @@ struct SampleSmem {
 
 // Workgroup memory of the tile kernels.
 struct TileSmem {
-    uint32_t scan[SS_WAVES * 8];
     uint32_t red[SS_WAVES];
-    uint32_t surv[2 * SS_K];    // candidates at or above the tile's lower bound
-    uint32_t run64[4 * 64];     // merge tree: every wave's sorted 64
-    uint32_t run128[2 * SS_K];  // merge tree: the sorted 128-runs of waves 0 and 1
-    int32_t hist[64];           // drafted tokens that extend the decode history
+    uint32_t cnt[SS_WAVES];       // survivors of each wave
+    uint32_t run[SS_WAVES][SS_K];  // each wave's survivors, then its sorted run
+    uint32_t run2[2][SS_K];       // merge tree: the top-128 of runs (0, 1) and (2, 3)
+    int32_t hist[64];             // drafted tokens that extend the decode history
 };
 
 // Request state of one logit row, uniform over the workgroup. Row pointers are already offset to
@@ -506,6 +505,45 @@ __device__ __forceinline__ uint32_t block_count(uint32_t n, uint32_t *red) {
     return s;
 }
 
+__device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// One wave's part of the tile selection: its elements with key > T (or, with EXACT, key == T and
+// column < C) go to the wave's own LDS region as composites (key << 16) | (0xffff - column), placed
+// by ballot and mbcnt, and the wave sorts them there in descending order (zero padded to 128).
+// Returns the wave's survivor count; above 128 the region holds only the first 128, unsorted.
+template <int E, bool EXACT>
+__device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t (&keys)[E],
+                                                   uint32_t T, int C) {
+    const int lane = lane_id();
+    uint32_t *run = sm.run[threadIdx.x >> 6];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const bool p = EXACT ? (keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C)) : keys[j] > T;
+        const uint64_t m = __ballot(p);
+        if (m) {
+            const uint32_t pos = cnt + mbcnt64(m);
+            if (p && pos < (uint32_t)SS_K) run[pos] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
+            cnt += (uint32_t)__popcll(m);
+        }
+    }
+    if (cnt <= 64) {
+        uint32_t v = lane < (int)cnt ? run[lane] : 0u;
+        wave_sort64_desc(v);
+        run[lane] = v;
+        run[64 + lane] = 0u;
+    } else if (cnt <= (uint32_t)SS_K) {
+        uint32_t a0 = 2 * lane < (int)cnt ? run[2 * lane] : 0u;
+        uint32_t a1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0u;
+        wave_bitonic128_desc<2>(a0, a1);
+        run[2 * lane] = a0;
+        run[2 * lane + 1] = a1;
+    }
+    return cnt;
+}
+
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose
 // maximum picks the lowest column among equal maxima. Other rows store their exact top-128 as the
 // same composites, sorted in descending order (0 for absent entries), at scratch[tile * 128 ...].
@@ -513,15 +551,15 @@ __device__ __forceinline__ uint32_t block_count(uint32_t n, uint32_t *red) {
 // The top-128 is found without a selection over the whole tile. Lower bound: per wave, the
 // largest t such that the lanes' largest and second-largest keys include at least 32 keys >= t,
 // so the wave holds at least 32 keys >= t; with lo the smallest of the four wave bounds, the tile
-// holds at least 128 keys >= lo. The survivors (keys >= lo: about 160 of a 4096-wide tile of
-// unstructured logits) are compacted into LDS and sorted by a merge tree: every wave sorts 64 of
-// them, waves 0-1 merge pairs into sorted 128-runs, wave 0 keeps the top-128 of the two runs.
+// holds at least 128 keys >= lo. Every wave then collects its survivors (keys >= lo: about 160 of
+// a 4096-wide tile of unstructured logits, 30-50 per wave) in its own LDS region and sorts them
+// (wave_survivors); a two-level merge tree keeps the top-128 of the four sorted runs.
 //
-// A tile with more than 256 survivors (long runs of equal keys) finds the exact 128th key T by
-// bisection on workgroup counts, then the column cut C of its ties, and keeps the elements with
-// key > T or key == T and column < C: exactly the first 128 of the stable descending order. The
-// cut is expressed through the same (T, C) test the normal path uses with T = lo - 1, C = 0, so
-// both share one compaction.
+// When a wave has more than 128 survivors (long runs of equal keys, or the tile's high values
+// concentrated in one wave), the tile finds the exact 128th key T by bisection on workgroup
+// counts, then the column cut C of its ties, and the waves collect the elements with key > T or
+// key == T and column < C instead: exactly the first 128 of the stable descending order, so no
+// wave can exceed 128.
 template <int E>
 __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint32_t (&keys)[E],
                                            uint32_t *scr, int tile) {
@@ -560,14 +598,10 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
     __syncthreads();
     const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
     uint32_t T = lo ? lo - 1 : 0u;  // key 0 (absent) never survives
-    int C = 0;
-    uint32_t n = 0;
-#pragma unroll
-    for (int j = 0; j < E; ++j) n += keys[j] > T;
-    uint32_t off[1] = {n}, tot[1];
-    block_exclusive_scan<1>(off, tot, sm.scan);
-    uint32_t count = tot[0];
-    if (count > 2 * SS_K) {
+    uint32_t cnt = wave_survivors<E, false>(sm, keys, T, 0);
+    if (lane == 0) sm.cnt[wave] = cnt;
+    __syncthreads();
+    if (max(max(sm.cnt[0], sm.cnt[1]), max(sm.cnt[2], sm.cnt[3])) > (uint32_t)SS_K) {
         uint32_t t = 0;  // the largest t with at least 128 keys >= t
 #pragma unroll 1
         for (int b = 15; b >= 0; --b) {
@@ -591,51 +625,25 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
             for (int j = 0; j < E; ++j) q += (keys[j] == T) & (tile_col(j) <= mid);
             if (block_count(q, sm.red) >= need) chi = mid; else clo = mid + 1;
         }
-        C = clo + 1;
-        n = 0;
-#pragma unroll
-        for (int j = 0; j < E; ++j) n += (keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C));
-        off[0] = n;
-        block_exclusive_scan<1>(off, tot, sm.scan);
-        count = tot[0];
-    }
-    uint32_t pos = off[0];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        if ((keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C)))
-            sm.surv[pos++] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
-    }
-    __syncthreads();
-    {
-        const uint32_t e = 64u * (uint32_t)wave + (uint32_t)lane;
-        uint32_t v = e < count ? sm.surv[e] : 0u;
-        if (count > 64u * (uint32_t)wave) wave_sort64_desc(v);
-        sm.run64[e] = v;
-    }
-    __syncthreads();
-    if (wave < 2) {
-        // runs 2w and 2w+1, the second reversed, form a bitonic sequence of 128
-        const uint32_t *A = sm.run64 + 128 * wave, *B = A + 64;
-        uint32_t a0 = lane < 32 ? A[2 * lane] : B[127 - 2 * lane];
-        uint32_t a1 = lane < 32 ? A[2 * lane + 1] : B[126 - 2 * lane];
-        if (count > 128u * (uint32_t)wave + 64u) wave_bitonic128_desc<128>(a0, a1);
-        if (count <= (uint32_t)SS_K) {
-            if (wave == 0) *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(a0, a1);
-        } else {
-            sm.run128[SS_K * wave + 2 * lane] = a0;
-            sm.run128[SS_K * wave + 2 * lane + 1] = a1;
-        }
-    }
-    if (count > (uint32_t)SS_K) {
+        wave_survivors<E, true>(sm, keys, T, clo + 1);
         __syncthreads();
-        if (wave == 0) {
-            // the elementwise maximum against the reversed second run is a bitonic sequence
-            // holding the top-128 of both
-            uint32_t c0 = max(sm.run128[2 * lane], sm.run128[SS_K + 127 - 2 * lane]);
-            uint32_t c1 = max(sm.run128[2 * lane + 1], sm.run128[SS_K + 126 - 2 * lane]);
-            wave_bitonic128_desc<128>(c0, c1);
-            *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(c0, c1);
-        }
+    }
+    if (wave < 2) {
+        // runs 2w and 2w+1, the second reversed: the elementwise maximum is a bitonic sequence
+        // holding the top-128 of both
+        const uint32_t *A = sm.run[2 * wave], *B = sm.run[2 * wave + 1];
+        uint32_t a0 = max(A[2 * lane], B[127 - 2 * lane]);
+        uint32_t a1 = max(A[2 * lane + 1], B[126 - 2 * lane]);
+        wave_bitonic128_desc<128>(a0, a1);
+        sm.run2[wave][2 * lane] = a0;
+        sm.run2[wave][2 * lane + 1] = a1;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t c0 = max(sm.run2[0][2 * lane], sm.run2[1][127 - 2 * lane]);
+        uint32_t c1 = max(sm.run2[0][2 * lane + 1], sm.run2[1][126 - 2 * lane]);
+        wave_bitonic128_desc<128>(c0, c1);
+        *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(c0, c1);
     }
 }
 

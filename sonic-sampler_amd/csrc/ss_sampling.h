@@ -182,55 +182,61 @@ __device__ __forceinline__ float chain_fast(const FastChain &k, float x, int32_t
     return rnd(x * k.trcp);
 }
 
+// Branch-free chain with IEEE divisions, for rows whose divisors have no exact reciprocal (zero,
+// infinite, NaN or extreme). Applied to every element it equals the gated chain: for an element
+// with zero counts and bias every processor but the temperature is the identity (up to the sign
+// of a zero, which keys do not see).
+__device__ __forceinline__ float chain_ieee(const Chain &k, float x, int32_t dec, int32_t ctx,
+                                            float b) {
+    const float xm = rnd(x < 0.0f ? x * k.rep : x / k.rdiv.d);
+    x = (k.mult && dec + ctx > 0) ? xm : x;
+    x = rnd(__builtin_fmaf(-rnd((float)dec), k.freq ? k.fr : 0.0f, x));
+    x = rnd(x - (dec > 0 && k.pres ? k.pr : 0.0f));
+    x = rnd(x + b);
+    return k.temp ? rnd(x / k.tdiv.d) : x;
+}
+
 // Keys of E elements from their (grammar-masked) logits x, decode counts, context counts and
 // bias bits. Most elements of a row have zero counts and zero bias; for them every penalty and the
 // bias are the identity and the chain reduces to the temperature division, which runs for all
 // elements with one multiply each. Elements with a nonzero count or bias (or every element, when a
 // non-finite frequency penalty turns 0 * f into NaN) then run the full chain one element position
-// at a time, so a wave pays for it only at the positions where one of its lanes holds one. Every
-// decision that is uniform over the row (divisor form, partial tile) is taken once, outside the
-// per-element code. `ok` marks elements inside the vocabulary; it can be false only when
-// `partial` is set.
-template <int E>
-__device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial,
-                                            const float (&x)[E], const bool (&ok)[E],
-                                            const int32_t (&dec)[E], const int32_t (&ctx)[E],
-                                            const uint32_t (&bb)[E], uint32_t (&keys)[E]) {
-    float y[E];
-    if (k.temp && k.tdiv.fast) {
+// at a time, so a wave pays for it only at the positions where one of its lanes holds one. Rows
+// whose divisors have no exact reciprocal take the IEEE chain on every element instead. `ok` marks
+// elements inside the vocabulary; it can be false only when `partial` is set. x(j) and bb(j) return
+// the (grammar-masked) logit and the bias bits of element j.
+template <int E, class XOf, class BiasOf>
+__device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial, XOf x,
+                                            const bool (&ok)[E], const int32_t (&dec)[E],
+                                            const int32_t (&ctx)[E], BiasOf bb,
+                                            uint32_t (&keys)[E]) {
+    if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
+        const FastChain f = fast_chain(k);
 #pragma unroll
-        for (int j = 0; j < E; ++j) y[j] = x[j] * k.tdiv.rcp;
-    } else if (k.temp) {
+        for (int j = 0; j < E; j += 2) {
+            const f2v v = {x(j) * f.trcp, x(j + 1) * f.trcp};
+            const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
+            keys[j] = kk & 0xffffu;
+            keys[j + 1] = kk >> 16;
+        }
+        // The branch at each element position is on the wave's ballot, so it is uniform: the
+        // chain then runs with every lane active and its result is selected.
 #pragma unroll
-        for (int j = 0; j < E; ++j) y[j] = x[j] / k.tdiv.d;
+        for (int j = 0; j < E; ++j) {
+            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb(j) << 1)) != 0u;
+            if (__ballot(exc)) {
+                const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
+                keys[j] = exc ? kc : keys[j];
+            }
+        }
     } else {
 #pragma unroll
-        for (int j = 0; j < E; ++j) y[j] = x[j];
-    }
-#pragma unroll
-    for (int j = 0; j < E; j += 2) {
-        const f2v v = {y[j], y[j + 1]};
-        const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
-        keys[j] = kk & 0xffffu;
-        keys[j + 1] = kk >> 16;
+        for (int j = 0; j < E; ++j)
+            keys[j] = key_of(chain_ieee(k, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
     }
     if (partial) {
 #pragma unroll
         for (int j = 0; j < E; ++j) keys[j] = ok[j] ? keys[j] : 0u;
-    }
-    if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
-        const FastChain f = fast_chain(k);
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
-            if (exc && ok[j]) keys[j] = key_of(chain_fast(f, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb[j] << 1)) != 0u;
-            if (exc && ok[j]) keys[j] = key_of(chain(k, x[j], dec[j], ctx[j], __uint_as_float(bb[j])));
-        }
     }
 }
 
@@ -336,39 +342,35 @@ __device__ __forceinline__ void issue_planes(const RowState &rs, const Uses &u, 
 
 template <int E>
 __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, int col0, int V,
-                                            const int32_t *hist, const u32x2 (&lw)[E / 4],
+                                            const int32_t *hist, const u32x2 (&lw_in)[E / 4],
                                             const Planes<E> &pl, uint32_t (&keys)[E]) {
     constexpr int NCH = E / 4;
     const int lane4 = (int)threadIdx.x * 4;
     bool all_exc;
     const Chain k = row_chain(rs, u, all_exc);
-    float x[E];
+    // logits and bias stay in their loaded bf16 pairs and are widened where they are used
+    u32x2 lw[NCH];
     bool ok[E];
     int32_t dec[E], ctx[E];
-    uint32_t bbits[E];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int base = col0 + c * (SS_BLOCK * 4);
-        const bool in = base + lane4 < V;
-        x[4 * c + 0] = __uint_as_float(lw[c].x << 16);
-        x[4 * c + 1] = __uint_as_float(lw[c].x & 0xffff0000u);
-        x[4 * c + 2] = __uint_as_float(lw[c].y << 16);
-        x[4 * c + 3] = __uint_as_float(lw[c].y & 0xffff0000u);
+        lw[c] = lw_in[c];
+        const bool in = col0 + c * (SS_BLOCK * 4) + lane4 < V;
         dec[4 * c + 0] = pl.dw[c].x; dec[4 * c + 1] = pl.dw[c].y; dec[4 * c + 2] = pl.dw[c].z; dec[4 * c + 3] = pl.dw[c].w;
         ctx[4 * c + 0] = pl.cw[c].x; ctx[4 * c + 1] = pl.cw[c].y; ctx[4 * c + 2] = pl.cw[c].z; ctx[4 * c + 3] = pl.cw[c].w;
-        bbits[4 * c + 0] = pl.bw[c].x << 16;
-        bbits[4 * c + 1] = pl.bw[c].x & 0xffff0000u;
-        bbits[4 * c + 2] = pl.bw[c].y << 16;
-        bbits[4 * c + 3] = pl.bw[c].y & 0xffff0000u;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
     }
     if (u.g) {
+        // a masked element becomes bf16 -inf (0xff80) in place
 #pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                x[4 * c + i] = ((pl.gw[c] >> ((lane4 & 31) + i)) & 1u) ? x[4 * c + i] : -INFINITY;
+        for (int c = 0; c < NCH; ++c) {
+            const uint32_t g = pl.gw[c] >> (lane4 & 31);
+            lw[c].x = (g & 1u) ? lw[c].x : ((lw[c].x & 0xffff0000u) | 0xff80u);
+            lw[c].x = (g & 2u) ? lw[c].x : ((lw[c].x & 0x0000ffffu) | 0xff800000u);
+            lw[c].y = (g & 4u) ? lw[c].y : ((lw[c].y & 0xffff0000u) | 0xff80u);
+            lw[c].y = (g & 8u) ? lw[c].y : ((lw[c].y & 0x0000ffffu) | 0xff800000u);
+        }
     }
     if (u.rep && rs.nhist > 0) {
         // The history never counts token 0: the reference pads the history with 0 and then
@@ -379,7 +381,15 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
             for (int j = 0; j < E; ++j) dec[j] += (col0 + tile_col(j) == t && t != 0) ? 1 : 0;
         }
     }
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bbits, keys);
+    auto x = [&](int j) {
+        const uint32_t w = (j & 2) ? lw[j >> 2].y : lw[j >> 2].x;
+        return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+    };
+    auto bb = [&](int j) {
+        const uint32_t w = (j & 2) ? pl.bw[j >> 2].y : pl.bw[j >> 2].x;
+        return (j & 1) ? (w & 0xffff0000u) : (w << 16);
+    };
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bb, keys);
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
@@ -467,7 +477,8 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                 bbits[j] = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << 16;
         }
     }
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bbits, keys);
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, [&](int j) { return x[j]; }, ok, dec, ctx,
+                   [&](int j) { return bbits[j]; }, keys);
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:
@@ -734,20 +745,39 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
 // the reads of the request state: every thread's two sample slots of merge_row, and for wave 0
 // the first unmerged entry of list t = lane (lists from 64 on are read inside the merge).
 struct RowSamples {
-    uint32_t raw[2];
+    uint32_t raw[2];   // list entries of the thread's two elements (0 past the last slot)
+    int slot[2];       // their sample slots s = list * kp + position
     uint32_t next;
 };
 
 __device__ __forceinline__ int merge_prefix(int tiles) { return min(SS_K, (4 * SS_K) / tiles); }
 
+// Run length of whole sorted lists placed in a wave's 128 elements: kp when kp is a power of two
+// from 8 to 64 (then 128 / kp lists per wave, odd ones reversed, so that the bitonic network can
+// start at merge size 2 kp), else 1 (arbitrary placement, full sort).
+__device__ __forceinline__ int merge_run(int kp) {
+    return (kp >= 8 && kp <= 64 && (kp & (kp - 1)) == 0) ? kp : 1;
+}
+
 __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, RowSamples &smp) {
     const int kp = merge_prefix(tiles);
     const int ns = tiles * kp;  // <= 512
+    const int run = merge_run(kp);
+    const int wave = (int)threadIdx.x >> 6, lane = lane_id();
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int s = (int)threadIdx.x + r * SS_BLOCK;
+    for (int i = 0; i < 2; ++i) {
+        int s;
+        if (run > 1) {
+            // element e = 2 * lane + i of the wave: run r = e / kp, i.e. list 128 / kp * wave + r
+            const int e = 2 * lane + i;
+            const int r = e / run, q = e - r * run;
+            s = (wave * (SS_K / run) + r) * run + ((r & 1) ? run - 1 - q : q);
+        } else {
+            s = 2 * ((int)threadIdx.x & ~63) + 2 * lane + i;  // any placement
+        }
         const int list = s / kp;
-        smp.raw[r] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
+        smp.slot[i] = s;
+        smp.raw[i] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
     }
     const int t = (int)threadIdx.x;
     smp.next = (t < 64 && t < tiles && kp < SS_K) ? scr[t * SS_K + kp] : 0u;
@@ -760,8 +790,8 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, Row
 // Only the first kp = min(128, 512 / tiles) entries of every list are merged: 512 sample slots,
 // slot s = list * kp + position, as composites (key << 16) | (0xffff - s), whose order is the
 // (value desc, column asc) order because lists are in tile order and equal keys of one list are
-// in column order. Each wave sorts 128 slots, and two rounds of bitonic merges keep the top-128
-// of the four runs. The result is exact unless some list holds more than kp of the row's top-128,
+// in column order. Each wave sorts 128 slots (from merge size 2 kp when whole lists fill its
+// elements, see merge_run), and two rounds of bitonic merges keep the top-128 of the four runs. The result is exact unless some list holds more than kp of the row's top-128,
 // i.e. unless a list's first unmerged entry beats the 128th merged one; that case (rare: 17 of the
 // top-128 in one of 32 tiles) falls back to the radix merge over every candidate.
 __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
@@ -772,21 +802,26 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
     const int kp = merge_prefix(tiles);
     uint32_t c[2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int s = (int)threadIdx.x + r * SS_BLOCK;
+    for (int i = 0; i < 2; ++i) {
+        const int s = smp.slot[i];
         uint32_t comp = 0;
-        {
-            const int list = s / kp;
-            const uint32_t raw = smp.raw[r];  // 0 past the last slot
-            if (raw) {
-                const int idx = list * block_n + (int)(0xffffu - (raw & 0xffffu));
-                sm.col[s] = idx < V ? idx : V - 1;
-                comp = (raw & 0xffff0000u) | (0xffffu - (uint32_t)s);
-            }
+        const uint32_t raw = smp.raw[i];
+        if (raw) {
+            const int idx = (s / kp) * block_n + (int)(0xffffu - (raw & 0xffffu));
+            sm.col[s] = idx < V ? idx : V - 1;
+            comp = (raw & 0xffff0000u) | (0xffffu - (uint32_t)s);
         }
-        c[r] = comp;
+        c[i] = comp;
     }
-    wave_bitonic128_desc<2>(c[0], c[1]);
+    // sorted lists in alternating directions are already the runs of a bitonic network of size
+    // 2 * run; equal composites cannot occur (the slot is part of them)
+    switch (merge_run(kp)) {
+        case 8: wave_bitonic128_desc<16>(c[0], c[1]); break;
+        case 16: wave_bitonic128_desc<32>(c[0], c[1]); break;
+        case 32: wave_bitonic128_desc<64>(c[0], c[1]); break;
+        case 64: wave_bitonic128_desc<128>(c[0], c[1]); break;
+        default: wave_bitonic128_desc<2>(c[0], c[1]); break;
+    }
     sm.runs[wave][2 * lane] = c[0];
     sm.runs[wave][2 * lane + 1] = c[1];
     __syncthreads();

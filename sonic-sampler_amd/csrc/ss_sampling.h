@@ -35,6 +35,7 @@ struct SampleSmem {
 
 // Workgroup memory of the tile kernels.
 struct TileSmem {
+    uint32_t scan[SS_WAVES * 8];  // workgroup scans of up to 8 values per thread
     uint32_t red[SS_WAVES];
     uint32_t cnt[SS_WAVES];       // survivors of each wave
     uint32_t run[SS_WAVES][SS_K];  // each wave's survivors, then its sorted run
@@ -441,8 +442,18 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
         for (int j = 0; j < E; ++j) tcol[j] = col0 + tile_col(j);
         if (u.remap) {
             const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)V * 4);
+            if (VEC) {
+                // the 4 columns of a chunk are consecutive (and V % 4 == 0): one 16-byte load
 #pragma unroll
-            for (int j = 0; j < E; ++j) tcol[j] = __builtin_amdgcn_raw_buffer_load_b32(m, tcol[j] * 4, 0, 0);
+                for (int c = 0; c < NCH; ++c) {
+                    const i32x4 t = __builtin_bit_cast(
+                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(m, lane4 * 4, (col0 + c * (SS_BLOCK * 4)) * 4, 0));
+                    tcol[4 * c + 0] = t.x; tcol[4 * c + 1] = t.y; tcol[4 * c + 2] = t.z; tcol[4 * c + 3] = t.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < E; ++j) tcol[j] = __builtin_amdgcn_raw_buffer_load_b32(m, tcol[j] * 4, 0, 0);
+            }
         }
         if (u.g) {
             const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
@@ -520,19 +531,19 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// One wave's part of the tile selection: its elements with key > T (or, with EXACT, key == T and
-// column < C) go to the wave's own LDS region as composites (key << 16) | (0xffff - column), placed
+// One wave's part of the tile selection: its elements with key > T (or, with EXACT, those key == T
+// elements whose bit is set in tie_keep) go to the wave's own LDS region as composites (key << 16) | (0xffff - column), placed
 // by ballot and mbcnt, and the wave sorts them there in descending order (zero padded to 128).
 // Returns the wave's survivor count; above 128 the region holds only the first 128, unsorted.
 template <int E, bool EXACT>
 __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t (&keys)[E],
-                                                   uint32_t T, int C) {
+                                                   uint32_t T, uint32_t tie_keep) {
     const int lane = lane_id();
     uint32_t *run = sm.run[threadIdx.x >> 6];
     uint32_t cnt = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const bool p = EXACT ? (keys[j] > T) | ((keys[j] == T) & (tile_col(j) < C)) : keys[j] > T;
+        const bool p = EXACT ? (keys[j] > T) | (((tie_keep >> j) & 1u) != 0u) : keys[j] > T;
         const uint64_t m = __ballot(p);
         if (m) {
             const uint32_t pos = cnt + mbcnt64(m);
@@ -566,11 +577,13 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t 
 // a 4096-wide tile of unstructured logits, 30-50 per wave) in its own LDS region and sorts them
 // (wave_survivors); a two-level merge tree keeps the top-128 of the four sorted runs.
 //
-// When a wave has more than 128 survivors (long runs of equal keys, or the tile's high values
-// concentrated in one wave), the tile finds the exact 128th key T by bisection on workgroup
-// counts, then the column cut C of its ties, and the waves collect the elements with key > T or
-// key == T and column < C instead: exactly the first 128 of the stable descending order, so no
-// wave can exceed 128.
+// When a wave has more than 128 survivors (long runs of equal keys such as the -inf of
+// grammar-masked elements, or the tile's high values concentrated in one wave), the tile finds
+// the exact 128th key T (the bound itself when the ties sit there, confirmed by one pair of
+// counts; otherwise by bisection on workgroup counts) and ranks the keys equal to T in column
+// order with one workgroup scan; the waves then collect the elements with key > T and the first
+// 128 - #(key > T) of the ties: exactly the first 128 of the stable descending order, so no wave
+// can exceed 128.
 template <int E>
 __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint32_t (&keys)[E],
                                            uint32_t *scr, int tile) {
@@ -609,34 +622,65 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
     __syncthreads();
     const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
     uint32_t T = lo ? lo - 1 : 0u;  // key 0 (absent) never survives
-    uint32_t cnt = wave_survivors<E, false>(sm, keys, T, 0);
+    uint32_t cnt = wave_survivors<E, false>(sm, keys, T, 0u);
     if (lane == 0) sm.cnt[wave] = cnt;
     __syncthreads();
     if (max(max(sm.cnt[0], sm.cnt[1]), max(sm.cnt[2], sm.cnt[3])) > (uint32_t)SS_K) {
-        uint32_t t = 0;  // the largest t with at least 128 keys >= t
+        // Exact cut. T is the 128th key: usually the bound itself (ties at lo, e.g. the -inf of
+        // grammar-masked elements), which one pair of counts confirms; otherwise bisection.
+        uint32_t gt = 0, ge = 0;
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            gt += keys[j] > lo;
+            ge += keys[j] >= lo;
+        }
+        const uint32_t above_lo = block_count(gt, sm.red), from_lo = block_count(ge, sm.red);
+        uint32_t above;  // keys > T
+        if (lo != 0 && above_lo < (uint32_t)SS_K && from_lo >= (uint32_t)SS_K) {
+            T = lo;
+            above = above_lo;
+        } else {
+            uint32_t t = 0;  // the largest t with at least 128 keys >= t
 #pragma unroll 1
-        for (int b = 15; b >= 0; --b) {
-            const uint32_t c = t | (1u << b);
+            for (int b = 15; b >= 0; --b) {
+                const uint32_t c = t | (1u << b);
+                uint32_t k = 0;
+#pragma unroll
+                for (int j = 0; j < E; ++j) k += keys[j] >= c;
+                if (block_count(k, sm.red) >= (uint32_t)SS_K) t = c;
+            }
+            T = t;
             uint32_t k = 0;
 #pragma unroll
-            for (int j = 0; j < E; ++j) k += keys[j] >= c;
-            if (block_count(k, sm.red) >= (uint32_t)SS_K) t = c;
+            for (int j = 0; j < E; ++j) k += keys[j] > T;
+            above = block_count(k, sm.red);
         }
-        T = t;
-        uint32_t k = 0;
+        // The first `need` keys equal to T in column order (chunk, thread, element) are kept: their
+        // ranks come from one workgroup scan of the per-chunk tie counts.
+        const uint32_t need = (uint32_t)SS_K - above;
+        constexpr int NCH = E / 4;
+        uint32_t eq[NCH], tot[NCH];
 #pragma unroll
-        for (int j = 0; j < E; ++j) k += keys[j] > T;
-        const uint32_t need = (uint32_t)SS_K - block_count(k, sm.red);
-        int clo = 0, chi = SS_BLOCK * E;  // the smallest column with `need` ties at or before it
-#pragma unroll 1
-        while (clo < chi) {
-            const int mid = (clo + chi) >> 1;
-            uint32_t q = 0;
+        for (int c = 0; c < NCH; ++c) {
+            eq[c] = 0;
 #pragma unroll
-            for (int j = 0; j < E; ++j) q += (keys[j] == T) & (tile_col(j) <= mid);
-            if (block_count(q, sm.red) >= need) chi = mid; else clo = mid + 1;
+            for (int i = 0; i < 4; ++i) eq[c] += keys[4 * c + i] == T;
         }
-        wave_survivors<E, true>(sm, keys, T, clo + 1);
+        block_exclusive_scan<NCH>(eq, tot, sm.scan);
+        uint32_t tie_keep = 0, before = 0;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            uint32_t r = before + eq[c];  // rank of this thread's first tie in chunk c
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (keys[4 * c + i] == T) {
+                    tie_keep |= (r < need ? 1u : 0u) << (4 * c + i);
+                    ++r;
+                }
+            }
+            before += tot[c];
+        }
+        wave_survivors<E, true>(sm, keys, T, tie_keep);
         __syncthreads();
     }
     if (wave < 2) {

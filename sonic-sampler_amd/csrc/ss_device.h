@@ -192,6 +192,14 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     return v;
 }
 
+// b in the lanes whose bit of the wave-uniform mask m is set, a in the others: one v_cndmask with
+// the mask as its lane-select operand.
+__device__ __forceinline__ uint32_t lane_select(uint64_t m, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(m));
+    return r;
+}
+
 // Value of lane `src` (uniform) in every lane, through the scalar unit.
 __device__ __forceinline__ uint32_t lane_u32(uint32_t v, int src) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, __builtin_amdgcn_readfirstlane(src));

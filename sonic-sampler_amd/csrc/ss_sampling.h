@@ -38,7 +38,7 @@ struct TileSmem {
     uint32_t scan[SS_WAVES * 8];  // workgroup scans of up to 8 values per thread
     uint32_t red[SS_WAVES];
     uint32_t cnt[SS_WAVES];       // survivors of each wave
-    uint32_t run[SS_WAVES][SS_K];  // each wave's survivors, then its sorted run
+    uint32_t run[SS_WAVES][SS_K + 64];  // each wave's survivors, then its sorted run
     uint32_t run2[2][SS_K];       // merge tree: the top-128 of runs (0, 1) and (2, 3)
     int32_t hist[64];             // drafted tokens that extend the decode history
 };
@@ -79,8 +79,9 @@ __device__ __forceinline__ void round_all(float (&x)[E]) {
     for (int j = 0; j < E; j += 2) round_pair(x[j], x[j + 1]);
 }
 
-// Divisor state of a per-row constant d: rcp = RN(1/d); `fast` is false when d is 0, infinite
-// or NaN, where the plain IEEE quotient is used instead.
+// Divisor state of a per-row constant d: rcp = 1/d from v_rcp_f32 (within 1 ulp); `fast` is
+// false when d is 0, infinite or NaN or the reciprocal is not a finite nonzero value, where the
+// plain IEEE quotient is used instead.
 struct Divisor {
     float d, rcp;
     bool fast;
@@ -89,22 +90,28 @@ struct Divisor {
 __device__ __forceinline__ Divisor make_divisor(float d) {
     Divisor v;
     v.d = d;
-    v.rcp = 1.0f / d;
+    v.rcp = __builtin_amdgcn_rcpf(d);
     v.fast = d != 0.0f && __builtin_isfinite(d) && __builtin_isfinite(v.rcp) && v.rcp != 0.0f;
     return v;
 }
 
 // x / d for bf16 x and d, valid as the input of a bf16 rounding. Both carry 8 significant bits, so
 // x / d is either exact with at most 8 significant bits (a bf16 value) or at least 2^-17 (relative)
-// away from every bf16 rounding boundary, since a boundary needs 9 significant bits. x * RN(1/d)
-// is within 2^-23 of x / d, so its bf16 rounding equals that of torch's correctly rounded fp32
-// quotient.
+// away from every bf16 rounding boundary, since a boundary needs 9 significant bits. x * rcp with
+// rcp within 1 ulp of 1/d is within 2^-22 of x / d, so its bf16 rounding equals that of torch's
+// correctly rounded fp32 quotient.
 __device__ __forceinline__ float div_bf16(float x, const Divisor &v) {
     return v.fast ? x * v.rcp : x / v.d;
 }
 
-// Order-preserving 16-bit key (key16) of a bf16-exact float.
-__device__ __forceinline__ uint32_t key_of(float x) { return key16(__float_as_uint(x) >> 16); }
+// Order-preserving 16-bit key (key16) of a bf16-exact float: 0x8000 plus the signed magnitude
+// of its top 16 bits (negation by xor with the sign mask and subtraction of it).
+__device__ __forceinline__ uint32_t key_of(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t s = (uint32_t)((int32_t)u >> 31);
+    const uint32_t m = (u >> 16) & 0x7fffu;
+    return ((m ^ s) - s) + 0x8000u;
+}
 
 // Raw buffer view of one row: loads past `bytes` return 0 without faulting, so every load below is
 // unconditional. Descriptor word 3 for gfx9-family raw buffers.
@@ -126,11 +133,11 @@ __device__ __forceinline__ uint32_t packed_keys(uint32_t u) {
     return (neg & m) | ((u | 0x80008000u) & ~m);
 }
 
-// bf16 rounding of one value (round-to-nearest-even).
+// bf16 rounding of one value (round-to-nearest-even): converted into the high half of a packed
+// pair whose low half is bf16(0) = 0, the register is the rounded value as a float.
 __device__ __forceinline__ float rnd(float a) {
-    float b = a;
-    round_pair(a, b);
-    return a;
+    const f2v v = {0.0f, a};
+    return __uint_as_float(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
 }
 
 // Processor constants of one row, uniform over the workgroup.
@@ -205,11 +212,12 @@ __device__ __forceinline__ float chain_ieee(const Chain &k, float x, int32_t dec
 // at a time, so a wave pays for it only at the positions where one of its lanes holds one. Rows
 // whose divisors have no exact reciprocal take the IEEE chain on every element instead. `ok` marks
 // elements inside the vocabulary; it can be false only when `partial` is set. x(j) and bb(j) return
-// the (grammar-masked) logit and the bias bits of element j.
-template <int E, class XOf, class BiasOf>
+// the (grammar-masked) logit and the bias bits of element j; bw(j) is nonzero whenever element j's
+// bias is nonzero (it may also be nonzero for a zero bias: the chain is exact for every element).
+template <int E, class XOf, class BiasOf, class BiasWordOf>
 __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial, XOf x,
                                             const bool (&ok)[E], const int32_t (&dec)[E],
-                                            const int32_t (&ctx)[E], BiasOf bb,
+                                            const int32_t (&ctx)[E], BiasOf bb, BiasWordOf bw,
                                             uint32_t (&keys)[E]) {
     if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
         const FastChain f = fast_chain(k);
@@ -221,13 +229,14 @@ __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool p
             keys[j + 1] = kk >> 16;
         }
         // The branch at each element position is on the wave's ballot, so it is uniform: the
-        // chain then runs with every lane active and its result is selected.
+        // chain then runs with every lane active and the ballot selects its result.
+        const uint64_t forced = all_exc ? ~0ull : 0ull;
 #pragma unroll
         for (int j = 0; j < E; ++j) {
-            const bool exc = all_exc || ((uint32_t)(dec[j] | ctx[j]) | (bb(j) << 1)) != 0u;
-            if (__ballot(exc)) {
+            const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u) | forced;
+            if (m) {
                 const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
-                keys[j] = exc ? kc : keys[j];
+                keys[j] = lane_select(m, keys[j], kc);
             }
         }
     } else {
@@ -376,10 +385,15 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
     if (u.rep && rs.nhist > 0) {
         // The history never counts token 0: the reference pads the history with 0 and then
         // restores the original count of token 0 (core/naive.py:179-203).
+        // Offset of the token from the lane's element 0, compared with each element's constant
+        // offset (j / 4) * 1024 + j % 4, so no per-element column is kept live.
+        const int base = col0 + 4 * (int)threadIdx.x;
         for (int h = 0; h < rs.nhist; ++h) {
             const int t = hist[h];
+            if (t == 0) continue;
+            const int d = t - base;
 #pragma unroll
-            for (int j = 0; j < E; ++j) dec[j] += (col0 + tile_col(j) == t && t != 0) ? 1 : 0;
+            for (int j = 0; j < E; ++j) dec[j] += d == (j >> 2) * (SS_BLOCK * 4) + (j & 3) ? 1 : 0;
         }
     }
     auto x = [&](int j) {
@@ -390,7 +404,9 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
         const uint32_t w = (j & 2) ? pl.bw[j >> 2].y : pl.bw[j >> 2].x;
         return (j & 1) ? (w & 0xffff0000u) : (w << 16);
     };
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bb, keys);
+    // the bias word of the element's pair, shifted so that -0 in the high half does not count
+    auto bw = [&](int j) { return ((j & 2) ? pl.bw[j >> 2].y : pl.bw[j >> 2].x) << 1; };
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bb, bw, keys);
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
@@ -489,7 +505,7 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
         }
     }
     finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, [&](int j) { return x[j]; }, ok, dec, ctx,
-                   [&](int j) { return bbits[j]; }, keys);
+                   [&](int j) { return bbits[j]; }, [&](int j) { return bbits[j] << 1; }, keys);
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:
@@ -539,17 +555,19 @@ template <int E, bool EXACT>
 __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t (&keys)[E],
                                                    uint32_t T, uint32_t tie_keep) {
     const int lane = lane_id();
-    uint32_t *run = sm.run[threadIdx.x >> 6];
+    uint32_t *run = sm.run[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
+    // 0xffff - column of the lane's element 0; element j subtracts its offset (j / 4) * 1024 + j % 4
+    const uint32_t cb = 0xffffu - 4u * threadIdx.x;
+    // Wave-uniform count, saturated at SS_K + 1: positions stay below SS_K + 64, inside the run,
+    // and a count above SS_K still reads as an overflow.
     uint32_t cnt = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const bool p = EXACT ? (keys[j] > T) | (((tie_keep >> j) & 1u) != 0u) : keys[j] > T;
         const uint64_t m = __ballot(p);
-        if (m) {
-            const uint32_t pos = cnt + mbcnt64(m);
-            if (p && pos < (uint32_t)SS_K) run[pos] = (keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j));
-            cnt += (uint32_t)__popcll(m);
-        }
+        uint32_t *at = run + cnt;  // uniform
+        if (p) at[mbcnt64(m)] = ((keys[j] << 16) | cb) - (uint32_t)((j >> 2) * (SS_BLOCK * 4) + (j & 3));
+        cnt = min(cnt + (uint32_t)__popcll(m), (uint32_t)SS_K + 1u);
     }
     if (cnt <= 64) {
         uint32_t v = lane < (int)cnt ? run[lane] : 0u;

@@ -157,41 +157,104 @@ __device__ __forceinline__ int order_pos(int sc, int j) {
     return sc * (SS_BLOCK * E) + (j / CH) * (SS_BLOCK * CH) + (int)threadIdx.x * CH + (j % CH);
 }
 
-// One compare-exchange step at lane distance LD of a bitonic network whose merge runs have the
-// direction `desc`; every element of the lane pairs with the same element of lane (lane ^ LD).
-template <int LD, int N, typename T>
-__device__ __forceinline__ void bitonic_lane_step(T (&a)[N], bool desc) {
-    const bool keep_hi = ((lane_id() & LD) == 0) == desc;  // the lower lane keeps the max
+// Lane mask of one compare-exchange step at lane distance LD: bit l is set when lane l keeps the
+// larger value of its pair, i.e. when it is the pair's lower lane (bit LD clear) in a descending
+// run or its upper lane in an ascending one. The run of lane l descends when bit DB of l is clear
+// (DB = 64: every run descends).
+constexpr uint64_t keep_hi_mask(int LD, int DB) {
+    uint64_t m = 0;
+    for (int l = 0; l < 64; ++l)
+        if (((l & LD) == 0) == ((l & DB) == 0)) m |= 1ull << l;
+    return m;
+}
+
+// Lanes whose run descends (bit DB clear).
+constexpr uint64_t desc_mask(int DB) { return keep_hi_mask(0, DB); }
+
+// Larger and smaller of a and the value of lane (lane ^ LD).
+template <int LD>
+__device__ __forceinline__ void pair_max_min(uint32_t a, uint32_t &hi, uint32_t &lo) {
+    static_assert(LD == 1 || LD == 2 || LD == 4 || LD == 8 || LD == 16 || LD == 32, "lane distance");
+    if constexpr (LD == 1 || LD == 2 || LD == 8) {
+        // quad_perm [1,0,3,2] / [2,3,0,1] and row_ror:8 are exact xor permutations; a DPP move
+        // that writes every lane and has no old value folds into the max and the min as their DPP
+        // operand
+        constexpr int CTRL = LD == 1 ? 0xB1 : LD == 2 ? 0x4E : 0x128;
+        const uint32_t p = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a, CTRL, 0xf, 0xf, true);
+        hi = max(a, p);
+        lo = min(a, p);
+    } else if constexpr (LD == 4) {
+        // lane - 4 (row_shr:4), then lane + 4 (row_shl:4) written only to the 4-lane banks 0 and
+        // 2 of every row, whose bit 2 is clear
+        uint32_t p = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a, 0x114, 0xf, 0xf, false);
+        p = (uint32_t)__builtin_amdgcn_update_dpp((int)p, (int)a, 0x104, 0xf, 0x5, false);
+        hi = max(a, p);
+        lo = min(a, p);
+    } else {
+        // the gfx950 row swaps leave every lane's own value in one output and its partner's in
+        // the other
+        const auto q = LD == 16 ? __builtin_amdgcn_permlane16_swap(a, a, false, false)
+                                : __builtin_amdgcn_permlane32_swap(a, a, false, false);
+        hi = max(q[0], q[1]);
+        lo = min(q[0], q[1]);
+    }
+}
+
+__device__ __forceinline__ uint64_t lane_select(uint64_t m, uint64_t a, uint64_t b) {
+    return ((uint64_t)lane_select(m, (uint32_t)(a >> 32), (uint32_t)(b >> 32)) << 32) |
+           lane_select(m, (uint32_t)a, (uint32_t)b);
+}
+
+// One compare-exchange step at lane distance LD of a bitonic network whose runs descend where
+// bit DB of the lane is clear; every element of the lane pairs with the same element of lane
+// (lane ^ LD).
+template <int LD, int DB, int N>
+__device__ __forceinline__ void bitonic_lane_step(uint32_t (&a)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const T p = xor_lanes<LD>(a[i]);
-        const T hi = a[i] > p ? a[i] : p, lo = a[i] > p ? p : a[i];
-        a[i] = keep_hi ? hi : lo;
+        uint32_t hi, lo;
+        pair_max_min<LD>(a[i], hi, lo);
+        a[i] = lane_select(keep_hi_mask(LD, DB), lo, hi);
+    }
+}
+
+template <int LD, int DB, int N>
+__device__ __forceinline__ void bitonic_lane_step(uint64_t (&a)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const uint64_t p = xor_lanes<LD>(a[i]);
+        const uint64_t hi = a[i] > p ? a[i] : p, lo = a[i] > p ? p : a[i];
+        a[i] = lane_select(keep_hi_mask(LD, DB), lo, hi);
     }
 }
 
 // The lane-distance steps LD, LD / 2, ..., 1 of one merge size.
-template <int LD, int N, typename T>
-__device__ __forceinline__ void bitonic_lane_steps(T (&a)[N], bool desc) {
+template <int LD, int DB, int N, typename T>
+__device__ __forceinline__ void bitonic_lane_steps(T (&a)[N]) {
     if constexpr (LD >= 1) {
-        bitonic_lane_step<LD>(a, desc);
-        bitonic_lane_steps<LD / 2>(a, desc);
+        bitonic_lane_step<LD, DB>(a);
+        bitonic_lane_steps<LD / 2, DB>(a);
     }
 }
 
 // One merge size of a bitonic network over 128 values held by one wave, two per lane (element
 // 2 * lane + i in a_i), ordering each run of SIZE elements descending or ascending by the run's
-// parity, as the descending network needs.
+// parity, as the descending network needs: the runs of lane l descend where bit SIZE / 2 of l is
+// clear.
 template <int SIZE, typename T>
 __device__ __forceinline__ void bitonic128_size(T &a0, T &a1) {
-    const int lane = lane_id();
-    const bool desc = ((2 * lane) & SIZE) == 0;  // the same for both elements of the lane
+    constexpr int DB = SIZE / 2;
     T a[2] = {a0, a1};
-    bitonic_lane_steps<SIZE / 4>(a, desc);
+    bitonic_lane_steps<SIZE / 4, DB>(a);
     // partner inside the lane: elements 2 * lane and 2 * lane + 1
     const T lo = a[0] < a[1] ? a[0] : a[1], hi = a[0] < a[1] ? a[1] : a[0];
-    a0 = desc ? hi : lo;
-    a1 = desc ? lo : hi;
+    if constexpr (DB >= 64) {
+        a0 = hi;
+        a1 = lo;
+    } else {
+        a0 = lane_select(desc_mask(DB), lo, hi);
+        a1 = lane_select(desc_mask(DB), hi, lo);
+    }
 }
 
 // Bitonic network sorting 128 values held by one wave (two per lane) in descending order, from
@@ -215,7 +278,7 @@ template <int SIZE>
 __device__ __forceinline__ void bitonic256_size(uint32_t (&v)[4]) {
     const int lane = lane_id();
     if constexpr (SIZE >= 8) {
-        bitonic_lane_steps<SIZE / 8>(v, ((4 * lane) & SIZE) == 0);
+        bitonic_lane_steps<SIZE / 8, SIZE / 4>(v);
     }
 #pragma unroll
     for (int dist = (SIZE >= 4 ? 2 : 1); dist > 0; dist >>= 1) {
@@ -242,14 +305,13 @@ __device__ __forceinline__ void bitonic256_from(uint32_t (&v)[4]) {
 
 // Sorts 64 values held by one wave (one per lane, element = lane) in descending order.
 __device__ __forceinline__ void wave_sort64_desc(uint32_t &v) {
-    const int lane = lane_id();
     uint32_t a[1] = {v};
-    bitonic_lane_steps<1>(a, (lane & 2) == 0);
-    bitonic_lane_steps<2>(a, (lane & 4) == 0);
-    bitonic_lane_steps<4>(a, (lane & 8) == 0);
-    bitonic_lane_steps<8>(a, (lane & 16) == 0);
-    bitonic_lane_steps<16>(a, (lane & 32) == 0);
-    bitonic_lane_steps<32>(a, true);
+    bitonic_lane_steps<1, 2>(a);
+    bitonic_lane_steps<2, 4>(a);
+    bitonic_lane_steps<4, 8>(a);
+    bitonic_lane_steps<8, 16>(a);
+    bitonic_lane_steps<16, 32>(a);
+    bitonic_lane_steps<32, 64>(a);
     v = a[0];
 }
 

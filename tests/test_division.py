@@ -1,12 +1,14 @@
-"""The kernels' division x / d = x * RN(1/d) rounds to the same bf16 as torch's IEEE fp32 division
+"""The kernels' division x / d = x * rcp(d) rounds to the same bf16 as torch's IEEE fp32 division
 for bf16 operands -- the claim that lets the prologue replace every per-element divide by one
-multiply (the reciprocal is computed once per row).
+multiply (the reciprocal is computed once per row, by v_rcp_f32, whose result is within 1 ulp of
+1/d).
 
 Why it holds: x and d carry 8 significant bits, so x / d is either exact with at most 8 bits (a bf16
 value) or at least 2^-17 (relative) away from every bf16 rounding boundary (a boundary needs 9
-bits); x * RN(1/d) is within 2^-23 of x / d. The device formula is restated here in exact rational
-arithmetic (every fp32 operation rounded once) and compared with torch's fp32 division followed by
-the bf16 cast, the reference's `logits / scales` and `logits.div_(temperature)`
+bits); x * rcp is within 2^-22 of x / d for any rcp within 1 ulp of 1/d. The device formula is
+restated here in exact rational arithmetic (every fp32 operation rounded once), with each of the
+three fp32 values within 1 ulp of 1/d as the reciprocal, and compared with torch's fp32 division
+followed by the bf16 cast, the reference's `logits / scales` and `logits.div_(temperature)`
 (core/naive.py:218, :266).
 """
 
@@ -32,11 +34,17 @@ def rn32(value: Fraction) -> float:
     return best
 
 
-def kernel_div(x: float, d: float) -> float:
+def reciprocals(d: float):
+    """RN(1/d) and its two fp32 neighbours: every value a 1-ulp reciprocal may return."""
 
-    rcp = rn32(Fraction(1) / Fraction(d))
+    r = np.float32(rn32(Fraction(1) / Fraction(d)))
 
-    return rn32(Fraction(x) * Fraction(rcp))
+    return (float(r), float(np.nextafter(r, np.float32(np.inf))), float(np.nextafter(r, np.float32(-np.inf))))
+
+
+def kernel_divs(x: float, d: float):
+
+    return [rn32(Fraction(x) * Fraction(rcp)) for rcp in reciprocals(d)]
 
 
 def bf16(v: float) -> float:
@@ -66,7 +74,7 @@ def test_random_operands():
 
         x = random_bf16(rng, -20, 20)
         d = abs(random_bf16(rng, -6, 6))
-        assert bf16(kernel_div(x, d)) == reference(x, d), (x, d)
+        assert all(bf16(q) == reference(x, d) for q in kernel_divs(x, d)), (x, d)
 
 
 def test_quotients_near_bf16_midpoints():
@@ -81,7 +89,7 @@ def test_quotients_near_bf16_midpoints():
         d = abs(random_bf16(rng, -3, 3))
         m = (2 * rng.randrange(128, 256) + 1) * 2.0 ** (rng.randrange(-8, 8) - 8)   # 9-bit odd
         x = bf16(d * m)
-        assert bf16(kernel_div(x, d)) == reference(x, d), (x, d)
+        assert all(bf16(q) == reference(x, d) for q in kernel_divs(x, d)), (x, d)
 
 
 def test_exact_quotients_and_specials():
@@ -90,5 +98,5 @@ def test_exact_quotients_and_specials():
 
         for d in (1.0, 2.0, 0.5, 1.25, 3.0):
 
-            got = kernel_div(x, d) if np.isfinite(x) else x / d
-            assert bf16(got) == reference(x, d) or (np.isnan(got) and np.isnan(reference(x, d)))
+            for got in (kernel_divs(x, d) if np.isfinite(x) else [x / d]):
+                assert bf16(got) == reference(x, d) or (np.isnan(got) and np.isnan(reference(x, d)))

@@ -47,17 +47,6 @@ __device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, i
     return r;
 }
 
-// First sorted position in row `rowi` whose token equals d, or -1 (wave 0).
-__device__ __forceinline__ int find_position(const int32_t *idx, int d) {
-    const int lane = lane_id();
-    const uint64_t m0 = __ballot(idx[2 * lane] == d);
-    const uint64_t m1 = __ballot(idx[2 * lane + 1] == d);
-    const int p0 = m0 ? 2 * (__ffsll((unsigned long long)m0) - 1) : 1 << 20;
-    const int p1 = m1 ? 2 * (__ffsll((unsigned long long)m1) - 1) + 1 : 1 << 20;
-    const int p = p0 < p1 ? p0 : p1;
-    return p < SS_K ? p : -1;
-}
-
 __device__ __forceinline__ RowState multistep_row_state(const ss_multistep_args &a, int row,
                                                         int step, int slot, uint32_t ind) {
     RowState rs;
@@ -176,6 +165,7 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
     const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
     const uint32_t ind = a.indicators[slot];
     const bool greedy = (ind & IND_GREEDY) != 0;
+    const int top_lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
 
     // ---- request stage (wave 0) -------------------------------------------------------------------
     const int lane = threadIdx.x;
@@ -189,28 +179,72 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
                             ? a.draft_probabilities + (int64_t)slot * a.probs_stride_slot
                             : nullptr;
 
+    const bool want_lp = a.return_logprobs && a.logprobs;
     int j = n - 1;
     int token;
     if (greedy) {
-        for (int i = 0; i < n - 1; ++i) {
-            if (idxs[(int64_t)i * SS_K] != drafted[i]) {
-                j = i;
+        // lane i compares row i's argmax with drafted token i; all of them in one round of loads
+        for (int base = 0; base < n - 1; base += 64) {
+            const int i = base + lane;
+            const bool mismatch = i < n - 1 && idxs[(int64_t)i * SS_K] != drafted[i];
+            const uint64_t m = __ballot(mismatch);
+            if (m) {
+                j = base + __ffsll((unsigned long long)m) - 1;
                 break;
             }
         }
         token = idxs[(int64_t)j * SS_K];
     } else {
+        // Draft positions VCH at a time: every load of a chunk is issued before any result is
+        // used (rows at and past n - 1 read row n - 2 and are ignored), so a chunk costs two
+        // rounds of loads (candidate rows, then the drafted token's value and draft probability)
+        // instead of two per position.
+        constexpr int VCH = 8;
         const uint16_t *u = a.uniform + (int64_t)slot * a.stride_uniform;
-        for (int i = 0; i < n - 1; ++i) {
-            const int d = drafted[i];
-            const bool in_vocab = d >= 0 && d < a.vocab_size;
-            const int pos = find_position(idxs + (int64_t)i * SS_K, d);
-            const float p = pos >= 0 ? expf(vals[(int64_t)i * SS_K + pos]) : 0.0f;
-            const float qd = svgd ? 1.0f
-                                  : (in_vocab ? bf2f(q[(int64_t)i * a.probs_stride_step + d]) : 0.0f);
-            // bf16(u * q) <= p  (core/naive.py:594-599)
-            if (!(rbf(bf2f(u[i]) * qd) <= p)) {
-                j = i;
+        for (int base = 0; base < n - 1; base += VCH) {
+            int d[VCH], pos[VCH];
+            int2 w[VCH];
+            float uk[VCH];
+#pragma unroll
+            for (int k = 0; k < VCH; ++k) {
+                const int r = min(base + k, n - 2);
+                d[k] = drafted[r];
+                uk[k] = bf2f(u[r]);
+                w[k] = *(const int2 *)(idxs + (int64_t)r * SS_K + e0);
+            }
+            float v[VCH], qd[VCH];
+#pragma unroll
+            for (int k = 0; k < VCH; ++k) {
+                const int r = min(base + k, n - 2);
+                // first sorted position whose token is d[k] (core/naive.py:580-584), or -1
+                const uint64_t m0 = __ballot(w[k].x == d[k]), m1 = __ballot(w[k].y == d[k]);
+                const int p0 = m0 ? 2 * (__ffsll((unsigned long long)m0) - 1) : 1 << 20;
+                const int p1 = m1 ? 2 * (__ffsll((unsigned long long)m1) - 1) + 1 : 1 << 20;
+                pos[k] = min(p0, p1) < SS_K ? min(p0, p1) : -1;
+                v[k] = vals[(int64_t)r * SS_K + (pos[k] >= 0 ? pos[k] : 0)];
+                const bool in_vocab = d[k] >= 0 && d[k] < a.vocab_size;
+                qd[k] = svgd ? 1.0f
+                             : bf2f(q[(int64_t)r * a.probs_stride_step + (in_vocab ? d[k] : 0)]);
+                qd[k] = in_vocab || svgd ? qd[k] : 0.0f;
+            }
+            int rej = -1;
+#pragma unroll
+            for (int k = 0; k < VCH; ++k) {
+                const float pk = pos[k] >= 0 ? expf(v[k]) : 0.0f;
+                // bf16(u * q) <= p  (core/naive.py:594-599)
+                if (rej < 0 && base + k < n - 1 && !(rbf(uk[k] * qd[k]) <= pk)) rej = k;
+            }
+            // logprobs of the accepted positions: the value at the drafted token's position, or
+            // at position 0 when the token is not among the candidates (argmax of an all-false
+            // match row, core/naive.py:580-584)
+            if (want_lp && lane == 0) {
+#pragma unroll
+                for (int k = 0; k < VCH; ++k)
+                    if ((rej < 0 || k < rej) && base + k < n - 1)
+                        a.logprobs[rq.margin + base + k] = (uint16_t)f2bf(v[k]);
+            }
+            if (rej >= 0) {
+                j = base + rej;
                 break;
             }
         }
@@ -245,21 +279,11 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
         const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
         token = lane_i32((sel & 1) ? c1 : c0, sel >> 1);
 
-        if (a.return_logprobs && a.logprobs) {
-            for (int i = 0; i <= j; ++i) {
-                int pos;
-                if (i == j) {
-                    pos = sel;
-                } else {
-                    pos = find_position(idxs + (int64_t)i * SS_K, drafted[i]);
-                    if (pos < 0) pos = 0;  // argmax of an all-false match row (core/naive.py:580-584)
-                }
-                if (lane == 0)
-                    a.logprobs[rq.margin + i] = (uint16_t)f2bf(vals[(int64_t)i * SS_K + pos]);
-            }
+        if (want_lp) {
+            // positions before j were written during verification
+            if (lane == 0) a.logprobs[rq.margin + j] = (uint16_t)f2bf(vals[(int64_t)j * SS_K + sel]);
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                int lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
-                lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
+                const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
                 for (int i = 0; i <= j; ++i) {
                     const int64_t o = (int64_t)(rq.margin + i) * a.stride_top;
                     const int64_t s = (int64_t)i * SS_K;

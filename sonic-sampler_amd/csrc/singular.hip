@@ -72,6 +72,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
     const int32_t topk = a.top_k ? uniform_i32(a.top_k, slot) : SS_K;
     const float topp = a.top_p ? bf2f(uniform_u16(a.top_p, slot)) : 1.0f;
     const float minp = a.min_p ? bf2f(uniform_u16(a.min_p, slot)) : 0.0f;
+    const int top_lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
 
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
@@ -142,8 +143,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
             const float osel = lane_f32((sel & 1) ? o1 : o0, sel >> 1);
             if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                int lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
-                lim = lim < a.max_top_logprobs ? lim : a.max_top_logprobs;
+                const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
                 const int64_t o = (int64_t)row * a.stride_top;
                 if (e0 < lim) {
                     a.top_values[o + e0] = (uint16_t)f2bf(o0);

@@ -390,7 +390,8 @@ def _queue_behind_sleep(ms: float = 60.0) -> None:
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
-def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox: bool = True) -> dict:
+def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox: bool = True,
+              block_n: Optional[int] = None) -> dict:
 
     from sonic_sampler import _native
     from sonic_sampler.interface import UnshardedFusedSingular
@@ -400,7 +401,7 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     batch, vocab = base.logits.shape
 
     sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch,
-                                                max_top_logprobs=5, device=device)
+                                                max_top_logprobs=5, block_size=block_n, device=device)
     inputs = []
 
     for i in range(sets):
@@ -608,7 +609,7 @@ CONFIG_NAMES = {
 }
 
 
-def run_config(config: int, steps: int, warmup: int, sets: int = 3) -> dict:
+def run_config(config: int, steps: int, warmup: int, sets: int = 3, block_n: Optional[int] = None) -> dict:
     """Timing of one of the other configurations (their parity is covered by the GPU tests)."""
 
     from sonic_sampler.interface import UnshardedBoundedTopK, UnshardedFusedMultistep, UnshardedFusedSingular
@@ -618,7 +619,8 @@ def run_config(config: int, steps: int, warmup: int, sets: int = 3) -> dict:
     if config == 0:
 
         inputs = [c0_inputs(seed=1000 + 100 * i)[0].to(device) for i in range(sets)]
-        topk = UnshardedBoundedTopK.initialize(vocab_size=32000, batch_size=8, k=32, device=device)
+        topk = UnshardedBoundedTopK.initialize(vocab_size=32000, batch_size=8, k=32, block_size=block_n,
+                                               device=device)
         step = lambda i: topk(inputs[i % sets])  # noqa: E731
         rows, algorithmic = 8, 8 * 32000 * 4 + 8 * 32 * 8
 
@@ -629,7 +631,7 @@ def run_config(config: int, steps: int, warmup: int, sets: int = 3) -> dict:
         batch = len(works[0].cu_seqlens) - 1
         verifier = UnshardedFusedMultistep.initialize(vocab_size=works[0].vocab, lookahead=works[0].lookahead,
                                                       batch_size=batch, max_top_logprobs=works[0].max_top_logprobs,
-                                                      device=device)
+                                                      block_size=block_n, device=device)
         staged = []
 
         for w in works:
@@ -665,7 +667,7 @@ def run_config(config: int, steps: int, warmup: int, sets: int = 3) -> dict:
         w0 = works[0]
         rows = w0.logits.size(0)
         sampler = UnshardedFusedSingular.initialize(vocab_size=w0.vocab, batch_size=rows, lookahead=4,
-                                                    max_top_logprobs=5, device=device)
+                                                    max_top_logprobs=5, block_size=block_n, device=device)
         staged = []
 
         for w in works:
@@ -744,6 +746,8 @@ def main(argv=None) -> int:
                         help="only run a 1 GiB device copy (PMC counter calibration)")
     parser.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4],
                         help="configuration to time (1, the headline, by default)")
+    parser.add_argument("--block-n", type=int, default=None,
+                        help="tile width instead of the dispatch table's (tuning sweeps)")
     args = parser.parse_args(argv)
 
     if args.copy_calibration:
@@ -761,11 +765,12 @@ def main(argv=None) -> int:
 
     if args.config != 1:
 
-        print(json.dumps(run_config(args.config, args.steps, args.warmup)), flush=True)
+        print(json.dumps(run_config(args.config, args.steps, args.warmup, block_n=args.block_n)), flush=True)
 
         return 0
 
-    result = run_bench(args.steps, args.warmup, cpu_rows=args.cpu_rows, philox=not args.buffer_noise)
+    result = run_bench(args.steps, args.warmup, cpu_rows=args.cpu_rows, philox=not args.buffer_noise,
+                       block_n=args.block_n)
     print(json.dumps(result), flush=True)
 
     return 0

@@ -214,8 +214,11 @@ __device__ __forceinline__ float chain_ieee(const Chain &k, float x, int32_t dec
 // elements inside the vocabulary; it can be false only when `partial` is set. x(j) and bb(j) return
 // the (grammar-masked) logit and the bias bits of element j; bw(j) is nonzero whenever element j's
 // bias is nonzero (it may also be nonzero for a zero bias: the chain is exact for every element).
+// maybe_exc is false when no element can have a nonzero count or bias (no penalty or bias plane is
+// read) and the chain is not forced on every element: the keys are then the temperature keys.
 template <int E, class XOf, class BiasOf, class BiasWordOf>
 __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial, XOf x,
+                                            bool maybe_exc,
                                             const bool (&ok)[E], const int32_t (&dec)[E],
                                             const int32_t (&ctx)[E], BiasOf bb, BiasWordOf bw,
                                             uint32_t (&keys)[E]) {
@@ -231,12 +234,14 @@ __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool p
         // The branch at each element position is on the wave's ballot, so it is uniform: the
         // chain then runs with every lane active and the ballot selects its result.
         const uint64_t forced = all_exc ? ~0ull : 0ull;
+        if (maybe_exc) {
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u) | forced;
-            if (m) {
-                const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
-                keys[j] = lane_select(m, keys[j], kc);
+            for (int j = 0; j < E; ++j) {
+                const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u) | forced;
+                if (m) {
+                    const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
+                    keys[j] = lane_select(m, keys[j], kc);
+                }
             }
         }
     } else {
@@ -406,7 +411,32 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
     };
     // the bias word of the element's pair, shifted so that -0 in the high half does not count
     auto bw = [&](int j) { return ((j & 2) ? pl.bw[j >> 2].y : pl.bw[j >> 2].x) << 1; };
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, ok, dec, ctx, bb, bw, keys);
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, all_exc || u.rep || u.mult || u.bias, ok, dec,
+                   ctx, bb, bw, keys);
+}
+
+// Direct layout, row with every side plane off (no grammar, penalty or bias): the keys come from
+// the logits alone and no other plane is read.
+template <int E>
+__device__ __forceinline__ void plain_keys(const RowState &rs, const Uses &u, int col0, int V,
+                                           const u32x2 (&lw)[E / 4], uint32_t (&keys)[E]) {
+    const int lane4 = (int)threadIdx.x * 4;
+    bool all_exc;
+    const Chain k = row_chain(rs, u, all_exc);
+    bool ok[E];
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        const bool in = col0 + c * (SS_BLOCK * 4) + lane4 < V;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
+    }
+    const int32_t zero[E] = {};
+    auto x = [&](int j) {
+        const uint32_t w = (j & 2) ? lw[j >> 2].y : lw[j >> 2].x;
+        return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+    };
+    auto none = [](int) { return 0u; };
+    finish_keys<E>(k, false, col0 + SS_BLOCK * E > V, x, false, ok, zero, zero, none, none, keys);
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
@@ -504,7 +534,8 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                 bbits[j] = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << 16;
         }
     }
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, [&](int j) { return x[j]; }, ok, dec, ctx,
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, [&](int j) { return x[j]; },
+                   all_exc || u.rep || u.mult || u.bias, ok, dec, ctx,
                    [&](int j) { return bbits[j]; }, [&](int j) { return bbits[j] << 1; }, keys);
 }
 
@@ -523,9 +554,13 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
                                               uint32_t (&keys)[E]) {
     const Uses u = row_uses(rs);
     if constexpr (MODE == MODE_DIRECT) {
-        Planes<E> pl;
-        issue_planes<E>(rs, u, true, col0, pl);
-        direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
+        if (!(u.g || u.rep || u.mult || u.bias)) {
+            plain_keys<E>(rs, u, col0, V, lw, keys);
+        } else {
+            Planes<E> pl;
+            issue_planes<E>(rs, u, true, col0, pl);
+            direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
+        }
     } else {
         gather_keys<E, MODE == MODE_GATHER_VEC>(rs, u, col0, V, hist, lw, keys);
     }

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
         if ((int)threadIdx.x < step) sm.hist[threadIdx.x] = a.drafted_tokens[rq.margin + threadIdx.x];
         __syncthreads();
     }
-    uint32_t keys[E];
+    Keys<E> keys;
     prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
 }

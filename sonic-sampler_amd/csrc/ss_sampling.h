@@ -62,6 +62,36 @@ __device__ __forceinline__ int tile_col(int j) {  // column offset of element j 
     return (j >> 2) * (SS_BLOCK * 4) + (int)threadIdx.x * 4 + (j & 3);
 }
 
+// The 16-bit keys of a thread's E elements, two per register: element 2i in the low half of p[i],
+// element 2i + 1 in the high half. Comparisons with a 16-bit threshold t read a half in place: the
+// low half through a 16-bit source select, the high half against (t << 16) | 0xffff.
+template <int E>
+struct Keys {
+    uint32_t p[E / 2];
+
+    __device__ __forceinline__ uint32_t at(int j) const {
+        return (j & 1) ? p[j >> 1] >> 16 : p[j >> 1] & 0xffffu;
+    }
+    __device__ __forceinline__ bool gt(int j, uint32_t t) const {
+        return (j & 1) ? p[j >> 1] > ((t << 16) | 0xffffu) : (uint16_t)p[j >> 1] > (uint16_t)t;
+    }
+    __device__ __forceinline__ bool ge(int j, uint32_t t) const {
+        return (j & 1) ? p[j >> 1] >= (t << 16) : (uint16_t)p[j >> 1] >= (uint16_t)t;
+    }
+    __device__ __forceinline__ bool eq(int j, uint32_t t) const {
+        return (j & 1) ? (p[j >> 1] >> 16) == t : (uint16_t)p[j >> 1] == (uint16_t)t;
+    }
+    // the pair register of element j with element j's key replaced by k
+    __device__ __forceinline__ uint32_t with(int j, uint32_t k) const {
+        return (j & 1) ? (p[j >> 1] & 0xffffu) | (k << 16) : (p[j >> 1] & 0xffff0000u) | k;
+    }
+    // (key << 16) | (0xffff - column of element j), from cb = 0xffff - 4 * thread
+    __device__ __forceinline__ uint32_t composite(int j, uint32_t cb) const {
+        const uint32_t hi = (j & 1) ? (p[j >> 1] & 0xffff0000u) : (p[j >> 1] << 16);
+        return (hi | cb) - (uint32_t)((j >> 2) * (SS_BLOCK * 4) + (j & 3));
+    }
+};
+
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef __bf16 b2v __attribute__((ext_vector_type(2)));
 
@@ -221,15 +251,13 @@ __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool p
                                             bool maybe_exc,
                                             const bool (&ok)[E], const int32_t (&dec)[E],
                                             const int32_t (&ctx)[E], BiasOf bb, BiasWordOf bw,
-                                            uint32_t (&keys)[E]) {
+                                            Keys<E> &keys) {
     if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
         const FastChain f = fast_chain(k);
 #pragma unroll
         for (int j = 0; j < E; j += 2) {
             const f2v v = {x(j) * f.trcp, x(j + 1) * f.trcp};
-            const uint32_t kk = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
-            keys[j] = kk & 0xffffu;
-            keys[j + 1] = kk >> 16;
+            keys.p[j >> 1] = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
         }
         // The branch at each element position is on the wave's ballot, so it is uniform: the
         // chain then runs with every lane active and the ballot selects its result.
@@ -240,18 +268,20 @@ __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool p
                 const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u) | forced;
                 if (m) {
                     const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
-                    keys[j] = lane_select(m, keys[j], kc);
+                    keys.p[j >> 1] = lane_select(m, keys.p[j >> 1], keys.with(j, kc));
                 }
             }
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < E; ++j)
-            keys[j] = key_of(chain_ieee(k, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
+        for (int j = 0; j < E; j += 2)
+            keys.p[j >> 1] = key_of(chain_ieee(k, x(j), dec[j], ctx[j], __uint_as_float(bb(j)))) |
+                             (key_of(chain_ieee(k, x(j + 1), dec[j + 1], ctx[j + 1], __uint_as_float(bb(j + 1)))) << 16);
     }
     if (partial) {
 #pragma unroll
-        for (int j = 0; j < E; ++j) keys[j] = ok[j] ? keys[j] : 0u;
+        for (int j = 0; j < E; j += 2)
+            keys.p[j >> 1] = (ok[j] ? keys.p[j >> 1] & 0xffffu : 0u) | (ok[j + 1] ? keys.p[j >> 1] & 0xffff0000u : 0u);
     }
 }
 
@@ -358,7 +388,7 @@ __device__ __forceinline__ void issue_planes(const RowState &rs, const Uses &u, 
 template <int E>
 __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, int col0, int V,
                                             const int32_t *hist, const u32x2 (&lw_in)[E / 4],
-                                            const Planes<E> &pl, uint32_t (&keys)[E]) {
+                                            const Planes<E> &pl, Keys<E> &keys) {
     constexpr int NCH = E / 4;
     const int lane4 = (int)threadIdx.x * 4;
     bool all_exc;
@@ -419,7 +449,7 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
 // the logits alone and no other plane is read.
 template <int E>
 __device__ __forceinline__ void plain_keys(const RowState &rs, const Uses &u, int col0, int V,
-                                           const u32x2 (&lw)[E / 4], uint32_t (&keys)[E]) {
+                                           const u32x2 (&lw)[E / 4], Keys<E> &keys) {
     const int lane4 = (int)threadIdx.x * 4;
     bool all_exc;
     const Chain k = row_chain(rs, u, all_exc);
@@ -443,7 +473,7 @@ __device__ __forceinline__ void plain_keys(const RowState &rs, const Uses &u, in
 template <int E, bool VEC>
 __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, int col0, int V,
                                             const int32_t *hist, const u32x2 (&lw)[E / 4],
-                                            uint32_t (&keys)[E]) {
+                                            Keys<E> &keys) {
     constexpr int NCH = E / 4;
     const int lane4 = (int)threadIdx.x * 4;
     bool all_exc;
@@ -551,7 +581,7 @@ enum { MODE_DIRECT = 0, MODE_GATHER_VEC = 1, MODE_SCALAR = 2 };
 template <int E, int MODE>
 __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
                                               const int32_t *hist, const u32x2 (&lw)[E / 4],
-                                              uint32_t (&keys)[E]) {
+                                              Keys<E> &keys) {
     const Uses u = row_uses(rs);
     if constexpr (MODE == MODE_DIRECT) {
         if (!(u.g || u.rep || u.mult || u.bias)) {
@@ -587,21 +617,20 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
 // by ballot and mbcnt, and the wave sorts them there in descending order (zero padded to 128).
 // Returns the wave's survivor count; above 128 the region holds only the first 128, unsorted.
 template <int E, bool EXACT>
-__device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t (&keys)[E],
-                                                   uint32_t T, uint32_t tie_keep) {
+__device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &keys, uint32_t T,
+                                                   uint32_t tie_keep) {
     const int lane = lane_id();
     uint32_t *run = sm.run[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
-    // 0xffff - column of the lane's element 0; element j subtracts its offset (j / 4) * 1024 + j % 4
-    const uint32_t cb = 0xffffu - 4u * threadIdx.x;
+    const uint32_t cb = 0xffffu - 4u * threadIdx.x;  // 0xffff - column of the lane's element 0
     // Wave-uniform count, saturated at SS_K + 1: positions stay below SS_K + 64, inside the run,
     // and a count above SS_K still reads as an overflow.
     uint32_t cnt = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const bool p = EXACT ? (keys[j] > T) | (((tie_keep >> j) & 1u) != 0u) : keys[j] > T;
+        const bool p = EXACT ? keys.gt(j, T) | (((tie_keep >> j) & 1u) != 0u) : keys.gt(j, T);
         const uint64_t m = __ballot(p);
         uint32_t *at = run + cnt;  // uniform
-        if (p) at[mbcnt64(m)] = ((keys[j] << 16) | cb) - (uint32_t)((j >> 2) * (SS_BLOCK * 4) + (j & 3));
+        if (p) at[mbcnt64(m)] = keys.composite(j, cb);
         cnt = min(cnt + (uint32_t)__popcll(m), (uint32_t)SS_K + 1u);
     }
     if (cnt <= 64) {
@@ -638,17 +667,17 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const uint32_t 
 // 128 - #(key > T) of the ties: exactly the first 128 of the stable descending order, so no wave
 // can exceed 128.
 template <int E>
-__device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint32_t (&keys)[E],
+__device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const Keys<E> &keys,
                                            uint32_t *scr, int tile) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
     if (greedy) {
+        // an absent element (key 0) has a composite below 0x10000, under that of every element
+        // of the vocabulary, and every tile holds at least one such element
+        const uint32_t cb = 0xffffu - 4u * threadIdx.x;
         uint32_t best = 0;
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const uint32_t c = keys[j] ? ((keys[j] << 16) | (0xffffu - (uint32_t)tile_col(j))) : 0u;
-            best = best > c ? best : c;
-        }
+        for (int j = 0; j < E; ++j) best = max(best, keys.composite(j, cb));
         best = wave_max_u32(best);
         if (lane == 0) sm.red[wave] = best;
         __syncthreads();
@@ -659,12 +688,18 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
         }
         return;
     }
-    uint32_t m1 = 0, m2 = 0;  // the lane's largest and second-largest key
+    // The lane's largest and second-largest key: the two largest of its even and of its odd
+    // elements with packed 16-bit max / min, then the two largest of those four.
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 a1 = {0, 0}, a2 = {0, 0};
 #pragma unroll
-    for (int j = 0; j < E; ++j) {
-        m2 = max(m2, min(m1, keys[j]));
-        m1 = max(m1, keys[j]);
+    for (int i = 0; i < E / 2; ++i) {
+        const u16x2 v = __builtin_bit_cast(u16x2, keys.p[i]);
+        a2 = __builtin_elementwise_max(a2, __builtin_elementwise_min(a1, v));
+        a1 = __builtin_elementwise_max(a1, v);
     }
+    const uint32_t m1 = max((uint32_t)a1.x, (uint32_t)a1.y);
+    const uint32_t m2 = max(min((uint32_t)a1.x, (uint32_t)a1.y), max((uint32_t)a2.x, (uint32_t)a2.y));
     uint32_t bound = 0;
 #pragma unroll
     for (int b = 15; b >= 0; --b) {
@@ -684,8 +719,8 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
         uint32_t gt = 0, ge = 0;
 #pragma unroll
         for (int j = 0; j < E; ++j) {
-            gt += keys[j] > lo;
-            ge += keys[j] >= lo;
+            gt += keys.gt(j, lo);
+            ge += keys.ge(j, lo);
         }
         const uint32_t above_lo = block_count(gt, sm.red), from_lo = block_count(ge, sm.red);
         uint32_t above;  // keys > T
@@ -699,13 +734,13 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
                 const uint32_t c = t | (1u << b);
                 uint32_t k = 0;
 #pragma unroll
-                for (int j = 0; j < E; ++j) k += keys[j] >= c;
+                for (int j = 0; j < E; ++j) k += keys.ge(j, c);
                 if (block_count(k, sm.red) >= (uint32_t)SS_K) t = c;
             }
             T = t;
             uint32_t k = 0;
 #pragma unroll
-            for (int j = 0; j < E; ++j) k += keys[j] > T;
+            for (int j = 0; j < E; ++j) k += keys.gt(j, T);
             above = block_count(k, sm.red);
         }
         // The first `need` keys equal to T in column order (chunk, thread, element) are kept: their
@@ -717,7 +752,7 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
         for (int c = 0; c < NCH; ++c) {
             eq[c] = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) eq[c] += keys[4 * c + i] == T;
+            for (int i = 0; i < 4; ++i) eq[c] += keys.eq(4 * c + i, T);
         }
         block_exclusive_scan<NCH>(eq, tot, sm.scan);
         uint32_t tie_keep = 0, before = 0;
@@ -726,7 +761,7 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const uint
             uint32_t r = before + eq[c];  // rank of this thread's first tie in chunk c
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (keys[4 * c + i] == T) {
+                if (keys.eq(4 * c + i, T)) {
                     tie_keep |= (r < need ? 1u : 0u) << (4 * c + i);
                     ++r;
                 }

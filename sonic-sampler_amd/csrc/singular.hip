@@ -93,24 +93,32 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
     merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
-    if (threadIdx.x >= 64) return;
 
-    const int lane = threadIdx.x;
+    // Waves 1 and 2 remap the 128 candidates' columns and draw their noise (one candidate per
+    // lane) while wave 0 applies the truncation.
+    const int wave = (int)threadIdx.x >> 6;
+    const int lane = lane_id();
     const int e0 = 2 * lane, e1 = e0 + 1;
-    truncate(ind, topk, topp, minp, v0, v1);
-    if (a.d2t) {
-        i0 = a.d2t[i0];
-        i1 = a.d2t[i1];
+    if (wave == 0) {
+        sm.tok[e0] = i0;
+        sm.tok[e1] = i1;
     }
-    float w0, w1;
-    if (a.philox.enabled) {
-        w0 = philox_gumbel(a.philox.seed, a.philox.offset, slot, a.philox_step, i0);
-        w1 = philox_gumbel(a.philox.seed, a.philox.offset, slot, a.philox_step, i1);
-    } else {
-        const uint16_t *g = a.gumbel + (int64_t)slot * a.stride_gumbel;
-        w0 = bf2f(g[i0]);
-        w1 = bf2f(g[i1]);
+    __syncthreads();
+    if (wave == 1 || wave == 2) {
+        const int e = (wave - 1) * 64 + lane;
+        int t = sm.tok[e];
+        if (a.d2t) t = a.d2t[t];
+        sm.noise[e] = a.philox.enabled
+                          ? philox_gumbel(a.philox.seed, a.philox.offset, slot, a.philox_step, t)
+                          : bf2f(a.gumbel[(int64_t)slot * a.stride_gumbel + t]);
+        sm.tok[e] = t;
     }
+    if (wave == 0) truncate(ind, topk, topp, minp, v0, v1);
+    __syncthreads();
+    if (wave != 0) return;
+    i0 = sm.tok[e0];
+    i1 = sm.tok[e1];
+    const float w0 = sm.noise[e0], w1 = sm.noise[e1];
     const int sel = wave_argmax_first(rbf(v0 - w0), rbf(v1 - w1));
     const int token = lane_i32((sel & 1) ? i1 : i0, sel >> 1);
 

@@ -31,6 +31,8 @@ struct SampleSmem {
     int32_t idx[SS_K];
     int32_t hist[64];
     uint32_t red[SS_WAVES];
+    int32_t tok[SS_K];         // selection: the candidates' tokens (columns, then remapped)
+    float noise[SS_K];         // selection: their Gumbel noise
 };
 
 // Workgroup memory of the tile kernels.

@@ -60,10 +60,9 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
 }
 
-// Row stage: grid rows; merge of the tiles' candidates and the selection.
-__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
-    __shared__ SampleSmem sm;
-    const int row = blockIdx.x;
+// Row stage of one row: merge of the tiles' candidates and the selection. All threads call.
+__device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSmem &sm, int row,
+                                             int tiles) {
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     RowSamples smp;
     load_samples(scr, tiles, smp);  // depends on the row only: issued first
@@ -165,6 +164,12 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_arg
         }
     }
     if (lane == 0) a.tokens[(int64_t)row * a.stride_tokens] = token;
+}
+
+// Row stage: grid rows.
+__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
+    __shared__ SampleSmem sm;
+    singular_row(a, sm, blockIdx.x, tiles);
 }
 
 template <int MODE>

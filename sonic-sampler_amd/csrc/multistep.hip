@@ -284,16 +284,28 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
             if (lane == 0) a.logprobs[rq.margin + j] = (uint16_t)f2bf(vals[(int64_t)j * SS_K + sel]);
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
                 const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
-                for (int i = 0; i <= j; ++i) {
-                    const int64_t o = (int64_t)(rq.margin + i) * a.stride_top;
-                    const int64_t s = (int64_t)i * SS_K;
-                    if (e0 < lim) {
-                        a.top_values[o + e0] = (uint16_t)f2bf(vals[s + e0]);
-                        a.top_tokens[o + e0] = idxs[s + e0];
+                // rows 0..j eight at a time, every load of a group issued before its stores
+                for (int base = 0; base <= j; base += 8) {
+                    float2 v[8];
+                    int2 t[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int64_t s = (int64_t)min(base + k, j) * SS_K + e0;
+                        v[k] = *(const float2 *)(vals + s);
+                        t[k] = *(const int2 *)(idxs + s);
                     }
-                    if (e1 < lim) {
-                        a.top_values[o + e1] = (uint16_t)f2bf(vals[s + e1]);
-                        a.top_tokens[o + e1] = idxs[s + e1];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        if (base + k > j) break;
+                        const int64_t o = (int64_t)(rq.margin + base + k) * a.stride_top;
+                        if (e0 < lim) {
+                            a.top_values[o + e0] = (uint16_t)f2bf(v[k].x);
+                            a.top_tokens[o + e0] = t[k].x;
+                        }
+                        if (e1 < lim) {
+                            a.top_values[o + e1] = (uint16_t)f2bf(v[k].y);
+                            a.top_tokens[o + e1] = t[k].y;
+                        }
                     }
                 }
             }

@@ -119,7 +119,9 @@ class UnshardedFusedMultistep(TwoStageTiling):
             enable_pdl=self.pdl,
             update_counts=update_counts,
             return_logprobs=logprobs,
-            block_n=self.block_n,
+            # the batch-tuned tile width, as the single-step API uses (the reference passes the
+            # factory's width here); the scratchpad is sized for the narrowest width of the table
+            block_n=block_n,
             scratchpad=self.scratchpad,
             values=self.values,
             indices=self.indices,

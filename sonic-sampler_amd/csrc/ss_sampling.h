@@ -263,11 +263,14 @@ __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool p
         }
         // The branch at each element position is on the wave's ballot, so it is uniform: the
         // chain then runs with every lane active and the ballot selects its result.
-        const uint64_t forced = all_exc ? ~0ull : 0ull;
-        if (maybe_exc) {
+        if (all_exc) {
+#pragma unroll
+            for (int j = 0; j < E; ++j)
+                keys.p[j >> 1] = keys.with(j, key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j)))));
+        } else if (maybe_exc) {
 #pragma unroll
             for (int j = 0; j < E; ++j) {
-                const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u) | forced;
+                const uint64_t m = __ballot(((uint32_t)(dec[j] | ctx[j]) | bw(j)) != 0u);
                 if (m) {
                     const uint32_t kc = key_of(chain_fast(f, x(j), dec[j], ctx[j], __uint_as_float(bb(j))));
                     keys.p[j >> 1] = lane_select(m, keys.p[j >> 1], keys.with(j, kc));
@@ -655,7 +658,8 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &
 // same composites, sorted in descending order (0 for absent entries), at scratch[tile * 128 ...].
 //
 // The top-128 is found without a selection over the whole tile. Lower bound: per wave, the
-// largest t such that the lanes' largest and second-largest keys include at least 32 keys >= t,
+// largest multiple of 4, t, such that the lanes' largest and second-largest keys include at least
+// 32 keys >= t,
 // so the wave holds at least 32 keys >= t; with lo the smallest of the four wave bounds, the tile
 // holds at least 128 keys >= lo. Every wave then collects its survivors (keys >= lo: about 160 of
 // a 4096-wide tile of unstructured logits, 30-50 per wave) in its own LDS region and sorts them
@@ -702,9 +706,10 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const Keys
     }
     const uint32_t m1 = max((uint32_t)a1.x, (uint32_t)a1.y);
     const uint32_t m2 = max(min((uint32_t)a1.x, (uint32_t)a1.y), max((uint32_t)a2.x, (uint32_t)a2.y));
+    // 14 of the 16 key bits: the bound may sit up to 3 keys low, which only adds a few survivors
     uint32_t bound = 0;
 #pragma unroll
-    for (int b = 15; b >= 0; --b) {
+    for (int b = 15; b >= 2; --b) {
         const uint32_t c = bound | (1u << b);
         if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= 32) bound = c;
     }

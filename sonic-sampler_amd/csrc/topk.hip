@@ -15,6 +15,7 @@ struct TopkSmem {
     SelectSmem sel;
     uint64_t cand[SS_K];
     int32_t idx[SS_K];
+    uint64_t runs[SS_WAVES][SS_K];  // merge of up to 512 candidates: the waves' sorted runs
 };
 
 template <bool F32>
@@ -92,10 +93,64 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
     const int V = a.vocab_size;
     const int k = a.k;
     const Cand *scr = (const Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+    const int ncand = tiles * k;
+    if (ncand <= 2 * SS_BLOCK) {
+        // Up to 512 candidates, two per thread, as composites (key << 32) | (~column): their
+        // descending order is (value desc, column asc). Every wave sorts its 128, and two rounds
+        // of bitonic merges keep the top-128 of the four runs (the elementwise maximum of a run
+        // and its reversed partner is a bitonic sequence holding the top-128 of both).
+        const int lane = lane_id(), wave = (int)threadIdx.x >> 6;
+        uint64_t c[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = 2 * (int)threadIdx.x + i;
+            uint64_t v = 0;
+            if (p < ncand) {
+                const Cand cd = scr[p];
+                const uint32_t col = (uint32_t)((p / k) * a.block_n + Tr::cand_li(cd));
+                v = ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
+            }
+            c[i] = v;
+        }
+        wave_sort128_desc(c[0], c[1]);
+        sm.runs[wave][2 * lane] = c[0];
+        sm.runs[wave][2 * lane + 1] = c[1];
+        __syncthreads();
+        if (wave < 2) {
+            const uint64_t *A = sm.runs[2 * wave], *B = sm.runs[2 * wave + 1];
+            uint64_t x0 = max_u64(A[2 * lane], B[127 - 2 * lane]);
+            uint64_t x1 = max_u64(A[2 * lane + 1], B[126 - 2 * lane]);
+            wave_bitonic128_desc<128>(x0, x1);
+            sm.runs[2 * wave][2 * lane] = x0;
+            sm.runs[2 * wave][2 * lane + 1] = x1;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint64_t f[2];
+            f[0] = max_u64(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
+            f[1] = max_u64(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
+            wave_bitonic128_desc<128>(f[0], f[1]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int e = 2 * lane + i;
+                if (e < k) {
+                    const uint32_t key = (uint32_t)(f[i] >> 32);
+                    const int col = (int)(0xffffffffu - (uint32_t)f[i]);
+                    const int64_t o = (int64_t)row * k + e;
+                    if (F32) {
+                        ((float *)a.values)[o] = __uint_as_float(unkey32(key));
+                    } else {
+                        ((uint16_t *)a.values)[o] = (uint16_t)unkey16(key);
+                    }
+                    a.indices[o] = col < V ? col : V - 1;
+                }
+            }
+        }
+        return;
+    }
     uint32_t thi, margin;
     int level;
     constexpr int EM = 16;
-    const int ncand = tiles * k;
     const int nsc = (ncand + SS_BLOCK * EM - 1) / (SS_BLOCK * EM);
     auto cand_load = [&](int sc, uint32_t(&out)[EM]) {
 #pragma unroll

@@ -112,8 +112,8 @@ __device__ __forceinline__ void round_all(float (&x)[E]) {
 }
 
 // Divisor state of a per-row constant d: rcp = 1/d from v_rcp_f32 (within 1 ulp); `fast` is
-// false when d is 0, infinite or NaN or the reciprocal is not a finite nonzero value, where the
-// plain IEEE quotient is used instead.
+// false when d is 0, infinite or NaN or the reciprocal is not a normal number (|d| near the ends
+// of the fp32 range), where the plain IEEE quotient is used instead.
 struct Divisor {
     float d, rcp;
     bool fast;
@@ -123,7 +123,7 @@ __device__ __forceinline__ Divisor make_divisor(float d) {
     Divisor v;
     v.d = d;
     v.rcp = __builtin_amdgcn_rcpf(d);
-    v.fast = d != 0.0f && __builtin_isfinite(d) && __builtin_isfinite(v.rcp) && v.rcp != 0.0f;
+    v.fast = d != 0.0f && __builtin_isfinite(d) && __builtin_isnormal(v.rcp);
     return v;
 }
 

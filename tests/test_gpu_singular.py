@@ -199,3 +199,51 @@ def test_concentrated_and_tied_rows(seed):
     state = oracle.State.from_buffers(host)
     expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=8)
     check_singular(selection, expected, logprobs=True)
+
+
+def test_extreme_divisors_and_penalties():
+    """Rows whose divisors fall outside the reciprocal fast path (a subnormal temperature, a
+    subnormal repetition penalty on counted tokens, a temperature near the top of the bf16 range)
+    and a huge frequency penalty: the IEEE chain runs on every element, +inf and tiny values tie
+    in long runs, and the tokens must match the oracle. Top-k only and no logprobs, so no softmax
+    ever sees an infinity."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, ScopedIndicators
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    rows, vocab = 16, 16384
+    bf = lambda v: float(torch.tensor(v).to(torch.bfloat16))  # noqa: E731
+    temperature = [bf(1e-39)] * 4 + [bf(0.8)] * 4 + [bf(3e38)] * 4 + [1.0] * 4
+    multiplicative = [1.0] * 4 + [bf(1e-39)] * 4 + [1.0] * 8
+    frequency = [0.0] * 12 + [bf(1e30)] * 4
+    top_k = [50] * 4 + [20] * 4 + [128] * 4 + [64] * 4
+    scoped = ScopedIndicators.from_params(
+        size=rows, timesteps=1, multiplicative=multiplicative, frequency=frequency,
+        presence=[0.0] * rows, biases=[{} for _ in range(rows)], temperature=temperature,
+        top_k=top_k, top_p=[1.0] * rows, min_p=[0.0] * rows, top_logprobs=[0] * rows,
+    )
+    g = torch.Generator().manual_seed(5)
+    host = SamplingBuffers.default(size=rows, timesteps=1, vocab_size=vocab, device="cpu", noise=False)
+    host.flags = Flags.from_scoped(scoped, device="cpu")
+    host.weights.gumbel.target.exponential_(1.0, generator=g).log_()
+    host.temperature.copy_(torch.tensor(temperature).to(torch.bfloat16))
+    host.top_k.copy_(torch.tensor(top_k, dtype=torch.int32))
+    rep = host.repetition
+    rep.multiplicative.copy_(torch.tensor(multiplicative).to(torch.bfloat16))
+    rep.frequency.copy_(torch.tensor(frequency).to(torch.bfloat16))
+    history = torch.randint(0, vocab, (rows, 256), generator=g)
+    rep.counts.decode.zero_().scatter_add_(1, history, torch.ones_like(history, dtype=torch.int32))
+    logits = spiked_logits(rows, vocab, seed=404)
+    buffers = to_device(host, DEV)
+    print("extreme divisors and penalties", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, block_size=2048, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=False)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=False)
+    tokens = selection.tokens[:, 0].cpu()
+    assert [int(t) for t in tokens] == [e.token for e in expected]

@@ -111,17 +111,16 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
 __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
+    touch_kernargs<sizeof(ss_multistep_args)>();
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     RowSamples smp;
-    load_samples(scr, tiles, smp);  // depends on the row only: issued first
+    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
     const Request rq = resolve_request(a, row);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
-    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, rq.b) : rq.b;
-    const uint32_t ind = uniform_u16(a.indicators, slot);
-    const int32_t topk = a.top_k ? uniform_i32(a.top_k, slot) : SS_K;
-    const float topp = a.top_p ? bf2f(uniform_u16(a.top_p, slot)) : 1.0f;
-    const float minp = a.min_p ? bf2f(uniform_u16(a.min_p, slot)) : 0.0f;
+    const int slot = opt_i32(a.slot_mapping, rq.b, scr, rq.b);
+    const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, nullptr, slot, 0);
+    const uint32_t ind = lane_u32(prm, RP_IND);
     float *vrow = a.values + (int64_t)row * SS_K;
     int32_t *irow = a.indices + (int64_t)row * SS_K;
     if (ind & IND_GREEDY) {
@@ -138,7 +137,8 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     int i0 = 0, i1 = 0;
     merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
     if (threadIdx.x >= 64) return;
-    truncate(ind, topk, topp, minp, v0, v1);
+    truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
+             __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
     float m, x0, x1;
     const float logs = logf(exp_parts(v0, v1, m, x0, x1));
     const int e0 = 2 * threadIdx.x;
@@ -150,6 +150,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
 
 // Request stage: grid B, one wavefront per request.
 __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args a) {
+    touch_kernargs<sizeof(ss_multistep_args)>();
     const int b = blockIdx.x;
     Request rq;
     if (a.cu_seqlens) {

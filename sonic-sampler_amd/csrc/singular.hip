@@ -63,15 +63,14 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
 // Row stage of one row: merge of the tiles' candidates and the selection. All threads call.
 __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSmem &sm, int row,
                                              int tiles) {
+    touch_kernargs<sizeof(ss_singular_args)>();
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     RowSamples smp;
-    load_samples(scr, tiles, smp);  // depends on the row only: issued first
-    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
-    const uint32_t ind = uniform_u16(a.indicators, slot);
-    const int32_t topk = a.top_k ? uniform_i32(a.top_k, slot) : SS_K;
-    const float topp = a.top_p ? bf2f(uniform_u16(a.top_p, slot)) : 1.0f;
-    const float minp = a.min_p ? bf2f(uniform_u16(a.min_p, slot)) : 0.0f;
-    const int top_lim = a.top_logprobs ? uniform_i32(a.top_logprobs, slot) : a.max_top_logprobs;
+    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
+    const int slot = opt_i32(a.slot_mapping, row, scr, row);
+    const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
+                                    a.max_top_logprobs);
+    const uint32_t ind = lane_u32(prm, RP_IND);
 
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
@@ -112,7 +111,9 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
                           : bf2f(a.gumbel[(int64_t)slot * a.stride_gumbel + t]);
         sm.tok[e] = t;
     }
-    if (wave == 0) truncate(ind, topk, topp, minp, v0, v1);
+    if (wave == 0)
+        truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
+                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
     __syncthreads();
     if (wave != 0) return;
     i0 = sm.tok[e0];
@@ -150,6 +151,7 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
             const float osel = lane_f32((sel & 1) ? o1 : o0, sel >> 1);
             if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
             if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
+                const int top_lim = (int)lane_u32(prm, RP_TOPZ);
                 const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
                 const int64_t o = (int64_t)row * a.stride_top;
                 if (e0 < lim) {

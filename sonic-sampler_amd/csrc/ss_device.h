@@ -200,6 +200,20 @@ __device__ __forceinline__ uint32_t lane_select(uint64_t m, uint32_t a, uint32_t
     return r;
 }
 
+// Reads one dword of every 64-byte line of the kernel's first BYTES argument bytes, all issued
+// before one wait: the argument reads spread over the kernel then find their lines in the scalar
+// cache instead of each waiting for a memory round trip of its own. Worth it in kernels run by
+// one workgroup per row, whose waves have nothing else to hide that latency with.
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+    typedef const __attribute__((address_space(4))) uint32_t kword;
+    kword *p = (kword *)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t acc = 0;
+#pragma unroll
+    for (int o = 0; o < BYTES / 4; o += 16) acc ^= p[o];
+    asm volatile("" ::"s"(acc));
+}
+
 // Value of lane `src` (uniform) in every lane, through the scalar unit.
 __device__ __forceinline__ uint32_t lane_u32(uint32_t v, int src) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, __builtin_amdgcn_readfirstlane(src));

@@ -359,6 +359,47 @@ __device__ __forceinline__ float param_bf16(const uint16_t *p, const uint16_t *a
     return p ? bf2f(h) : dflt;
 }
 
+// Per-request parameters of a row stage, read with one vector load into one register of every
+// wave: lane RP_IND the indicator word, RP_TOPK top_k (SS_K when absent), RP_TOPP / RP_MINP the
+// fp32 bits of top_p / min_p (1 / 0 when absent), RP_TOPZ the top-logprob count (dflt_topz when
+// absent). Read as scalars they would be live across the merge, whose register pressure spills
+// each one right after its load, so that the reads would wait one after another.
+enum { RP_IND = 0, RP_TOPK = 1, RP_TOPP = 2, RP_MINP = 3, RP_TOPZ = 4 };
+
+__device__ __forceinline__ uint32_t row_params(const uint16_t *ind, const int32_t *topk,
+                                               const uint16_t *topp, const uint16_t *minp,
+                                               const int32_t *topz, int slot, int dflt_topz) {
+    const int lane = lane_id();
+    const void *p = lane == RP_IND    ? (const void *)ind
+                    : lane == RP_TOPK ? (const void *)topk
+                    : lane == RP_TOPP ? (const void *)topp
+                    : lane == RP_MINP ? (const void *)minp
+                    : lane == RP_TOPZ ? (const void *)topz
+                                      : nullptr;
+    const bool wide = lane == RP_TOPK || lane == RP_TOPZ;
+    uint32_t v = lane == RP_TOPK   ? (uint32_t)SS_K
+                 : lane == RP_TOPP ? 0x3f800000u
+                 : lane == RP_TOPZ ? (uint32_t)dflt_topz
+                                   : 0u;
+    if (p) {
+        // 16-bit fields as the aligned dword holding them
+        const uintptr_t addr = (uintptr_t)p + (uintptr_t)slot * (wide ? 4u : 2u);
+        const uint32_t w = *(const uint32_t *)(addr & ~(uintptr_t)3);
+        v = wide ? w : (addr & 2) ? (w >> 16) : (w & 0xffffu);
+        if (lane == RP_TOPP || lane == RP_MINP) v <<= 16;
+    }
+    return v;
+}
+
+// p[idx], or `dflt` when p is NULL; `valid` is any readable 4-byte aligned address, read instead
+// of a NULL p so that optional reads issue unbranched and wait together.
+__device__ __forceinline__ int32_t opt_i32(const int32_t *p, int idx, const void *valid,
+                                           int32_t dflt) {
+    const uintptr_t addr = p ? (uintptr_t)(p + idx) : (uintptr_t)valid;
+    const int32_t w = (int32_t)*(const_u32p)addr;
+    return p ? w : dflt;
+}
+
 // Direct layout (no d2t remap, vocabulary a multiple of 4, 8 / 16-byte aligned rows): the side
 // planes of one tile -- grammar words, decode and context counts, bias -- as loaded words.
 template <int E>
@@ -886,10 +927,18 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
 struct RowSamples {
     uint32_t raw[2];   // list entries of the thread's two elements (0 past the last slot)
     int slot[2];       // their sample slots s = list * kp + position
+    int base[2];       // first column of their lists' tiles
     uint32_t next;
+    int kp;            // merged prefix length of every list
+    uint32_t kpm;      // ceil(2^16 / kp): (s * kpm) >> 16 == s / kp for every slot s < 512
 };
 
 __device__ __forceinline__ int merge_prefix(int tiles) { return min(SS_K, (4 * SS_K) / tiles); }
+
+// List of sample slot s (< 512).
+__device__ __forceinline__ int slot_list(const RowSamples &smp, int s) {
+    return (int)(((uint32_t)s * smp.kpm) >> 16);
+}
 
 // Run length of whole sorted lists placed in a wave's 128 elements: kp when kp is a power of two
 // from 8 to 64 (then 128 / kp lists per wave, odd ones reversed, so that the bitonic network can
@@ -898,24 +947,30 @@ __device__ __forceinline__ int merge_run(int kp) {
     return (kp >= 8 && kp <= 64 && (kp & (kp - 1)) == 0) ? kp : 1;
 }
 
-__device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, RowSamples &smp) {
+__device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int block_n,
+                                             RowSamples &smp) {
     const int kp = merge_prefix(tiles);
+    smp.kp = kp;
+    smp.kpm = (65536u + (uint32_t)kp - 1u) / (uint32_t)kp;
     const int ns = tiles * kp;  // <= 512
     const int run = merge_run(kp);
     const int wave = (int)threadIdx.x >> 6, lane = lane_id();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        int s;
+        int s, list;
         if (run > 1) {
             // element e = 2 * lane + i of the wave: run r = e / kp, i.e. list 128 / kp * wave + r
+            const int lr = __builtin_ctz((unsigned)run);
             const int e = 2 * lane + i;
-            const int r = e / run, q = e - r * run;
-            s = (wave * (SS_K / run) + r) * run + ((r & 1) ? run - 1 - q : q);
+            const int r = e >> lr, q = e & (run - 1);
+            list = wave * (SS_K >> lr) + r;
+            s = (list << lr) + ((r & 1) ? run - 1 - q : q);
         } else {
-            s = 2 * ((int)threadIdx.x & ~63) + 2 * lane + i;  // any placement
+            s = 2 * (int)threadIdx.x + i;  // any placement
+            list = slot_list(smp, s);
         }
-        const int list = s / kp;
         smp.slot[i] = s;
+        smp.base[i] = list * block_n;
         smp.raw[i] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
     }
     const int t = (int)threadIdx.x;
@@ -938,7 +993,7 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
                                           float &v0, float &v1, int &i0, int &i1) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
-    const int kp = merge_prefix(tiles);
+    const int kp = smp.kp;
     uint32_t c[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -946,7 +1001,7 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
         uint32_t comp = 0;
         const uint32_t raw = smp.raw[i];
         if (raw) {
-            const int idx = (s / kp) * block_n + (int)(0xffffu - (raw & 0xffffu));
+            const int idx = smp.base[i] + (int)(0xffffu - (raw & 0xffffu));
             sm.col[s] = idx < V ? idx : V - 1;
             comp = (raw & 0xffff0000u) | (0xffffu - (uint32_t)s);
         }
@@ -980,17 +1035,18 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
         f0 = max(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
         f1 = max(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
         wave_bitonic128_desc<128>(f0, f1);
-        // exactness check: no list's first unmerged entry may beat the 128th merged element
+        // exactness check: no list's first unmerged entry may beat the 128th merged element.
+        // At equal keys the entry of list t comes first iff t is below the list of that element:
+        // tiles are in column order and a list's unmerged entries follow its merged ones.
         const uint32_t last = lane_u32(f1, 63);
         const uint32_t klast = last >> 16;
-        const int ilast = last ? sm.col[0xffffu - (last & 0xffffu)] : V;
+        const int llast = last ? slot_list(smp, (int)(0xffffu - (last & 0xffffu))) : tiles;
         bool beat = false;
         if (kp < SS_K) {
             for (int t = lane; t < tiles; t += 64) {
                 const uint32_t nx = t < 64 ? smp.next : scr[t * SS_K + kp];
                 const uint32_t kn = nx >> 16;
-                const int in = t * block_n + (int)(0xffffu - (nx & 0xffffu));
-                beat |= nx != 0u && (kn > klast || (kn == klast && in < ilast));
+                beat |= nx != 0u && (kn > klast || (kn == klast && t < llast));
             }
         }
         const bool any = __ballot(beat) != 0;

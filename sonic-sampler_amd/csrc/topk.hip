@@ -85,6 +85,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_tiles_kernel(ss_topk_args a, in
 // Merge stage: grid rows.
 template <bool F32>
 __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, int tiles) {
+    touch_kernargs<sizeof(ss_topk_args)>();
     using Tr = TopkTraits<F32>;
     using Cand = typename Tr::Cand;
     constexpr int CH = 4;
@@ -100,6 +101,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
         // of bitonic merges keep the top-128 of the four runs (the elementwise maximum of a run
         // and its reversed partner is a bitonic sequence holding the top-128 of both).
         const int lane = lane_id(), wave = (int)threadIdx.x >> 6;
+        const int lk = __builtin_ctz((unsigned)k);  // k is a power of two
         uint64_t c[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
             uint64_t v = 0;
             if (p < ncand) {
                 const Cand cd = scr[p];
-                const uint32_t col = (uint32_t)((p / k) * a.block_n + Tr::cand_li(cd));
+                const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
                 v = ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
             }
             c[i] = v;

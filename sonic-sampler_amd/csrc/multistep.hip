@@ -18,18 +18,31 @@ struct Request {
     int b, margin, n;
 };
 
-__device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, int row) {
+// The lane's pivot of the first round of resolve_request's search, cu_seqlens[lane * step] with
+// step = ceil(batch / 64) (INT_MAX past the end; 0 without cu_seqlens). Kernels issue it ahead of
+// their bulk loads: vector loads return in order, so behind a tile of logits it would wait for the
+// whole tile, and the request's reads that depend on it would start only then.
+__device__ __forceinline__ int request_pivot(const ss_multistep_args &a) {
+    if (!a.cu_seqlens) return 0;
+    const int p = lane_id() * ((a.batch + 63) >> 6);
+    return p < a.batch ? a.cu_seqlens[p] : INT_MAX;
+}
+
+__device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, int row, int pivot) {
     Request r;
     if (a.cu_seqlens) {
         // Every wave searches on its own: each round tests 64 evenly spaced pivots of (lo, hi), so
         // one round of loads resolves up to 64 requests and two up to 4096 (cu_seqlens is
-        // non-decreasing, so the pivots at or below `row` are a prefix of the lanes).
+        // non-decreasing, so the pivots at or below `row` are a prefix of the lanes). The first
+        // round's pivots (lo = 0, hi = batch) come from request_pivot.
         const int lane = lane_id();
         int lo = 0, hi = a.batch;  // invariant: cu[lo] <= row < cu[hi]
+        bool first = true;
         while (hi - lo > 1) {
             const int step = (hi - lo + 63) >> 6;
             const int p = lo + lane * step;
-            const bool le = p < hi && a.cu_seqlens[p] <= row;
+            const bool le = p < hi && (first ? pivot : a.cu_seqlens[p]) <= row;
+            first = false;
             const uint64_t m = __ballot(le);  // lane 0 (pivot lo) is set unless cu[0] > row
             if (!m) break;
             const int k = 63 - __clzll((long long)m);
@@ -37,8 +50,8 @@ __device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, i
             hi = min(lo + step, hi);
         }
         r.b = lo;
-        r.margin = a.cu_seqlens[lo];
-        r.n = a.cu_seqlens[lo + 1] - r.margin;
+        r.margin = uniform_i32(a.cu_seqlens, lo);
+        r.n = uniform_i32(a.cu_seqlens, lo + 1) - r.margin;
     } else {
         r.n = a.lookahead + 1;
         r.b = row / r.n;
@@ -86,12 +99,13 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
     __shared__ TileSmem sm;
     const int row = blockIdx.y;
     const int tile = blockIdx.x;
+    const int pivot = request_pivot(a);
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
-    const Request rq = resolve_request(a, row);
+    const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
-    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, rq.b) : rq.b;
     const uint32_t ind = uniform_u16(a.indicators, slot);
     RowState rs = multistep_row_state(a, row, step, slot, ind);
     if (step > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
@@ -113,12 +127,13 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     const int row = blockIdx.x;
     touch_kernargs<sizeof(ss_multistep_args)>();
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    const int pivot = request_pivot(a);
     RowSamples smp;
-    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
-    const Request rq = resolve_request(a, row);
+    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued early
+    const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
-    const int slot = opt_i32(a.slot_mapping, rq.b, scr, rq.b);
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, rq.b) : rq.b;
     const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, nullptr, slot, 0);
     const uint32_t ind = lane_u32(prm, RP_IND);
     float *vrow = a.values + (int64_t)row * SS_K;

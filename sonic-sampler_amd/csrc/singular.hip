@@ -67,7 +67,7 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     RowSamples smp;
     load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
-    const int slot = opt_i32(a.slot_mapping, row, scr, row);
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
     const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
                                     a.max_top_logprobs);
     const uint32_t ind = lane_u32(prm, RP_IND);

@@ -391,15 +391,6 @@ __device__ __forceinline__ uint32_t row_params(const uint16_t *ind, const int32_
     return v;
 }
 
-// p[idx], or `dflt` when p is NULL; `valid` is any readable 4-byte aligned address, read instead
-// of a NULL p so that optional reads issue unbranched and wait together.
-__device__ __forceinline__ int32_t opt_i32(const int32_t *p, int idx, const void *valid,
-                                           int32_t dflt) {
-    const uintptr_t addr = p ? (uintptr_t)(p + idx) : (uintptr_t)valid;
-    const int32_t w = (int32_t)*(const_u32p)addr;
-    return p ? w : dflt;
-}
-
 // Direct layout (no d2t remap, vocabulary a multiple of 4, 8 / 16-byte aligned rows): the side
 // planes of one tile -- grammar words, decode and context counts, bias -- as loaded words.
 template <int E>

@@ -623,6 +623,22 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     if constexpr (MODE == MODE_DIRECT) {
         if (!(u.g || u.rep || u.mult || u.bias)) {
             plain_keys<E>(rs, u, col0, V, lw, keys);
+        } else if constexpr (E == 32) {
+            // The processor chain in two 4096-column halves: element j of the second half is
+            // element j + 16 of the tile (4 chunks of 1024 columns further). Its per-element
+            // state for all 32 elements at once would set the kernel's register allocation, and so
+            // its occupancy, for every row (144 VGPRs, three waves per SIMD, against 90 for the
+            // plain rows alone).
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const u32x2 lh[4] = {lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]};
+                Planes<16> pl;
+                issue_planes<16>(rs, u, true, col0 + 4 * 4 * SS_BLOCK * h, pl);
+                Keys<16> kh;
+                direct_keys<16>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, pl, kh);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
+            }
         } else {
             Planes<E> pl;
             issue_planes<E>(rs, u, true, col0, pl);

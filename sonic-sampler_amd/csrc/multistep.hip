@@ -165,7 +165,6 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
 
 // Request stage: grid B, one wavefront per request.
 __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args a) {
-    touch_kernargs<sizeof(ss_multistep_args)>();
     const int b = blockIdx.x;
     Request rq;
     if (a.cu_seqlens) {

@@ -212,13 +212,35 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
     } else {
         // Draft positions VCH at a time: every load of a chunk is issued before any result is
         // used (rows at and past n - 1 read row n - 2 and are ignored), so a chunk costs two
-        // rounds of loads (candidate rows, then the drafted token's value and draft probability)
-        // instead of two per position.
+        // rounds of loads instead of two per position: first the candidate rows (the lane's two
+        // candidate tokens and values of each row), then the drafted token's value and draft
+        // probability. The top logprobs and a rejected row's candidates then need no further
+        // loads; only the residual's draft probabilities at the rejected row's candidates are
+        // gathered once that row is known (gathering them for every row of a chunk costs more
+        // scattered reads than the round trip it saves).
         constexpr int VCH = 8;
         const uint16_t *u = a.uniform + (int64_t)slot * a.stride_uniform;
-        for (int base = 0; base < n - 1; base += VCH) {
+        const bool want_top = want_lp && (ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0;
+        const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
+        // top logprobs of row r from its candidate pairs
+        auto write_top = [&](int r, int2 tok, float2 val) {
+            const int64_t o = (int64_t)(rq.margin + r) * a.stride_top;
+            if (e0 < lim) {
+                a.top_values[o + e0] = (uint16_t)f2bf(val.x);
+                a.top_tokens[o + e0] = tok.x;
+            }
+            if (e1 < lim) {
+                a.top_values[o + e1] = (uint16_t)f2bf(val.y);
+                a.top_tokens[o + e1] = tok.y;
+            }
+        };
+        int2 cj = make_int2(0, 0);          // row j's candidate tokens (lane pair)
+        float2 lj = make_float2(0.f, 0.f);  // their log-softmax values
+        bool rejected = false;
+        for (int base = 0; base < n - 1 && !rejected; base += VCH) {
             int d[VCH], pos[VCH];
             int2 w[VCH];
+            float2 vv[VCH];
             float uk[VCH];
 #pragma unroll
             for (int k = 0; k < VCH; ++k) {
@@ -226,6 +248,7 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
                 d[k] = drafted[r];
                 uk[k] = bf2f(u[r]);
                 w[k] = *(const int2 *)(idxs + (int64_t)r * SS_K + e0);
+                vv[k] = *(const float2 *)(vals + (int64_t)r * SS_K + e0);
             }
             float v[VCH], qd[VCH];
 #pragma unroll
@@ -251,22 +274,30 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
             }
             // logprobs of the accepted positions: the value at the drafted token's position, or
             // at position 0 when the token is not among the candidates (argmax of an all-false
-            // match row, core/naive.py:580-584)
-            if (want_lp && lane == 0) {
+            // match row, core/naive.py:580-584); top logprobs of rows up to the rejected one
 #pragma unroll
-                for (int k = 0; k < VCH; ++k)
-                    if ((rej < 0 || k < rej) && base + k < n - 1)
-                        a.logprobs[rq.margin + base + k] = (uint16_t)f2bf(v[k]);
+            for (int k = 0; k < VCH; ++k) {
+                if (base + k >= n - 1 || (rej >= 0 && k > rej)) break;
+                if (want_lp && lane == 0 && k != rej) a.logprobs[rq.margin + base + k] = (uint16_t)f2bf(v[k]);
+                if (want_top) write_top(base + k, w[k], vv[k]);
+                if (k == rej) {
+                    cj = w[k];
+                    lj = vv[k];
+                }
             }
             if (rej >= 0) {
                 j = base + rej;
-                break;
+                rejected = true;
             }
         }
-        const int32_t *cj = idxs + (int64_t)j * SS_K;
-        const float *lj = vals + (int64_t)j * SS_K;
-        const int c0 = cj[e0], c1 = cj[e1];
-        const float p0 = expf(lj[e0]), p1 = expf(lj[e1]);
+        if (!rejected) {
+            // every draft accepted: the bonus row n - 1
+            cj = *(const int2 *)(idxs + (int64_t)j * SS_K + e0);
+            lj = *(const float2 *)(vals + (int64_t)j * SS_K + e0);
+            if (want_top) write_top(j, cj, lj);
+        }
+        const int c0 = cj.x, c1 = cj.y;
+        const float p0 = expf(lj.x), p1 = expf(lj.y);
         float r0, r1;
         if (j == n - 1) {
             r0 = p0;
@@ -277,9 +308,9 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
             r0 = c0 == dj ? 0.0f : p0;
             r1 = c1 == dj ? 0.0f : p1;
         } else {
-            const uint16_t *qj = q + (int64_t)j * a.probs_stride_step;
-            r0 = fmaxf(p0 - bf2f(qj[c0]), 0.0f);
-            r1 = fmaxf(p1 - bf2f(qj[c1]), 0.0f);
+            const uint16_t *qr = q + (int64_t)j * a.probs_stride_step;
+            r0 = fmaxf(p0 - bf2f(qr[c0]), 0.0f);
+            r1 = fmaxf(p1 - bf2f(qr[c1]), 0.0f);
         }
         float w0, w1;
         if (a.philox.enabled) {
@@ -293,38 +324,10 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
         }
         const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
         token = lane_i32((sel & 1) ? c1 : c0, sel >> 1);
-
-        if (want_lp) {
-            // positions before j were written during verification
-            if (lane == 0) a.logprobs[rq.margin + j] = (uint16_t)f2bf(vals[(int64_t)j * SS_K + sel]);
-            if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
-                // rows 0..j eight at a time, every load of a group issued before its stores
-                for (int base = 0; base <= j; base += 8) {
-                    float2 v[8];
-                    int2 t[8];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const int64_t s = (int64_t)min(base + k, j) * SS_K + e0;
-                        v[k] = *(const float2 *)(vals + s);
-                        t[k] = *(const int2 *)(idxs + s);
-                    }
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        if (base + k > j) break;
-                        const int64_t o = (int64_t)(rq.margin + base + k) * a.stride_top;
-                        if (e0 < lim) {
-                            a.top_values[o + e0] = (uint16_t)f2bf(v[k].x);
-                            a.top_tokens[o + e0] = t[k].x;
-                        }
-                        if (e1 < lim) {
-                            a.top_values[o + e1] = (uint16_t)f2bf(v[k].y);
-                            a.top_tokens[o + e1] = t[k].y;
-                        }
-                    }
-                }
-            }
-        }
+        // row j's logprob: the selected candidate's value (positions before j were written
+        // during verification)
+        const float lsel = lane_f32((sel & 1) ? lj.y : lj.x, sel >> 1);
+        if (want_lp && lane == 0) a.logprobs[rq.margin + j] = (uint16_t)f2bf(lsel);
     }
     if (greedy && a.return_logprobs && a.logprobs) {
         if (lane <= j) a.logprobs[rq.margin + lane] = 0;

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     int32_t *irow = a.indices + (int64_t)row * SS_K;
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
-            const int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
+            const int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, smp.greedy);
             if (threadIdx.x == 0) {
                 irow[0] = token;
                 vrow[0] = 0.0f;

@@ -74,7 +74,7 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
 
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
-            int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size);
+            int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, smp.greedy);
             if (a.d2t) token = a.d2t[token];
             if (threadIdx.x == 0) {
                 if (a.update_counts && a.decode_counts) {

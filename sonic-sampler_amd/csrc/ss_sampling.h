@@ -846,10 +846,12 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const Keys
 }
 
 // Greedy merge over the tiles' maxima (wave 0): the largest value, lowest column on ties.
-__device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int block_n, int V) {
+// `first` is scr[lane], read ahead by load_samples.
+__device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int block_n, int V,
+                                            uint32_t first) {
     uint64_t best = 0;
     for (int t = lane_id(); t < tiles; t += 64) {
-        const uint32_t c = scr[t];
+        const uint32_t c = t < 64 ? first : scr[t];
         const uint64_t c64 = ((uint64_t)(c >> 16) << 32) | ((uint64_t)(0xffffu - (uint32_t)t) << 16) |
                              (uint64_t)(c & 0xffffu);
         best = best > c64 ? best : c64;
@@ -936,6 +938,7 @@ struct RowSamples {
     int slot[2];       // their sample slots s = list * kp + position
     int base[2];       // first column of their lists' tiles
     uint32_t next;
+    uint32_t greedy;   // wave 0: tile t = lane's greedy composite, had the row been greedy
     int kp;            // merged prefix length of every list
     uint32_t kpm;      // ceil(2^16 / kp): (s * kpm) >> 16 == s / kp for every slot s < 512
 };
@@ -982,6 +985,9 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int
     }
     const int t = (int)threadIdx.x;
     smp.next = (t < 64 && t < tiles && kp < SS_K) ? scr[t * SS_K + kp] : 0u;
+    // read before the row's indicator is known, so that a greedy row's merge waits for no
+    // further load
+    smp.greedy = (t < 64 && t < tiles) ? scr[t] : 0u;
 }
 
 // Row merge over the tiles' sorted candidate lists, from the samples of load_samples. All threads

@@ -961,7 +961,9 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int
                                              RowSamples &smp) {
     const int kp = merge_prefix(tiles);
     smp.kp = kp;
-    smp.kpm = (65536u + (uint32_t)kp - 1u) / (uint32_t)kp;
+    // above 512 tiles kp is 0: nothing is merged and the exactness check sends the row to the
+    // radix merge
+    smp.kpm = kp ? (65536u + (uint32_t)kp - 1u) / (uint32_t)kp : 0u;
     const int ns = tiles * kp;  // <= 512
     const int run = merge_run(kp);
     const int wave = (int)threadIdx.x >> 6, lane = lane_id();

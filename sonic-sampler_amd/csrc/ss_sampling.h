@@ -516,39 +516,40 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
     bool all_exc;
     const Chain k = row_chain(rs, u, all_exc);
 
-    float x[E];
+    // logits and bias stay in bf16 pairs (element 2i in the low half), as loaded: widened where
+    // they are used, they would hold one register per element
+    u32x2 lv[NCH];
     bool ok[E];
     const __amdgpu_buffer_rsrc_t lg = row_buffer(rs.logits, (int64_t)V * 2);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int base = col0 + c * (SS_BLOCK * 4);  // uniform
         if (VEC) {
-            const u32x2 w = lw[c];
-            x[4 * c + 0] = __uint_as_float(w.x << 16);
-            x[4 * c + 1] = __uint_as_float(w.x & 0xffff0000u);
-            x[4 * c + 2] = __uint_as_float(w.y << 16);
-            x[4 * c + 3] = __uint_as_float(w.y & 0xffff0000u);
+            lv[c] = lw[c];
             const bool in = base + lane4 < V;
 #pragma unroll
             for (int i = 0; i < 4; ++i) ok[4 * c + i] = in;
         } else {
+            uint32_t h[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(lg, (lane4 + i) * 2, base * 2, NT);
-                x[4 * c + i] = __uint_as_float(h << 16);
+                h[i] = __builtin_amdgcn_raw_buffer_load_b16(lg, (lane4 + i) * 2, base * 2, NT);
                 ok[4 * c + i] = base + lane4 + i < V;
             }
+            lv[c].x = h[0] | (h[1] << 16);
+            lv[c].y = h[2] | (h[3] << 16);
         }
     }
 
     int32_t dec[E], ctx[E];
-    uint32_t bbits[E];
+    uint32_t bpk[E / 2];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         dec[j] = 0;
         ctx[j] = 0;
-        bbits[j] = 0;
     }
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) bpk[i] = 0;
     if (u.g || u.rep || u.bias) {
         int tcol[E];
 #pragma unroll
@@ -572,8 +573,12 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
             const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
 #pragma unroll
             for (int j = 0; j < E; ++j) {
+                // a masked element becomes bf16 -inf (0xff80) in place
                 const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
-                x[j] = ((w >> (tcol[j] & 31)) & 1u) ? x[j] : -INFINITY;
+                const bool keep = ((w >> (tcol[j] & 31)) & 1u) != 0u;
+                uint32_t p = (j & 2) ? lv[j >> 2].y : lv[j >> 2].x;
+                p = keep ? p : (j & 1) ? ((p & 0x0000ffffu) | 0xff800000u) : ((p & 0xffff0000u) | 0xff80u);
+                if (j & 2) lv[j >> 2].y = p; else lv[j >> 2].x = p;
             }
         }
         if (u.rep) {
@@ -598,12 +603,18 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
             const __amdgpu_buffer_rsrc_t b = row_buffer(rs.bias, (int64_t)rs.vt * 2);
 #pragma unroll
             for (int j = 0; j < E; ++j)
-                bbits[j] = __builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << 16;
+                bpk[j >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b, tcol[j] * 2, 0, 0) << (16 * (j & 1));
         }
     }
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, [&](int j) { return x[j]; },
-                   all_exc || u.rep || u.mult || u.bias, ok, dec, ctx,
-                   [&](int j) { return bbits[j]; }, [&](int j) { return bbits[j] << 1; }, keys);
+    auto x = [&](int j) {
+        const uint32_t w = (j & 2) ? lv[j >> 2].y : lv[j >> 2].x;
+        return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+    };
+    auto bb = [&](int j) { return (j & 1) ? (bpk[j >> 1] & 0xffff0000u) : (bpk[j >> 1] << 16); };
+    // the bias word of the element's pair, shifted so that -0 in the high half does not count
+    auto bw = [&](int j) { return bpk[j >> 1] << 1; };
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, all_exc || u.rep || u.mult || u.bias, ok,
+                   dec, ctx, bb, bw, keys);
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:

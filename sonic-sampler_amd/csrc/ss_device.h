@@ -202,8 +202,10 @@ __device__ __forceinline__ uint32_t lane_select(uint64_t m, uint32_t a, uint32_t
 
 // Reads one dword of every 64-byte line of the kernel's first BYTES argument bytes, all issued
 // before one wait: the argument reads spread over the kernel then find their lines in the scalar
-// cache instead of each waiting for a memory round trip of its own. Worth it in kernels run by
-// one workgroup per row, whose waves have nothing else to hide that latency with.
+// cache instead of each waiting for a memory round trip of its own. Worth it in the row stages,
+// which read arguments from most lines at different points of one dependent chain; a kernel
+// whose first reads need only a few lines (the verify stage) loses more by waiting for all of
+// them first than it saves later.
 template <int BYTES>
 __device__ __forceinline__ void touch_kernargs() {
     typedef const __attribute__((address_space(4))) uint32_t kword;

@@ -165,14 +165,19 @@ def c2_workload(seed: int = 1002, batch: int = 128, gamma: int = 4, vocab: int =
                              vocab=vocab, max_top_logprobs=5)
 
 
-def c3_workload(seed: int = 1003, batch: int = 64, gamma: int = 7, vocab: int = 128256) -> MultistepWorkload:
-    """Config 3: stochastic verification, variable lookahead U{1..7}, top-20 logprobs."""
+def c3_workload(seed: int = 1003, batch: int = 64, gamma: int = 7, vocab: int = 128256,
+                lengths: Optional[List[int]] = None) -> MultistepWorkload:
+    """Config 3: stochastic verification, variable lookahead U{1..7}, top-20 logprobs.
+
+    ``lengths`` (rows per request, each within [2, gamma + 1]) fixes the request layout; by default
+    it is drawn from the seed."""
 
     from sonic_sampler.core.buffer import SamplingBuffers
     from sonic_sampler.core.flags import Flags, Indicator
 
     g = torch.Generator("cpu").manual_seed(seed + 7)
-    lengths = (torch.randint(1, gamma + 1, (batch,), generator=g) + 1).tolist()
+    drawn = (torch.randint(1, gamma + 1, (batch,), generator=g) + 1).tolist()
+    lengths = drawn if lengths is None else list(lengths)
     cu = [0]
 
     for length in lengths:
@@ -348,39 +353,71 @@ def measured_traffic(kernel: str, batch: int, vocab: int) -> Optional[int]:
         return None
 
 
-def cpu_baseline_c1(workload: SingularWorkload, rows: int) -> dict:
-    """The CPU restatement of the reference's PyTorch path on `rows` rows of config 1."""
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu reports it), or the machine type."""
 
+    try:
+
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+
+            if line.startswith("model name"):
+
+                return line.split(":", 1)[1].strip()
+
+    except OSError:
+
+        pass
+
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline_c1(workload: SingularWorkload, budget_s: float = 15.0) -> dict:
+    """The reference's PyTorch path restated in ``oracle/batch.py``, one call over the whole
+    config-1 batch (as the reference's ``NaiveSampler`` runs it), timed on the host cores: one
+    warm-up call, then calls until about ``budget_s`` seconds have passed (at least 3)."""
+
+    from oracle import batch
     from oracle import sampler as oracle
 
-    threads = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     torch.set_num_threads(threads)
     state = oracle.State.from_buffers(workload.buffers)
-    logits = workload.logits[:rows]
 
     def run():
 
-        oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=5)
+        batch.singular(workload.logits, state, max_top_logprobs=5)
 
     run()
     times = []
+    t_end = time.perf_counter() + budget_s
 
-    for _ in range(5):
+    while len(times) < 3 or time.perf_counter() < t_end:
 
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
 
-    per_row = statistics.median(times) / rows
+    rows = workload.logits.size(0)
 
     return {
-        "value": round(per_row * workload.logits.size(0) * 1e6, 1),
+        "value": round(statistics.median(times) * 1e6, 1),
         "unit": "us/step",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{rows} of {workload.logits.size(0)} rows of config 1, median of 5 runs after "
-                  f"1 warm-up, scaled to the full batch; CPU: {platform.processor() or platform.machine()}",
+        "sample": f"oracle/batch.py singular over all {rows} rows of config 1 (one batched call, "
+                  f"stable sort for the top-128), median of {len(times)} calls after 1 warm-up; "
+                  f"CPU: {cpu_model()}",
     }
+
+
+MALL_BYTES = 256 << 20
+
+
+def rotation_sets(bytes_per_set: int) -> int:
+    """Input sets to rotate so that together they exceed the 256 MB MALL by a quarter: a set's
+    data is then evicted before it comes round again, and steps read HBM, not the cache."""
+
+    return max(3, -(-int(1.25 * MALL_BYTES) // max(1, bytes_per_set)))
 
 
 def _queue_behind_sleep(ms: float = 60.0) -> None:
@@ -390,8 +427,8 @@ def _queue_behind_sleep(ms: float = 60.0) -> None:
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
-def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox: bool = True,
-              block_n: Optional[int] = None) -> dict:
+def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline: bool = True,
+              philox: bool = True, block_n: Optional[int] = None) -> dict:
 
     from sonic_sampler import _native
     from sonic_sampler.interface import UnshardedFusedSingular
@@ -399,6 +436,7 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     device = torch.device("cuda:0")
     base = c1_workload()
     batch, vocab = base.logits.shape
+    sets = sets or rotation_sets(c1_tile_bytes(batch, vocab))
 
     sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch,
                                                 max_top_logprobs=5, block_size=block_n, device=device)
@@ -430,7 +468,6 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(steps)]
     _queue_behind_sleep(max(60.0, steps * 0.3))
-    wall0 = time.perf_counter()
 
     for i in range(steps):
 
@@ -439,9 +476,21 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
         events[i][1].record(stream)
 
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
     launch_us = [a.elapsed_time(b) * 1e3 for a, b in events]
     kernel_us = statistics.mean(launch_us)
+
+    # Host cost of one eager call (argument resolution + two launches), with the GPU idle at the
+    # start so that nothing but the enqueue is timed.
+    enqueue = []
+
+    for i in range(min(steps, 50)):
+
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step(i)
+        enqueue.append(time.perf_counter() - t0)
+
+    torch.cuda.synchronize()
 
     # The tile kernel alone, from events its own dispatch records at its start and end (a second
     # pass: recording them adds a little to each step, so the step time above runs without them).
@@ -504,7 +553,7 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(wall * 1e3 / steps, 4),
+        "ms_per_step": round(kernel_us * 1e-3, 5),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -517,13 +566,15 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
             "rows": batch,
             "vocab": vocab,
             "input_sets_rotated": sets,
+            "rotated_bytes": sets * c1_tile_bytes(batch, vocab),
             "algorithmic_bytes_per_step": algorithmic,
             "step_hbm_gbs": round(algorithmic / (kernel_us * 1e-6) / 1e9, 1),
+            "step_hbm_frac": round(algorithmic / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "rows_per_s": round(batch / (kernel_us * 1e-6), 1),
             "median_step_us": round(statistics.median(launch_us), 3),
             "tile_kernel_us": round(tile_kernel_us, 3),
             "graph_replay_us_per_step": round(graph_us, 3),
-            "host_us_per_eager_call": round(wall * 1e6 / steps, 1),
+            "host_us_per_eager_call": round(statistics.median(enqueue) * 1e6, 1),
         },
         "roofline": {
             "kernel": TILE_KERNEL,
@@ -537,10 +588,10 @@ def run_bench(steps: int, warmup: int, sets: int = 3, cpu_rows: int = 64, philox
         },
     }
 
-    if cpu_rows > 0:
+    if cpu_baseline:
 
         sys.path.insert(0, str(ROOT))
-        result["cpu_baseline"] = cpu_baseline_c1(base, min(cpu_rows, batch))
+        result["cpu_baseline"] = cpu_baseline_c1(base)
 
     return result
 
@@ -609,12 +660,51 @@ CONFIG_NAMES = {
 }
 
 
-def run_config(config: int, steps: int, warmup: int, sets: int = 3, block_n: Optional[int] = None) -> dict:
-    """Timing of one of the other configurations (their parity is covered by the GPU tests)."""
+def c4_rotation(base: SingularWorkload, sets: int, device) -> list:
+    """Device inputs of `sets` config-4 steps that share the large gathered planes (noise, counts,
+    bias: 128 gathers per row) but stream distinct memory: every set has its own logits, its own
+    copy of the grammar plane (with the bits of its own spike tokens set) and its own slot map."""
+
+    import dataclasses
+
+    buffers = to_device(base.buffers, device)
+    d2t = base.d2t.to(device)
+    rows, words = base.logits.size(0), base.target_vocab // 32
+    staged = []
+
+    for i in range(sets):
+
+        g = torch.Generator("cpu").manual_seed(5000 + i)
+        logits = base.logits if i == 0 else spiked_logits(rows, base.vocab, seed=1004 + 100 * i)
+        slots = base.slot_mapping if i == 0 else torch.randperm(buffers.layout.rows, generator=g)[:rows].to(I32)
+        grammar = buffers.grammar.clone()
+
+        if i:
+
+            spike = base.d2t[logits.float().argmax(dim=-1)].to(I64)
+            word = grammar.view(I32)[slots.to(I64).to(device), base.timestep, (spike // 32).to(device)]
+            bit = torch.ones_like(spike).bitwise_left_shift(spike % 32)
+            bit = (bit - ((bit >> 31) << 32)).to(I32).to(device)
+            grammar.view(I32)[slots.to(I64).to(device), base.timestep, (spike // 32).to(device)] = word | bit
+
+        probs = torch.zeros(buffers.layout.rows, base.target_vocab, dtype=BF16, device=device)
+        staged.append((logits.to(device), dataclasses.replace(buffers, grammar=grammar),
+                       base.tokens.to(device), probs, slots.to(device), d2t))
+
+    return staged
+
+
+def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
+               block_n: Optional[int] = None) -> dict:
+    """Timing of one of the other configurations (their parity is covered by the GPU tests).
+    Input sets rotate so that together they exceed the 256 MB MALL (rotation_sets)."""
 
     from sonic_sampler.interface import UnshardedBoundedTopK, UnshardedFusedMultistep, UnshardedFusedSingular
 
     device = torch.device("cuda:0")
+    per_set = {0: 8 * 32000 * 4, 2: 128 * 5 * 151936 * 2, 3: 300 * 128256 * 2,
+               4: 256 * 32000 * 2 + 256 * 8192 * 4}
+    sets = sets or rotation_sets(per_set[config])
 
     if config == 0:
 
@@ -663,18 +753,11 @@ def run_config(config: int, steps: int, warmup: int, sets: int = 3, block_n: Opt
 
     elif config == 4:
 
-        works = [c4_workload(seed=1004 + 100 * i) for i in range(sets)]
-        w0 = works[0]
+        w0 = c4_workload()
         rows = w0.logits.size(0)
         sampler = UnshardedFusedSingular.initialize(vocab_size=w0.vocab, batch_size=rows, lookahead=4,
                                                     max_top_logprobs=5, block_size=block_n, device=device)
-        staged = []
-
-        for w in works:
-
-            probs = torch.zeros(w.buffers.layout.rows, w.target_vocab, dtype=BF16, device=device)
-            staged.append((w.logits.to(device), to_device(w.buffers, device), w.tokens.to(device), probs,
-                           w.slot_mapping.to(device), w.d2t.to(device)))
+        staged = c4_rotation(w0, sets, device)
 
         def step(i):
 
@@ -701,14 +784,19 @@ def run_config(config: int, steps: int, warmup: int, sets: int = 3, block_n: Opt
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "ms_per_step": round(us * 1e-3, 5),
         "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
         "dtype": "fp32" if config == 0 else "bf16",
         "data": "synthetic (spiked N(0,3^2) logits, configuration generators of bench.py)",
         "config": {
             "workload": CONFIG_NAMES[config],
             "rows": rows,
+            "input_sets_rotated": sets,
             "algorithmic_bytes_per_step": algorithmic,
             "achieved_hbm_gbs": round(algorithmic / (us * 1e-6) / 1e9, 1),
+            "step_hbm_frac": round(algorithmic / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "rows_per_s": round(rows / (us * 1e-6), 1),
             "median_step_us": round(t["median_eager_us"], 3),
             "graph_replay_us_per_step": round(t["graph_us"], 3),
@@ -738,8 +826,10 @@ def main(argv=None) -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--cpu-rows", type=int, default=64,
-                        help="rows of config 1 timed for the CPU baseline (0 to skip)")
+    parser.add_argument("--no-cpu-baseline", action="store_true",
+                        help="skip the CPU baseline of config 1")
+    parser.add_argument("--sets", type=int, default=None,
+                        help="input sets to rotate (default: enough to exceed the 256 MB MALL)")
     parser.add_argument("--buffer-noise", action="store_true",
                         help="read Gumbel noise from the buffers instead of the Philox stream")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -765,12 +855,13 @@ def main(argv=None) -> int:
 
     if args.config != 1:
 
-        print(json.dumps(run_config(args.config, args.steps, args.warmup, block_n=args.block_n)), flush=True)
+        print(json.dumps(run_config(args.config, args.steps, args.warmup, sets=args.sets, block_n=args.block_n)),
+              flush=True)
 
         return 0
 
-    result = run_bench(args.steps, args.warmup, cpu_rows=args.cpu_rows, philox=not args.buffer_noise,
-                       block_n=args.block_n)
+    result = run_bench(args.steps, args.warmup, sets=args.sets, cpu_baseline=not args.no_cpu_baseline,
+                       philox=not args.buffer_noise, block_n=args.block_n)
     print(json.dumps(result), flush=True)
 
     return 0

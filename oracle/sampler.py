@@ -510,16 +510,24 @@ def apply_multistep_counts(decode: Tensor, results: List[RequestResult],
 # Output tolerance
 # ------------------------------------------------------------------------------------------------
 
-def bf16_within(actual: float, expected_fp32: float, rel: float = REL) -> bool:
-    """True when the bf16 output equals the bf16 rounding of some value within `rel` (relative)
-    of the fp32 reference value; -inf must match exactly."""
+def bf16_within(actual: float, expected_fp32: float, rel: float = REL, floor: float = 0.0) -> bool:
+    """True when the bf16 output equals the bf16 rounding of some value within `rel` (relative) of
+    the fp32 reference value, or within the absolute `floor`; -inf must match exactly.
+
+    Log-probabilities pass ``floor=LOGPROB_FLOOR``: an fp32 log-softmax ``(v - m) - log(s)`` with
+    ``s = sum(exp(v - m))`` carries an absolute error of a few ulp of ``s`` (near 1) whatever the
+    result's size, so close to 0 no fp32 evaluation -- the reference's included -- is relatively
+    accurate to 1e-5 (e.g. log(1.0017) = 0.0017 with one ulp of s worth 7e-5 of it)."""
 
     if expected_fp32 == float("-inf") or actual == float("-inf"):
 
         return actual == expected_fp32
 
-    lo = expected_fp32 - abs(expected_fp32) * rel - 1e-30
-    hi = expected_fp32 + abs(expected_fp32) * rel + 1e-30
+    band = max(abs(expected_fp32) * rel, floor) + 1e-30
     r = lambda v: float(torch.tensor(v, dtype=F32).to(BF16))  # noqa: E731
 
-    return r(lo) <= actual <= r(hi)
+    return r(expected_fp32 - band) <= actual <= r(expected_fp32 + band)
+
+
+# Absolute tolerance of fp32 log-probabilities: 4 ulp of 1.0 (see bf16_within).
+LOGPROB_FLOOR = 2.0 ** -21

@@ -686,15 +686,16 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &
     const int lane = lane_id();
     uint32_t *run = sm.run[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
     const uint32_t cb = 0xffffu - 4u * threadIdx.x;  // 0xffff - column of the lane's element 0
-    // Wave-uniform count, saturated at SS_K + 1: positions stay below SS_K + 64, inside the run,
-    // and a count above SS_K still reads as an overflow.
+    // Wave-uniform count, saturated at SS_K + 1 so that a count above SS_K still reads as an
+    // overflow. Writes happen only while cnt <= SS_K: positions then stay below SS_K + 64, inside
+    // the run (an overflowed run is rewritten by the exact pass).
     uint32_t cnt = 0;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const bool p = EXACT ? keys.gt(j, T) | (((tie_keep >> j) & 1u) != 0u) : keys.gt(j, T);
         const uint64_t m = __ballot(p);
         uint32_t *at = run + cnt;  // uniform
-        if (p) at[mbcnt64(m)] = keys.composite(j, cb);
+        if (p && cnt <= (uint32_t)SS_K) at[mbcnt64(m)] = keys.composite(j, cb);
         cnt = min(cnt + (uint32_t)__popcll(m), (uint32_t)SS_K + 1u);
     }
     if (cnt <= 64) {

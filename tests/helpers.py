@@ -4,7 +4,7 @@ from __future__ import annotations
 
 import torch
 
-from oracle.sampler import bf16_within
+from oracle.sampler import LOGPROB_FLOOR, bf16_within
 
 
 def assert_tokens(actual, expected, what: str, allow_fraction: float = 0.05):
@@ -45,14 +45,14 @@ def check_singular(selection, expected, *, logprobs: bool, probabilities=None, s
 
         if lp is not None:
 
-            assert bf16_within(float(lp[r, 0]), e.logprob), (r, float(lp[r, 0]), e.logprob)
+            assert bf16_within(float(lp[r, 0]), e.logprob, floor=LOGPROB_FLOOR), (r, float(lp[r, 0]), e.logprob)
 
         if top is not None:
 
             for z, (t, v) in enumerate(zip(e.top_tokens, e.top_logprobs)):
 
                 assert int(top_tokens[r, z]) == t, (r, z, int(top_tokens[r, z]), t)
-                assert bf16_within(float(top_values[r, z]), v), (r, z, float(top_values[r, z]), v)
+                assert bf16_within(float(top_values[r, z]), v, floor=LOGPROB_FLOOR), (r, z, float(top_values[r, z]), v)
 
         if probs is not None and e.probs is not None:
 
@@ -108,7 +108,7 @@ def check_multistep(verification, expected, cu_seqlens, *, logprobs: bool,
 
         for i, v in enumerate(e.logprobs):
 
-            assert bf16_within(float(lp[margin + i]), v), (b, i, float(lp[margin + i]), v)
+            assert bf16_within(float(lp[margin + i]), v, floor=LOGPROB_FLOOR), (b, i, float(lp[margin + i]), v)
 
         if top is not None:
 
@@ -117,6 +117,41 @@ def check_multistep(verification, expected, cu_seqlens, *, logprobs: bool,
                 for z, (t, v) in enumerate(zip(tt, tv)):
 
                     assert int(top_tokens[margin + i, z]) == t, (b, i, z)
-                    assert bf16_within(float(top_values[margin + i, z]), v), (b, i, z, float(top_values[margin + i, z]), v)
+                    assert bf16_within(float(top_values[margin + i, z]), v, floor=LOGPROB_FLOOR), (b, i, z, float(top_values[margin + i, z]), v)
 
     return mismatched
+
+
+def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, block_size=None,
+                 slot_mapping=None, buffers=None):
+
+    from bench import to_device
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    batch = len(work.cu_seqlens) - 1
+    buffers = buffers if buffers is not None else to_device(work.buffers, "cuda:0")
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=work.vocab, lookahead=work.lookahead,
+                                                  batch_size=batch, block_size=block_size,
+                                                  max_top_logprobs=work.max_top_logprobs, device="cuda:0")
+    drafted = work.drafted.to("cuda:0")
+
+    if work.varlen:
+
+        logits = work.logits.to("cuda:0")
+        tokens = drafted
+        cu = torch.tensor(work.cu_seqlens, dtype=torch.int32, device="cuda:0")
+
+    else:
+
+        n = work.lookahead + 1
+        logits = work.logits.view(batch, n, -1).to("cuda:0")
+        tokens = drafted.view(batch, n)
+        cu = None
+
+    probs = work.probabilities.to("cuda:0") if work.probabilities is not None else None
+    verification = verifier(logits, tokens, buffers, probabilities=probs, update_counts=update_counts,
+                            logprobs=logprobs, in_place=in_place, cu_seqlens=cu,
+                            slot_mapping=slot_mapping)
+    torch.cuda.synchronize()
+
+    return verification, buffers, verifier

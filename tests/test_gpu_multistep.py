@@ -3,47 +3,12 @@
 import pytest
 import torch
 
-from helpers import check_multistep
+from helpers import check_multistep, run_verifier
 from oracle import sampler as oracle
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
-
-
-def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, block_size=None,
-                 slot_mapping=None, buffers=None):
-
-    from bench import to_device
-    from sonic_sampler.interface import UnshardedFusedMultistep
-
-    batch = len(work.cu_seqlens) - 1
-    buffers = buffers if buffers is not None else to_device(work.buffers, DEV)
-    verifier = UnshardedFusedMultistep.initialize(vocab_size=work.vocab, lookahead=work.lookahead,
-                                                  batch_size=batch, block_size=block_size,
-                                                  max_top_logprobs=work.max_top_logprobs, device=DEV)
-    drafted = work.drafted.to(DEV)
-
-    if work.varlen:
-
-        logits = work.logits.to(DEV)
-        tokens = drafted
-        cu = torch.tensor(work.cu_seqlens, dtype=torch.int32, device=DEV)
-
-    else:
-
-        n = work.lookahead + 1
-        logits = work.logits.view(batch, n, -1).to(DEV)
-        tokens = drafted.view(batch, n)
-        cu = None
-
-    probs = work.probabilities.to(DEV) if work.probabilities is not None else None
-    verification = verifier(logits, tokens, buffers, probabilities=probs, update_counts=update_counts,
-                            logprobs=logprobs, in_place=in_place, cu_seqlens=cu,
-                            slot_mapping=slot_mapping)
-    torch.cuda.synchronize()
-
-    return verification, buffers, verifier
 
 
 def test_config2_greedy():

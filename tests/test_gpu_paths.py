@@ -1,0 +1,466 @@
+"""GPU parity on the kernel paths the configuration tests do not reach.
+
+* per-element (scalar) loads: vocabularies that are not multiples of 4, logits whose rows start 2
+  bytes off an 8-byte boundary or whose row stride is not a multiple of 4, and d2t gathers over a
+  draft vocabulary that is not a multiple of 4;
+* the 8192-column tile, whose processor chain runs in two 4096-column halves, on rows with every
+  processor on and a partial last tile ending in either half;
+* outputs under hipGraph replay: one captured single-step call and one captured verification,
+  replayed over three input sets copied into the captured tensors (logits, slot mapping,
+  indicators, parameters, counts, noise), each replay checked against an eager call on the same
+  inputs and against the oracle (the reference's contract that results hold across capture,
+  docs/slot-based.md:351-378).
+"""
+
+import dataclasses
+
+import pytest
+import torch
+
+from helpers import check_multistep, check_singular, run_verifier
+from oracle import sampler as oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+# grammar, repetition / frequency / presence penalties, bias, temperature, top-k, top-p, min-p
+EVERY_PROCESSOR = 0x3BF
+
+
+def random_host(slots, timesteps, vocab, seed, indicator=None, max_top_logprobs=5):
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Indicator
+
+    return SamplingBuffers.random(size=slots, timesteps=timesteps, vocab_size=vocab, device="cpu",
+                                  seed=seed, max_top_logprobs=max_top_logprobs,
+                                  indicators=None if indicator is None else Indicator(indicator))
+
+
+def autoregressive_case(logits, host, block, *, prefill=False, slot_mapping=None):
+    """One autoregressive call with logprobs and count updates, checked against the oracle."""
+
+    from bench import to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    rows, vocab = logits.shape
+    buffers = to_device(host, DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=5,
+                                                block_size=block, device=DEV)
+    dev_slots = None if slot_mapping is None else slot_mapping.to(DEV)
+    selection = sampler.autoregressive(logits, buffers, prefill=prefill, update_counts=True, logprobs=True,
+                                       slot_mapping=dev_slots)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    slots = None if slot_mapping is None else slot_mapping.tolist()
+    expected = oracle.singular(logits.cpu().contiguous(), state, scope="target", slot_mapping=slots,
+                               logprobs=True, max_top_logprobs=5)
+    mismatched, checked = check_singular(selection, expected, logprobs=True)
+
+    if not mismatched:
+
+        counts = oracle.apply_singular_counts(state.decode, expected, slots, prefill=prefill)
+        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+    return checked
+
+
+# ------------------------------------------------------------------------------------------------
+# Per-element loads
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("indicator,seed", [(EVERY_PROCESSOR, 31), (None, 32)])
+def test_scalar_path_vocabulary_not_a_multiple_of_4(indicator, seed):
+
+    from bench import spiked_logits
+
+    rows, vocab = 16, 50257
+    print(f"scalar path: V={vocab} indicator={indicator} seed={seed}", flush=True)
+    host = random_host(rows, 1, vocab, seed, indicator)
+    logits = spiked_logits(rows, vocab, seed=500 + seed).to(DEV)
+    assert autoregressive_case(logits, host, 2048) >= rows - 2
+
+
+@pytest.mark.parametrize("layout", ["offset_2_bytes", "stride_not_multiple_of_4"])
+def test_scalar_path_unaligned_logit_rows(layout):
+
+    from bench import spiked_logits
+
+    rows, vocab = 8, 16384
+    print(f"scalar path: logits {layout}", flush=True)
+    host = random_host(rows, 1, vocab, 33, EVERY_PROCESSOR)
+    wide = spiked_logits(rows, vocab + 2, seed=533).to(DEV)
+    # a view 2 bytes into every row (stride V + 2), or rows of stride V + 2 starting aligned
+    logits = wide[:, 1:vocab + 1] if layout == "offset_2_bytes" else wide[:, :vocab]
+    assert logits.stride(0) % 4 != 0 or logits.data_ptr() % 8 != 0
+    assert autoregressive_case(logits, host, 2048) >= rows - 1
+
+
+@pytest.mark.parametrize("seed", [40, 41])
+def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    slots, rows, gamma, t = 12, 8, 3, 2
+    draft_vocab, target_vocab = 4099, 8192
+    g = torch.Generator().manual_seed(seed)
+    host = random_host(slots, gamma + 1, target_vocab, seed)
+    buffers = to_device(host, DEV)
+    logits = spiked_logits(rows, draft_vocab, seed=600 + seed)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(torch.int32)
+    d2t = torch.randperm(target_vocab, generator=g)[:draft_vocab].to(torch.int32)
+    tokens = torch.randint(1, target_vocab, (rows, gamma + 1), generator=g).to(torch.int32)
+    print(f"d2t scalar path seed={seed} indicators={[hex(int(v)) for v in host.flags.indicators.draft]}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=draft_vocab, batch_size=rows, lookahead=gamma,
+                                                block_size=1024, max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, target_vocab, dtype=torch.bfloat16, device=DEV)
+    selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=tokens.to(DEV),
+                                 probabilities=probs, slot_mapping=slot_mapping.to(DEV),
+                                 d2t_mapping=d2t.to(DEV), target_vocab=target_vocab, in_place=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    stochastic = not host.flags.all_greedy
+    expected = oracle.singular(logits, state, scope="draft", timestep=t, slot_mapping=slot_mapping.tolist(),
+                               d2t=d2t, drafted=tokens, history=t, probs=stochastic, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False, probabilities=probs if stochastic else None,
+                   slot_mapping=slot_mapping)
+
+
+@pytest.mark.parametrize("seed", [50, 51])
+def test_scalar_path_multistep(seed):
+
+    from bench import MultistepWorkload, spiked_logits
+
+    slots, batch, gamma, vocab = 10, 6, 3, 50257
+    n = gamma + 1
+    g = torch.Generator().manual_seed(seed)
+    host = random_host(slots, n, vocab, 70 + seed, max_top_logprobs=4)
+    logits = spiked_logits(batch * n, vocab, seed=700 + seed)
+    slot_mapping = torch.randperm(slots, generator=g)[:batch].to(torch.int32)
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch * n, generator=g) < 0.6, argmax,
+                          torch.randint(1, vocab, (batch * n,), generator=g)).to(torch.int32)
+    probabilities = torch.softmax(torch.randn(slots, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print(f"multistep scalar path seed={seed}", flush=True)
+    verification, buffers, _ = run_verifier(work, update_counts=True, block_size=2048,
+                                            slot_mapping=slot_mapping.to(DEV))
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, slot_mapping=slot_mapping.tolist(),
+                                probabilities=probabilities, logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
+
+    if not mismatched:
+
+        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
+        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+# ------------------------------------------------------------------------------------------------
+# 8192-column tiles with every processor on (the chain in two halves)
+# ------------------------------------------------------------------------------------------------
+
+# the last tile holds 2048 columns (ends inside the first half) or 6144 (inside the second)
+SPLIT_VOCABS = [3 * 8192 + 2048, 3 * 8192 + 6144]
+
+
+@pytest.mark.parametrize("vocab", SPLIT_VOCABS)
+def test_8192_tiles_autoregressive_every_processor(vocab):
+
+    from bench import spiked_logits
+
+    rows = 12
+    print(f"8192 tiles, autoregressive: V={vocab}", flush=True)
+    host = random_host(rows, 1, vocab, vocab % 97, EVERY_PROCESSOR)
+    logits = spiked_logits(rows, vocab, seed=vocab).to(DEV)
+    assert autoregressive_case(logits, host, 8192) >= rows - 1
+
+
+@pytest.mark.parametrize("vocab", SPLIT_VOCABS)
+def test_8192_tiles_drafting_history(vocab):
+    """Drafting without d2t: the first t drafted columns extend the decode history."""
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    slots, rows, gamma, t = 10, 8, 4, 3
+    g = torch.Generator().manual_seed(vocab)
+    host = random_host(slots, gamma + 1, vocab, vocab % 89, EVERY_PROCESSOR)
+    buffers = to_device(host, DEV)
+    logits = spiked_logits(rows, vocab, seed=vocab + 1)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(torch.int32)
+    # half the history hits the row's own spikes, so the penalties change the top of the row
+    spikes = logits.float().argsort(-1, descending=True)[:, :gamma + 1].to(torch.int32)
+    tokens = torch.where(torch.rand(rows, gamma + 1, generator=g) < 0.5, spikes,
+                         torch.randint(0, vocab, (rows, gamma + 1), generator=g).to(torch.int32))
+    print(f"8192 tiles, drafting with history: V={vocab}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, lookahead=gamma,
+                                                block_size=8192, max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, vocab, dtype=torch.bfloat16, device=DEV)
+    selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=tokens.to(DEV),
+                                 probabilities=probs, slot_mapping=slot_mapping.to(DEV))
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="draft", timestep=t, slot_mapping=slot_mapping.tolist(),
+                               drafted=tokens, history=t, probs=True, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=slot_mapping)
+
+
+@pytest.mark.parametrize("vocab", SPLIT_VOCABS)
+def test_8192_tiles_multistep_every_processor(vocab):
+
+    from bench import MultistepWorkload, spiked_logits
+
+    slots, batch, gamma = 8, 4, 3
+    n = gamma + 1
+    g = torch.Generator().manual_seed(vocab + 2)
+    host = random_host(slots, n, vocab, vocab % 83, EVERY_PROCESSOR, max_top_logprobs=4)
+    logits = spiked_logits(batch * n, vocab, seed=vocab + 3)
+    slot_mapping = torch.randperm(slots, generator=g)[:batch].to(torch.int32)
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch * n, generator=g) < 0.6, argmax,
+                          torch.randint(1, vocab, (batch * n,), generator=g)).to(torch.int32)
+    probabilities = torch.softmax(torch.randn(slots, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print(f"8192 tiles, multistep: V={vocab}", flush=True)
+    verification, buffers, _ = run_verifier(work, update_counts=True, block_size=8192,
+                                            slot_mapping=slot_mapping.to(DEV))
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, slot_mapping=slot_mapping.tolist(),
+                                probabilities=probabilities, logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.25)
+
+    if not mismatched:
+
+        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
+        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+# ------------------------------------------------------------------------------------------------
+# hipGraph replay
+# ------------------------------------------------------------------------------------------------
+
+def load_into(dst, src):
+    """Copies every device tensor of a (device) SamplingBuffers from a CPU one of the same layout,
+    in place, so that a captured graph sees the new contents at the same addresses."""
+
+    from sonic_sampler.core.flags import Flags
+
+    if isinstance(dst, Flags):
+
+        dst.packed.copy_(src.packed)
+
+    elif dataclasses.is_dataclass(dst):
+
+        for f in dataclasses.fields(dst):
+
+            load_into(getattr(dst, f.name), getattr(src, f.name))
+
+    elif isinstance(dst, torch.Tensor) and dst.device.type == "cuda":
+
+        dst.copy_(src)
+
+
+def singular_outputs(selection):
+
+    lp = selection.logprobs
+    return [t.clone() for t in (selection.tokens, lp.selected, lp.top_k.tokens, lp.top_k.logprobs)]
+
+
+def test_graph_replay_autoregressive_config1():
+
+    from bench import c1_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    sets = []
+
+    for k in range(3):
+
+        work = c1_workload(seed=1001 + 10 * k)
+        slots = torch.randperm(64, generator=torch.Generator().manual_seed(k)).to(torch.int32)
+        sets.append((work, slots))
+
+    batch, vocab = sets[0][0].logits.shape
+    buffers = to_device(sets[0][0].buffers, DEV)
+    logits = sets[0][0].logits.to(DEV)
+    slot_mapping = sets[0][1].to(DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch, max_top_logprobs=5, device=DEV)
+
+    def load(k):
+
+        work, slots = sets[k]
+        load_into(buffers, work.buffers)
+        logits.copy_(work.logits)
+        slot_mapping.copy_(slots)
+
+    def call():
+
+        return sampler.autoregressive(logits, buffers, update_counts=True, logprobs=True,
+                                      slot_mapping=slot_mapping)
+
+    eager = []
+
+    for k in range(3):
+
+        load(k)
+        eager.append(singular_outputs(call()) + [buffers.repetition.counts.decode.clone()])
+
+    torch.cuda.synchronize()
+    print("config 1 eager outputs for 3 input sets; capturing", flush=True)
+
+    load(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        call()                                   # warm-up on the capture stream's side
+
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(graph):
+
+        captured = call()
+
+    for rnd, k in enumerate([1, 0, 2, 1, 2, 0]):
+
+        load(k)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = singular_outputs(captured) + [buffers.repetition.counts.decode.clone()]
+        print(f"replay {rnd}: input set {k}", flush=True)
+
+        for a, b in zip(got, eager[k]):
+
+            assert torch.equal(a, b), f"replay {rnd} of input set {k} differs from the eager call"
+
+        if rnd < 3:
+
+            work, slots = sets[k]
+            state = oracle.State.from_buffers(work.buffers)
+            expected = oracle.singular(work.logits, state, scope="target", slot_mapping=slots.tolist(),
+                                       logprobs=True, max_top_logprobs=5)
+            mismatched, _ = check_singular(captured, expected, logprobs=True)
+
+            if not mismatched:
+
+                counts = oracle.apply_singular_counts(state.decode, expected, slots.tolist(), prefill=False)
+                assert torch.equal(got[-1].cpu(), counts)
+
+
+def test_graph_replay_verifier_config3():
+
+    from bench import c3_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    base = c3_workload()
+    lengths = [base.cu_seqlens[b + 1] - base.cu_seqlens[b] for b in range(len(base.cu_seqlens) - 1)]
+    sets = [(base, torch.arange(64, dtype=torch.int32))]
+
+    for k in (1, 2):
+
+        work = c3_workload(seed=1003 + 10 * k, lengths=lengths)
+        sets.append((work, torch.randperm(64, generator=torch.Generator().manual_seed(k)).to(torch.int32)))
+
+    batch = len(lengths)
+    buffers = to_device(base.buffers, DEV)
+    logits = base.logits.to(DEV)
+    drafted = base.drafted.to(DEV)
+    probs = base.probabilities.to(DEV)
+    slot_mapping = sets[0][1].to(DEV)
+    cu = torch.tensor(base.cu_seqlens, dtype=torch.int32, device=DEV)
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=base.vocab, lookahead=base.lookahead,
+                                                  batch_size=batch, max_top_logprobs=20, device=DEV)
+
+    def load(k):
+
+        work, slots = sets[k]
+        load_into(buffers, work.buffers)
+        logits.copy_(work.logits)
+        drafted.copy_(work.drafted)
+        # request b reads the draft distribution of its slot
+        probs.copy_(work.probabilities[torch.argsort(slots.long())])
+        slot_mapping.copy_(slots)
+
+    def call():
+
+        return verifier(logits, drafted, buffers, probabilities=probs, update_counts=True, logprobs=True,
+                        cu_seqlens=cu, slot_mapping=slot_mapping)
+
+    starts = torch.tensor(base.cu_seqlens[:-1], dtype=torch.int64)
+    request = torch.repeat_interleave(torch.arange(batch), torch.tensor(lengths))
+    position = torch.arange(base.cu_seqlens[-1]) - starts[request]
+
+    def outputs(v):
+        """What the call defines: offsets, and tokens / logprobs / top logprobs of the emitted
+        positions (rows past a request's offset are not written, as in the reference)."""
+
+        offsets = v.offsets.reshape(-1).cpu()
+        emitted = (position <= offsets[request]).to(DEV)
+        top = v.logprobs.top_k
+        return [v.offsets.clone(), v.tokens.reshape(-1)[emitted], v.logprobs.selected.reshape(-1)[emitted],
+                top.tokens.reshape(-1, 20)[emitted], top.logprobs.reshape(-1, 20)[emitted],
+                buffers.repetition.counts.decode.clone()]
+
+    eager = []
+
+    for k in range(3):
+
+        load(k)
+        eager.append(outputs(call()))
+
+    torch.cuda.synchronize()
+    print("config 3 eager outputs for 3 input sets; capturing", flush=True)
+
+    load(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        call()
+
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(graph):
+
+        captured = call()
+
+    for rnd, k in enumerate([2, 0, 1, 2, 1, 0]):
+
+        load(k)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = outputs(captured)
+        print(f"replay {rnd}: input set {k}", flush=True)
+
+        for a, b in zip(got, eager[k]):
+
+            assert torch.equal(a, b), f"replay {rnd} of input set {k} differs from the eager call"
+
+        if rnd < 3:
+
+            work, slots = sets[k]
+            state = oracle.State.from_buffers(work.buffers)
+            q = work.probabilities[torch.argsort(slots.long())]
+            expected = oracle.multistep(work.logits, state, work.drafted, work.cu_seqlens,
+                                        slot_mapping=slots.tolist(), probabilities=q, logprobs=True,
+                                        max_top_logprobs=20)
+            check_multistep(captured, expected, work.cu_seqlens, logprobs=True)

@@ -388,3 +388,217 @@ def test_per_row_oracle_matches_batch_naive(indicator):
     for r, rec in enumerate(res):
 
         assert float(torch.tensor(rec.logprob).to(BF16)) == float(expected.logprobs.selected[r, 0])
+
+
+# ------------------------------------------------------------------------------------------------
+# Decode-count updates, top-Z limits and the multistep history, by hand
+# (reference ops/singular.py:134-151, ops/verify.py:75-91,425-429, ops/singular.py:335-346,
+# core/naive.py:179-203)
+# ------------------------------------------------------------------------------------------------
+
+def slots_state(slots, vocab, indicator, timesteps=4):
+    """A state of `slots` requests sharing one indicator word, every processor neutral."""
+
+    def bf(v):
+
+        return torch.full((slots,), v, dtype=torch.float32).to(BF16)
+
+    return oracle.State(
+        target=[indicator] * slots, draft=[indicator] * slots,
+        grammar=torch.full((slots, timesteps, (vocab + 31) // 32), -1, dtype=I32),
+        context=torch.zeros(slots, vocab, dtype=I32), decode=torch.zeros(slots, vocab, dtype=I32),
+        bias=torch.zeros(slots, vocab, dtype=BF16),
+        multiplicative=bf(1.0), frequency=bf(0.0), presence=bf(0.0), temperature=bf(1.0),
+        top_p=bf(1.0), min_p=bf(0.0), top_k=torch.full((slots,), 128, dtype=I32),
+        top_logprobs=torch.zeros(slots, dtype=I32),
+        gumbel_target=torch.zeros(slots, timesteps, vocab, dtype=BF16),
+        gumbel_draft=torch.zeros(slots, timesteps, vocab, dtype=BF16),
+        uniform=torch.ones(slots, timesteps, dtype=BF16),
+    )
+
+
+def peaked(vocab, peaks):
+    """bf16 rows of -4 with a unique maximum 8 at column peaks[r]."""
+
+    x = torch.full((len(peaks), vocab), -4.0)
+
+    for r, c in enumerate(peaks):
+
+        x[r, c] = 8.0
+
+    return x.to(BF16)
+
+
+def test_singular_count_update_adds_one_at_the_slot():
+
+    st = slots_state(4, 64, oracle.GREEDY)
+    st.decode[2, 7] = 5
+    st.decode[0, 7] = 9      # the same token in another slot must not move
+    res = oracle.singular(peaked(64, [7, 11]), st, slot_mapping=[2, 3])
+    assert [r.token for r in res] == [7, 11]
+    after = oracle.apply_singular_counts(st.decode, res, [2, 3], prefill=False)
+    assert int(after[2, 7]) == 6 and int(after[3, 11]) == 1 and int(after[0, 7]) == 9
+    assert int((after != st.decode).sum()) == 2
+
+
+def test_singular_prefill_stores_one():
+    """Prefill writes 1 whatever the count held (reference ops/singular.py:143-145)."""
+
+    st = slots_state(2, 64, oracle.GREEDY)
+    st.decode[1, 7] = 5
+    res = oracle.singular(peaked(64, [30, 7]), st)
+    after = oracle.apply_singular_counts(st.decode, res, None, prefill=True)
+    assert int(after[1, 7]) == 1 and int(after[0, 30]) == 1
+    assert int((after != st.decode).sum()) == 2
+
+
+def test_drafted_count_update_lands_at_the_target_id():
+    """With d2t the update is at the remapped (target-vocabulary) id, in the row's slot."""
+
+    st = slots_state(2, 64, oracle.GREEDY)
+    d2t = torch.tensor([40, 3, 5, 7], dtype=torch.int64)
+    res = oracle.singular(peaked(4, [0]), st, scope="draft", slot_mapping=[1], d2t=d2t)
+    assert res[0].token == 40
+    after = oracle.apply_singular_counts(st.decode, res, [1], prefill=False)
+    assert int(after[1, 40]) == 1 and int(after[1, 0]) == 0 and int(after.sum()) == 1
+
+
+def test_multistep_counts_add_one_per_emitted_token_including_the_bonus():
+
+    vocab = 64
+    st = slots_state(3, vocab, oracle.GREEDY)
+    # request 0 (slot 2): argmax 9, 9, 12, 30 and drafts 9, 9, 5: two accepted, then 12
+    # request 1 (slot 0): every draft equals the argmax: three accepted plus the bonus 33
+    peaks = [9, 9, 12, 30, 20, 21, 22, 33]
+    drafted = torch.tensor([9, 9, 5, 0, 20, 21, 22, 0], dtype=I32)
+    st.decode[2, 9] = 1
+    res = oracle.multistep(peaked(vocab, peaks), st, drafted, [0, 4, 8], slot_mapping=[2, 0])
+    assert [r.offset for r in res] == [2, 3]
+    assert res[0].tokens == [9, 9, 12] and res[1].tokens == [20, 21, 22, 33]
+    after = oracle.apply_multistep_counts(st.decode, res, [2, 0])
+    assert int(after[2, 9]) == 3 and int(after[2, 12]) == 1 and int(after[2, 5]) == 0
+    assert [int(after[0, t]) for t in (20, 21, 22, 33)] == [1, 1, 1, 1]
+    assert int(after.sum()) == int(st.decode.sum()) + 7
+
+
+def test_top_logprobs_follow_the_row_limit_and_the_0x400_bit():
+
+    vocab = 256
+    st = slots_state(3, vocab, oracle.TOP_K_LOGPROBS)
+    st.target[1] = 0                                   # 0x400 off: no top logprobs at all
+    st.top_logprobs = torch.tensor([2, 9, 9], dtype=I32)   # slot 2: 9 > Z, capped at Z = 5
+    logits = torch.randn(3, vocab, generator=torch.Generator().manual_seed(4)).mul(2).to(BF16)
+    res = oracle.singular(logits, st, logprobs=True, max_top_logprobs=5)
+    assert [len(r.top_tokens) for r in res] == [2, 0, 5]
+    assert [len(r.top_logprobs) for r in res] == [2, 0, 5]
+    order = logits[0].float().sort(descending=True, stable=True).indices
+    assert res[0].top_tokens == order[:2].tolist()
+    v = logits[0].float().sort(descending=True).values[:128].double()
+    assert abs(res[0].top_logprobs[1] - float(v[1] - torch.logsumexp(v, 0))) < 1e-5
+
+
+def test_multistep_top_logprobs_per_emitted_position():
+
+    vocab, n = 256, 4
+    st = slots_state(1, vocab, oracle.TOP_K_LOGPROBS)
+    st.top_logprobs = torch.tensor([3], dtype=I32)
+    logits = torch.randn(n, vocab, generator=torch.Generator().manual_seed(5)).mul(2).to(BF16)
+    st.uniform.fill_(0.0)                              # u = 0: every point-mass draft is accepted
+    drafted = logits.float().argmax(-1).to(I32)
+    res = oracle.multistep(logits, st, drafted, [0, n], logprobs=True, max_top_logprobs=20)
+    assert res[0].offset == n - 1
+    assert [len(t) for t in res[0].top_tokens] == [3] * n
+    st.target[0] = 0
+    res = oracle.multistep(logits, st, drafted, [0, n], logprobs=True, max_top_logprobs=20)
+    assert [len(t) for t in res[0].top_tokens] == [0] * n
+
+
+def test_multistep_history_is_the_earlier_drafts():
+    """Step i is penalized by drafts[:i] (presence 2): with drafts (5, 6), step 1 must see 5
+    penalized (5 -> -1 < 6 = 0.5) and accept 6, and the bonus step sees both. Without the history
+    step 1 rejects; counting step i's own draft rejects step 0."""
+
+    vocab = 64
+    st = slots_state(1, vocab, oracle.GREEDY | oracle.PRES)
+    st.presence = torch.tensor([2.0]).to(BF16)
+    x = torch.full((3, vocab), -4.0)
+    x[:, 5], x[:, 6] = 1.0, 0.5
+    res = oracle.multistep(x.to(BF16), st, torch.tensor([5, 6, 0], dtype=I32), [0, 3])
+    assert res[0].offset == 2 and res[0].tokens == [5, 6, 5]
+
+
+def test_multistep_history_never_counts_token_0():
+    """Drafts of token 0 add nothing to the history (the reference pads with 0 and restores the
+    count of token 0): step 1 keeps token 0 at 1.0 above token 6 at 0.5."""
+
+    vocab = 64
+    st = slots_state(1, vocab, oracle.GREEDY | oracle.PRES)
+    st.presence = torch.tensor([2.0]).to(BF16)
+    x = torch.full((3, vocab), -4.0)
+    x[:, 0], x[:, 6] = 1.0, 0.5
+    res = oracle.multistep(x.to(BF16), st, torch.tensor([0, 0, 0], dtype=I32), [0, 3])
+    assert res[0].offset == 2 and res[0].tokens == [0, 0, 0]
+    # a counted token 0 in the slot's own decode counts does apply
+    st.decode[0, 0] = 1
+    res = oracle.multistep(x.to(BF16), st, torch.tensor([6, 0, 0], dtype=I32), [0, 3])
+    assert res[0].tokens[0] == 6
+
+
+# ------------------------------------------------------------------------------------------------
+# The batched restatement (bench.py's CPU baseline) against the per-row one
+# ------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("indicator", [None, 0x3BF, 0x5BE, 0x41, 0x7A0])
+def test_batched_oracle_matches_per_row(indicator):
+
+    from oracle import batch
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Indicator
+
+    rows, vocab = 12, 4096
+    seed = 7 if indicator is None else indicator
+    b = SamplingBuffers.random(size=rows, timesteps=1, vocab_size=vocab, device="cpu", seed=seed,
+                               indicators=None if indicator is None else Indicator(indicator),
+                               max_top_logprobs=5)
+    logits = (torch.randn(rows, vocab, generator=torch.Generator().manual_seed(seed)) * 3).to(BF16)
+    st = oracle.State.from_buffers(b)
+
+    got = batch.singular(logits, st, max_top_logprobs=5)
+    res = oracle.singular(logits, st, scope="target", logprobs=True, max_top_logprobs=5)
+
+    assert got.tokens.tolist() == [r.token for r in res]
+
+    for r, rec in enumerate(res):
+
+        assert float(got.logprobs[r]) == rec.logprob
+        z = len(rec.top_tokens)
+        assert got.top_tokens[r, :z].tolist() == rec.top_tokens
+        assert got.top_logprobs[r, :z].tolist() == rec.top_logprobs
+        assert bool((got.top_tokens[r, z:] == -1).all())
+
+
+def test_batched_oracle_on_config1_rows():
+
+    import bench
+    from oracle import batch
+
+    work = bench.c1_workload(batch=8, vocab=32768)
+    st = oracle.State.from_buffers(work.buffers)
+    got = batch.singular(work.logits, st, max_top_logprobs=5)
+    res = oracle.singular(work.logits, st, scope="target", logprobs=True, max_top_logprobs=5)
+    assert got.tokens.tolist() == [r.token for r in res]
+    assert got.logprobs.tolist() == [r.logprob for r in res]
+
+
+def test_logprob_tolerance_floor():
+    """The absolute floor admits the other bf16 rounding of a logprob near 0 whose fp32 value sits
+    a few ulp of log(s) from a rounding boundary, and nothing further away."""
+
+    e = -0.0017128810286521912          # fp32 log-softmax value near a bf16 midpoint
+    assert not oracle.bf16_within(-0.001708984375, e)
+    assert oracle.bf16_within(-0.001708984375, e, floor=oracle.LOGPROB_FLOOR)
+    assert oracle.bf16_within(-0.0017166137695, e, floor=oracle.LOGPROB_FLOOR)
+    assert not oracle.bf16_within(-0.0017013549805, e, floor=oracle.LOGPROB_FLOOR)
+    # away from 0 the relative band governs
+    assert oracle.bf16_within(-3.0, -3.0000001, floor=oracle.LOGPROB_FLOOR)
+    assert not oracle.bf16_within(-3.015625, -3.0, floor=oracle.LOGPROB_FLOOR)

@@ -42,7 +42,9 @@ typedef enum ss_status {
     SS_OK = 0,
     SS_ERR_INVALID_ARGUMENT = 1, /* a size, stride, pointer or alignment the kernels cannot honour */
     SS_ERR_UNSUPPORTED = 2,      /* a configuration outside what was compiled (e.g. block_n)      */
-    SS_ERR_LAUNCH = 3            /* the HIP runtime rejected the launch (hipGetLastError)         */
+    SS_ERR_LAUNCH = 3,           /* the HIP runtime rejected the launch (hipGetLastError)         */
+    SS_ERR_SCRATCH_LIMIT = 4     /* ss_fused_singular_noalloc: the call needs more candidate      */
+                                 /* storage than SS_STATIC_SCRATCH_BYTES                         */
 } ss_status;
 
 typedef enum ss_dtype {
@@ -154,6 +156,22 @@ typedef struct ss_singular_args {
 } ss_singular_args;
 
 int ss_fused_singular(const ss_singular_args *args);
+
+/* ---------------------------------------------------------------------------------------------
+ * ss_fused_singular without a caller-provided scratchpad. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory at all (code under hipGraph capture, serving
+ * loops or harnesses that forbid hipMalloc), which then need not size or own the in-flight
+ * candidate lists either. `scratch` / `stride_scratch` of `args` are ignored; the tiles' candidate
+ * lists (rows * ceil(vocab_size / block_n) * 128 * 4 bytes) go to a static device array of
+ * SS_STATIC_SCRATCH_BYTES that every device the library runs on holds until the process ends.
+ * A larger call fails with SS_ERR_SCRATCH_LIMIT. The call allocates nothing; the first call on a
+ * device only looks up that device's copy of the array. All calls on one device share the array:
+ * calls that overlap on one device (two streams, or two threads) race, so they must be ordered.
+ * Every other argument, output and error is that of ss_fused_singular.
+ * ------------------------------------------------------------------------------------------- */
+#define SS_STATIC_SCRATCH_BYTES (8u << 20)
+
+int ss_fused_singular_noalloc(const ss_singular_args *args);
 
 /* ---------------------------------------------------------------------------------------------
  * Fused chain speculative verification over rows = B*(gamma+1) (fixed) or cu_seqlens[B] (varlen)

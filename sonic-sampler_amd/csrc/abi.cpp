@@ -9,6 +9,9 @@ extern "C" const char *ss_status_string(int status) {
         case SS_ERR_INVALID_ARGUMENT: return "invalid argument";
         case SS_ERR_UNSUPPORTED: return "unsupported configuration";
         case SS_ERR_LAUNCH: return "kernel launch failed";
+        case SS_ERR_SCRATCH_LIMIT:
+            return "the call needs more candidate storage than the static scratch holds "
+                   "(rows * tiles * 128 * 4 > SS_STATIC_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }

@@ -8,9 +8,16 @@
 // logprobs, top-Z logprobs and the draft-probability scatter. The launch boundary orders the two
 // stages across all XCDs without per-workgroup cache maintenance. Semantics follow the
 // reference's PyTorch path (core/naive.py:377-495 `selection`, :648-692 `preamble` / `singular`).
+#include <atomic>
+#include <mutex>
+
 #include "ss_launch.h"
 #include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
+
+// Candidate lists of ss_fused_singular_noalloc. Host code never names this array in a launch or a
+// copy: its device address comes from hipGetSymbolAddress, once per device (static_scratch).
+static __device__ __align__(256) uint32_t scratch[SS_STATIC_SCRATCH_BYTES / 4];
 
 namespace ss {
 
@@ -225,4 +232,48 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
                                   aligned(a->logit_bias, a->stride_bias, 8)));
     if (!vec) return launch_singular<MODE_SCALAR>(a, tiles);
     return direct ? launch_singular<MODE_DIRECT>(a, tiles) : launch_singular<MODE_GATHER_VEC>(a, tiles);
+}
+
+namespace ss {
+
+constexpr int MAX_DEVICES = 64;
+static std::atomic<uint32_t *> g_static_scratch[MAX_DEVICES];
+static std::mutex g_static_scratch_lock;
+
+// The current device's copy of `scratch`, looked up on the first call on that device (with the
+// device current, as hipGetSymbolAddress resolves the symbol for the current device).
+static uint32_t *static_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    uint32_t *p = g_static_scratch[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    std::lock_guard<std::mutex> lock(g_static_scratch_lock);
+    p = g_static_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        void *addr = nullptr;
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return nullptr;
+        p = static_cast<uint32_t *>(addr);
+        g_static_scratch[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+}  // namespace ss
+
+extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
+    using namespace ss;
+    if (!a || a->vocab_size <= 0 || a->rows < 0) return SS_ERR_INVALID_ARGUMENT;
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+        return SS_ERR_UNSUPPORTED;
+    const int64_t tiles = ((int64_t)a->vocab_size + a->block_n - 1) / a->block_n;
+    if ((int64_t)a->rows * tiles * SS_K * (int64_t)sizeof(uint32_t) > (int64_t)SS_STATIC_SCRATCH_BYTES)
+        return SS_ERR_SCRATCH_LIMIT;
+    uint32_t *ptr = static_scratch();
+    if (!ptr) return SS_ERR_LAUNCH;
+    // Every list entry the row stage uses is written by the tile stage of the same call (a greedy
+    // row's merge samples are read but ignored), so the array needs no clearing between calls.
+    ss_singular_args b = *a;
+    b.scratch = ptr;
+    b.stride_scratch = tiles * SS_K;
+    return ss_fused_singular(&b);
 }

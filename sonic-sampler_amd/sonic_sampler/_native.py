@@ -22,6 +22,8 @@ c_u32 = ctypes.c_uint32
 c_u64 = ctypes.c_uint64
 
 SS_OK = 0
+SS_ERR_SCRATCH_LIMIT = 4
+STATIC_SCRATCH_BYTES = 8 << 20   # SS_STATIC_SCRATCH_BYTES
 SS_DTYPE_BF16 = 0
 SS_DTYPE_F32 = 1
 ABI_VERSION = 1
@@ -122,6 +124,7 @@ def load() -> ctypes.CDLL:
     lib.ss_args_size.argtypes = [c_i32]
 
     for name, struct in (("ss_topk", TopKArgs), ("ss_fused_singular", SingularArgs),
+                         ("ss_fused_singular_noalloc", SingularArgs),
                          ("ss_fused_multistep", MultistepArgs)):
         fn = getattr(lib, name)
         fn.restype = c_i32

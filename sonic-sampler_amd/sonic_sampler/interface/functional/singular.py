@@ -15,6 +15,11 @@ Additions to the reference's keywords (all optional):
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
 * ``tile_events`` -- a pair of timing ``torch.cuda.Event`` recorded by the tile kernel's own
   dispatch at its start and end (per-kernel timing without extra stream packets).
+* ``static_scratch`` -- keep the tiles' candidate lists in the library's static device array
+  (``ss_fused_singular_noalloc``) instead of a scratchpad: no scratchpad is allocated or passed,
+  for callers that cannot allocate. Calls of this kind on one device share the array, so they must
+  not overlap (one stream, one thread at a time); a call that needs more than
+  ``SS_STATIC_SCRATCH_BYTES`` (8 MiB: rows x tiles x 512 B) raises ``RuntimeError``.
 """
 
 from __future__ import annotations
@@ -110,6 +115,7 @@ def fused_singular(
     philox_offset: int = 0,
     philox_step: int = 0,
     tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
+    static_scratch: bool = False,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
@@ -140,7 +146,17 @@ def fused_singular(
     batch_size, vocab_size = logits.shape
     vocab_size = min(vocab_size, local_vocab or vocab_size)
 
-    _, _, bitpacked, vocab_blocks = resolve_scratchpad(logits, block_n, scratchpad)
+    if static_scratch:
+
+        bitpacked = None
+
+        if -(-logits.size(1) // block_n) <= 1:
+
+            raise ValueError("total vocab blocks must be greater than 1")
+
+    else:
+
+        _, _, bitpacked, vocab_blocks = resolve_scratchpad(logits, block_n, scratchpad)
 
     final_tokens = resolve_tokens(output_tokens, batch_size, logits)
 
@@ -210,11 +226,13 @@ def fused_singular(
         logprobs=p(token_logprobs), stride_logprobs=s(token_logprobs),
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
         probabilities=p(probabilities), stride_probabilities=s(probabilities),
-        scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
+        scratch=p(bitpacked), stride_scratch=s(bitpacked),
         stream=_native.stream_of(logits),
     )
     args.tile_start, args.tile_end = _native.event_pair(tile_events)
 
-    _native.check(_native.load().ss_fused_singular(ctypes.byref(args)), "ss_fused_singular")
+    lib = _native.load()
+    entry = "ss_fused_singular_noalloc" if static_scratch else "ss_fused_singular"
+    _native.check(getattr(lib, entry)(ctypes.byref(args)), entry)
 
     return selection

@@ -99,6 +99,16 @@ typedef struct ss_topk_args {
 
 int ss_topk(const ss_topk_args *args);
 
+/* Kernel layout of ss_fused_singular. TILES: a tile grid (rows x tiles) writes every tile's
+ * top-128 to the scratchpad, then one workgroup per row merges and selects (two launches).
+ * ROWWISE: one workgroup per row streams the row tile by tile and selects in the same launch
+ * (rows of at most 16 tiles; the scratchpad is not touched). AUTO currently picks TILES. */
+typedef enum ss_strategy {
+    SS_STRATEGY_AUTO = 0,
+    SS_STRATEGY_TILES = 1,
+    SS_STRATEGY_ROWWISE = 2
+} ss_strategy;
+
 /* ---------------------------------------------------------------------------------------------
  * Fused single-step sampling: logit processors -> bounded top-128 -> truncation -> Gumbel-max,
  * with optional logprobs, top-Z logprobs, draft-probability scatter and decode-count update.
@@ -120,7 +130,7 @@ typedef struct ss_singular_args {
     int32_t update_counts;
     int32_t return_logprobs;
     int32_t return_probabilities;
-    int32_t reserved;
+    int32_t strategy;            /* ss_strategy: kernel layout (0 = chosen by the library) */
     const uint16_t *indicators;  /* [slots] */
     const int32_t *slot_mapping; /* [rows] or NULL */
     const int32_t *d2t;          /* [vocab_size] or NULL */

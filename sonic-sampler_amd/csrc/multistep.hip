@@ -83,6 +83,7 @@ __device__ __forceinline__ RowState multistep_row_state(const ss_multistep_args 
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.vt = a.vocab_size;
     rs.nhist = 0;
+    rs.glds = nullptr;
     return rs;
 }
 
@@ -96,7 +97,7 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
 // Tile stage: grid (tiles, rows).
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
-    __shared__ TileSmem sm;
+    __shared__ TileSmem<E> sm;
     const int row = blockIdx.y;
     const int tile = blockIdx.x;
     const int pivot = request_pivot(a);
@@ -349,10 +350,10 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;

@@ -42,13 +42,19 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
     if (!a.temperature) rs.ind &= ~IND_TEMP;
     rs.vt = a.target_vocab > 0 ? a.target_vocab : a.vocab_size;
     rs.nhist = 0;
+    rs.glds = nullptr;
     return rs;
 }
 
-// Tile stage: grid (tiles, rows).
+// Tile stage: grid (tiles, rows). With d2t and a grammar mask, `stage_words` > 0 stages the
+// row's grammar words in workgroup memory (dynamic shared memory) before the prologue, so that the
+// per-element lookups through d2t read LDS: as scattered global gathers (one cache line per
+// element) they are bounded by the vector cache's line rate, not by HBM.
 template <int E, int MODE>
-__global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles) {
-    __shared__ TileSmem sm;
+__global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles,
+                                                                  int stage_words) {
+    __shared__ TileSmem<E> sm;
+    extern __shared__ __align__(16) uint32_t grammar_words[];
     const int row = blockIdx.y;
     const int tile = blockIdx.x;
     u32x2 lw[E / 4];
@@ -56,49 +62,51 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
     const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
     const uint32_t ind = uniform_u16(a.indicators, slot);
     RowState rs = singular_row_state(a, row, slot, ind);
+    bool sync = false;
+    if (MODE != MODE_DIRECT && stage_words > 0) {
+        const Uses u = row_uses(rs);
+        if (u.g && u.remap) {
+            stage_grammar(rs.grammar, stage_words, grammar_words);
+            rs.glds = grammar_words;
+            sync = true;
+        }
+    }
     if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         rs.nhist = a.timestep;
         if ((int)threadIdx.x < rs.nhist)
             sm.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
-        __syncthreads();
+        sync = true;
     }
+    if (sync) __syncthreads();
     Keys<E> keys;
     prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
 }
 
-// Row stage of one row: merge of the tiles' candidates and the selection. All threads call.
-__device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSmem &sm, int row,
-                                             int tiles) {
-    touch_kernargs<sizeof(ss_singular_args)>();
-    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
-    RowSamples smp;
-    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
-    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
-    const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
-                                    a.max_top_logprobs);
-    const uint32_t ind = lane_u32(prm, RP_IND);
-
-    if (ind & IND_GREEDY) {
-        if (threadIdx.x < 64) {
-            int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, smp.greedy);
-            if (a.d2t) token = a.d2t[token];
-            if (threadIdx.x == 0) {
-                if (a.update_counts && a.decode_counts) {
-                    int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
-                    if (a.is_prefill) atomicExch(d, 1); else atomicAdd(d, 1);
-                }
-                if (a.return_logprobs && a.logprobs) a.logprobs[(int64_t)row * a.stride_logprobs] = 0;
-                a.tokens[(int64_t)row * a.stride_tokens] = token;
-            }
+// Greedy row (wave 0): the argmax over the tiles' maxima, d2t remap, count update, outputs.
+// `first` is scr[lane], read ahead by load_samples.
+__device__ __forceinline__ void singular_greedy(const ss_singular_args &a, const uint32_t *scr,
+                                                int tiles, int row, int slot, uint32_t first) {
+    if (threadIdx.x >= 64) return;
+    int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, first);
+    if (a.d2t) token = a.d2t[token];
+    if (threadIdx.x == 0) {
+        if (a.update_counts && a.decode_counts) {
+            int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
+            if (a.is_prefill) atomicExch(d, 1); else atomicAdd(d, 1);
         }
-        return;
+        if (a.return_logprobs && a.logprobs) a.logprobs[(int64_t)row * a.stride_logprobs] = 0;
+        a.tokens[(int64_t)row * a.stride_tokens] = token;
     }
+}
 
-    float v0 = 0.f, v1 = 0.f;
-    int i0 = 0, i1 = 0;
-    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
-
+// Selection of a non-greedy row from its sorted top-128 (wave 0 holds element e = 2 * lane + i
+// as (v_i, idx_i)): truncation, d2t remap, Gumbel-max over bf16(v - w), count update, logprobs,
+// top-Z logprobs and the probability scatter. All threads call.
+__device__ __forceinline__ void singular_select(const ss_singular_args &a, SampleSmem &sm, int row,
+                                                int slot, uint32_t prm, float v0, float v1, int i0,
+                                                int i1) {
+    const uint32_t ind = lane_u32(prm, RP_IND);
     // Waves 1 and 2 remap the 128 candidates' columns and draw their noise (one candidate per
     // lane) while wave 0 applies the truncation.
     const int wave = (int)threadIdx.x >> 6;
@@ -175,10 +183,126 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
     if (lane == 0) a.tokens[(int64_t)row * a.stride_tokens] = token;
 }
 
+// Row stage of one row: merge of the tiles' candidates (`scr`, global scratch or workgroup
+// memory) and the selection. All threads call.
+__device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSmem &sm, int row,
+                                             int tiles, const uint32_t *scr) {
+    RowSamples smp;
+    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
+    const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
+                                    a.max_top_logprobs);
+    if (lane_u32(prm, RP_IND) & IND_GREEDY) {
+        singular_greedy(a, scr, tiles, row, slot, smp.greedy);
+        return;
+    }
+    float v0 = 0.f, v1 = 0.f;
+    int i0 = 0, i1 = 0;
+    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    singular_select(a, sm, row, slot, prm, v0, v1, i0, i1);
+}
+
 // Row stage: grid rows.
 __global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
     __shared__ SampleSmem sm;
-    singular_row(a, sm, blockIdx.x, tiles);
+    touch_kernargs<sizeof(ss_singular_args)>();
+    const int row = blockIdx.x;
+    singular_row(a, sm, row, tiles, a.scratch + (int64_t)row * a.stride_scratch);
+}
+
+// Workgroup memory of the one-launch form. The tile stage's and the row stage's memory share
+// space (a barrier separates the phases); the tiles' candidate lists stay resident throughout.
+constexpr int ROWWISE_MAX_TILES = 16;
+
+template <int E>
+struct RowwiseSmem {
+    union {
+        TileSmem<E> tile;
+        SampleSmem sample;
+    };
+    uint32_t lists[ROWWISE_MAX_TILES * SS_K];
+};
+
+// One-launch form, grid rows: one workgroup per row streams the row tile by tile (the next tile's
+// logits are in flight while the current tile is selected), keeps every tile's sorted top-128 in
+// workgroup memory, merges them and performs the selection -- no scratch round trip through
+// global memory and no second launch. With d2t and a grammar mask, `stage_words` > 0 asks for the
+// row's grammar words to be staged in workgroup memory first (dynamic shared memory), so that the
+// per-element lookups through d2t read LDS instead of scattered global words.
+template <int E, int MODE>
+__global__ __launch_bounds__(SS_BLOCK) void singular_rowwise_kernel(ss_singular_args a, int tiles,
+                                                                    int stage_words) {
+    __shared__ RowwiseSmem<E> sm;
+    extern __shared__ __align__(16) uint32_t grammar_words[];
+    const int row = blockIdx.x;
+    const uint16_t *lrow = a.logits + (int64_t)row * a.stride_logits;
+    u32x2 lw[E / 4];
+    if (MODE != MODE_SCALAR) load_logits_vec<E>(lrow, 0, a.vocab_size, lw);
+    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
+    const uint32_t ind = uniform_u16(a.indicators, slot);
+    RowState rs = singular_row_state(a, row, slot, ind);
+    const Uses u = row_uses(rs);
+    if (stage_words > 0 && u.g && u.remap) {
+        stage_grammar(rs.grammar, stage_words, grammar_words);
+        rs.glds = grammar_words;
+    }
+    if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
+        rs.nhist = a.timestep;
+        if ((int)threadIdx.x < rs.nhist)
+            sm.tile.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
+    }
+    __syncthreads();
+    const bool greedy = (ind & IND_GREEDY) != 0;
+#pragma unroll 1
+    for (int t = 0; t < tiles; ++t) {
+        u32x2 nx[E / 4];
+        if (MODE != MODE_SCALAR && t + 1 < tiles)
+            load_logits_vec<E>(lrow, (t + 1) * a.block_n, a.vocab_size, nx);
+        Keys<E> keys;
+        prologue_keys<E, MODE>(rs, t * a.block_n, a.vocab_size, sm.tile.hist, lw, keys);
+        tile_stage<E>(sm.tile, greedy, keys, sm.lists, t);
+        // the next tile reuses the tile stage's memory, and the lists feed the row stage
+        __syncthreads();
+        if (MODE != MODE_SCALAR) {
+#pragma unroll
+            for (int c = 0; c < E / 4; ++c) lw[c] = nx[c];
+        }
+    }
+    const uint32_t *scr = sm.lists;
+    RowSamples smp;
+    load_samples(scr, tiles, a.block_n, smp);
+    const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
+                                    a.max_top_logprobs);
+    if (greedy) {
+        singular_greedy(a, scr, tiles, row, slot, smp.greedy);
+        return;
+    }
+    float v0 = 0.f, v1 = 0.f;
+    int i0 = 0, i1 = 0;
+    merge_row(sm.sample, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    singular_select(a, sm.sample, row, slot, prm, v0, v1, i0, i1);
+}
+
+// Grammar words to stage per workgroup: with d2t and a grammar mask whose row fits, else 0.
+static int staged_grammar_words(const ss_singular_args *a) {
+    const int words = ((a->target_vocab > 0 ? a->target_vocab : a->vocab_size) + 31) >> 5;
+    return (a->d2t && a->grammar && words <= SS_STAGE_MAX_WORDS) ? words : 0;
+}
+
+template <int MODE>
+static int launch_rowwise(const ss_singular_args *a, int tiles) {
+    const int stage = staged_grammar_words(a);
+    const size_t dyn = (size_t)((stage + 3) & ~3) * sizeof(uint32_t);
+    dim3 grid((unsigned)a->rows), block(SS_BLOCK);
+    hipStream_t s = (hipStream_t)a->stream;
+    switch (a->block_n) {
+        case 1024: hipLaunchKernelGGL((singular_rowwise_kernel<4, MODE>), grid, block, dyn, s, *a, tiles, stage); break;
+        case 2048: hipLaunchKernelGGL((singular_rowwise_kernel<8, MODE>), grid, block, dyn, s, *a, tiles, stage); break;
+        case 4096: hipLaunchKernelGGL((singular_rowwise_kernel<16, MODE>), grid, block, dyn, s, *a, tiles, stage); break;
+        case 8192: hipLaunchKernelGGL((singular_rowwise_kernel<32, MODE>), grid, block, dyn, s, *a, tiles, stage); break;
+        default: return SS_ERR_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
 template <int MODE>
@@ -186,11 +310,13 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     // x: the tiles of a row, y: rows; the linear dispatch order is row-major as (row, tile)
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
+    const int stage = staged_grammar_words(a);
+    const size_t dyn = (size_t)((stage + 3) & ~3) * sizeof(uint32_t);
     switch (a->block_n) {
-        case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+        case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+        case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+        case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
@@ -230,6 +356,16 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
                      (!direct || (aligned(a->decode_counts, a->stride_decode, 16) &&
                                   aligned(a->context_counts, a->stride_context, 16) &&
                                   aligned(a->logit_bias, a->stride_bias, 8)));
+    if (a->strategy < SS_STRATEGY_AUTO || a->strategy > SS_STRATEGY_ROWWISE) return SS_ERR_INVALID_ARGUMENT;
+    if (a->strategy == SS_STRATEGY_ROWWISE && tiles > ROWWISE_MAX_TILES) return SS_ERR_UNSUPPORTED;
+    // AUTO takes the tile grid: one workgroup per row leaves a CU with a single workgroup (one
+    // wave per SIMD) working through its tiles one after another, which measured slower on every
+    // shape tried (config 4: 36 us for the row kernel against 23 + 7 us for the two launches).
+    const bool rowwise = a->strategy == SS_STRATEGY_ROWWISE;
+    if (rowwise) {
+        if (!vec) return launch_rowwise<MODE_SCALAR>(a, tiles);
+        return direct ? launch_rowwise<MODE_DIRECT>(a, tiles) : launch_rowwise<MODE_GATHER_VEC>(a, tiles);
+    }
     if (!vec) return launch_singular<MODE_SCALAR>(a, tiles);
     return direct ? launch_singular<MODE_DIRECT>(a, tiles) : launch_singular<MODE_GATHER_VEC>(a, tiles);
 }

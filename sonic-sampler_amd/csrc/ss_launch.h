@@ -10,12 +10,12 @@ namespace ss {
 // itself (hipExtLaunchKernelGGL), so they time exactly this kernel and add no packets to the
 // stream between it and its neighbours.
 template <class Kernel, class... Args>
-inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, hipStream_t stream, void *start,
-                         void *end, Args... args) {
+inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, size_t shared, hipStream_t stream,
+                         void *start, void *end, Args... args) {
     if (start && end)
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, (hipEvent_t)start, (hipEvent_t)end, 0, args...);
+        hipExtLaunchKernelGGL(kernel, grid, block, shared, stream, (hipEvent_t)start, (hipEvent_t)end, 0, args...);
     else
-        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+        hipLaunchKernelGGL(kernel, grid, block, shared, stream, args...);
 }
 
 }  // namespace ss

@@ -35,7 +35,8 @@ struct SampleSmem {
     float noise[SS_K];         // selection: their Gumbel noise
 };
 
-// Workgroup memory of the tile kernels.
+// Workgroup memory of the tile kernels (E keys per thread).
+template <int E>
 struct TileSmem {
     uint32_t scan[SS_WAVES * 8];  // workgroup scans of up to 8 values per thread
     uint32_t red[SS_WAVES];
@@ -43,6 +44,9 @@ struct TileSmem {
     uint32_t run[SS_WAVES][SS_K + 64];  // each wave's survivors, then its sorted run
     uint32_t run2[2][SS_K];       // merge tree: the top-128 of runs (0, 1) and (2, 3)
     int32_t hist[64];             // drafted tokens that extend the decode history
+    // each wave's packed keys, pair i of lane l at [i * 64 + l], read back by the survivors of
+    // wave_survivors_masked
+    uint32_t keys[SS_WAVES][E / 2 * 64];
 };
 
 // Request state of one logit row, uniform over the workgroup. Row pointers are already offset to
@@ -58,7 +62,12 @@ struct RowState {
     float rep, freq, pres, temp;
     int vt;     // width of the counts / bias / grammar rows (target vocabulary)
     int nhist;  // drafted tokens of the history staged in SampleSmem::hist
+    // The row's grammar words staged in workgroup memory (gather layout only), or NULL: the
+    // gathers through d2t then read LDS instead of scattered global words.
+    const uint32_t *glds;
 };
+
+typedef const __attribute__((address_space(3))) uint32_t *lds_cu32p;
 
 __device__ __forceinline__ int tile_col(int j) {  // column offset of element j inside a tile
     return (j >> 2) * (SS_BLOCK * 4) + (int)threadIdx.x * 4 + (j & 3);
@@ -248,18 +257,25 @@ __device__ __forceinline__ float chain_ieee(const Chain &k, float x, int32_t dec
 // bias is nonzero (it may also be nonzero for a zero bias: the chain is exact for every element).
 // maybe_exc is false when no element can have a nonzero count or bias (no penalty or bias plane is
 // read) and the chain is not forced on every element: the keys are then the temperature keys.
-template <int E, class XOf, class BiasOf, class BiasWordOf>
+// pair(j) (j even) is the 32-bit word holding the masked bf16 logits of elements j and j + 1.
+template <int E, class XOf, class PairOf, class BiasOf, class BiasWordOf>
 __device__ __forceinline__ void finish_keys(const Chain &k, bool all_exc, bool partial, XOf x,
-                                            bool maybe_exc,
+                                            PairOf pair, bool maybe_exc,
                                             const bool (&ok)[E], const int32_t (&dec)[E],
                                             const int32_t (&ctx)[E], BiasOf bb, BiasWordOf bw,
                                             Keys<E> &keys) {
     if ((!k.mult || k.rdiv.fast) && (!k.temp || k.tdiv.fast)) {
         const FastChain f = fast_chain(k);
+        if (!k.temp) {
+            // no temperature: the keys of the (grammar-masked) bf16 pairs as they are
 #pragma unroll
-        for (int j = 0; j < E; j += 2) {
-            const f2v v = {x(j) * f.trcp, x(j + 1) * f.trcp};
-            keys.p[j >> 1] = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
+            for (int j = 0; j < E; j += 2) keys.p[j >> 1] = packed_keys(pair(j));
+        } else {
+#pragma unroll
+            for (int j = 0; j < E; j += 2) {
+                const f2v v = {x(j) * f.trcp, x(j + 1) * f.trcp};
+                keys.p[j >> 1] = packed_keys(__builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2v)));
+            }
         }
         // The branch at each element position is on the wave's ballot, so it is uniform: the
         // chain then runs with every lane active and the ballot selects its result.
@@ -478,8 +494,9 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
     };
     // the bias word of the element's pair, shifted so that -0 in the high half does not count
     auto bw = [&](int j) { return ((j & 2) ? pl.bw[j >> 2].y : pl.bw[j >> 2].x) << 1; };
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, all_exc || u.rep || u.mult || u.bias, ok, dec,
-                   ctx, bb, bw, keys);
+    auto pair = [&](int j) { return (j & 2) ? lw[j >> 2].y : lw[j >> 2].x; };
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, pair, all_exc || u.rep || u.mult || u.bias, ok,
+                   dec, ctx, bb, bw, keys);
 }
 
 // Direct layout, row with every side plane off (no grammar, penalty or bias): the keys come from
@@ -503,7 +520,8 @@ __device__ __forceinline__ void plain_keys(const RowState &rs, const Uses &u, in
         return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
     };
     auto none = [](int) { return 0u; };
-    finish_keys<E>(k, false, col0 + SS_BLOCK * E > V, x, false, ok, zero, zero, none, none, keys);
+    auto pair = [&](int j) { return (j & 2) ? lw[j >> 2].y : lw[j >> 2].x; };
+    finish_keys<E>(k, false, col0 + SS_BLOCK * E > V, x, pair, false, ok, zero, zero, none, none, keys);
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
@@ -571,10 +589,13 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
         }
         if (u.g) {
             const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
+            const lds_cu32p gl = (lds_cu32p)rs.glds;
 #pragma unroll
             for (int j = 0; j < E; ++j) {
-                // a masked element becomes bf16 -inf (0xff80) in place
-                const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
+                // a masked element becomes bf16 -inf (0xff80) in place; a column outside the
+                // target vocabulary reads 0 (masked) on either path
+                const uint32_t w = rs.glds ? ((uint32_t)tcol[j] < (uint32_t)rs.vt ? gl[tcol[j] >> 5] : 0u)
+                                           : __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
                 const bool keep = ((w >> (tcol[j] & 31)) & 1u) != 0u;
                 uint32_t p = (j & 2) ? lv[j >> 2].y : lv[j >> 2].x;
                 p = keep ? p : (j & 1) ? ((p & 0x0000ffffu) | 0xff800000u) : ((p & 0xffff0000u) | 0xff80u);
@@ -613,8 +634,30 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
     auto bb = [&](int j) { return (j & 1) ? (bpk[j >> 1] & 0xffff0000u) : (bpk[j >> 1] << 16); };
     // the bias word of the element's pair, shifted so that -0 in the high half does not count
     auto bw = [&](int j) { return bpk[j >> 1] << 1; };
-    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, all_exc || u.rep || u.mult || u.bias, ok,
+    auto pair = [&](int j) { return (j & 2) ? lv[j >> 2].y : lv[j >> 2].x; };
+    finish_keys<E>(k, all_exc, col0 + SS_BLOCK * E > V, x, pair, all_exc || u.rep || u.mult || u.bias, ok,
                    dec, ctx, bb, bw, keys);
+}
+
+// Copies the row's `words` grammar words into workgroup memory `dst` (16-byte aligned, at least
+// `words` rounded up to 4 entries): one round of 16-byte loads, at most 8 per thread (words <= 8192),
+// all issued before any is stored. The caller synchronizes the workgroup before reading `dst`.
+constexpr int SS_STAGE_MAX_WORDS = 8192;
+
+__device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int words, uint32_t *dst) {
+    const __amdgpu_buffer_rsrc_t g = row_buffer(grammar, (int64_t)words * 4);
+    const int quads = (words + 3) >> 2;
+    i32x4 q[SS_STAGE_MAX_WORDS / 4 / SS_BLOCK];
+#pragma unroll
+    for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
+        const int w4 = (int)threadIdx.x + i * SS_BLOCK;
+        q[i] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(g, w4 * 16, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
+        const int w4 = (int)threadIdx.x + i * SS_BLOCK;
+        if (w4 < quads) *(i32x4 *)(dst + 4 * w4) = q[i];
+    }
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:
@@ -681,7 +724,7 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
 // by ballot and mbcnt, and the wave sorts them there in descending order (zero padded to 128).
 // Returns the wave's survivor count; above 128 the region holds only the first 128, unsorted.
 template <int E, bool EXACT>
-__device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &keys, uint32_t T,
+__device__ __forceinline__ uint32_t wave_survivors(TileSmem<E> &sm, const Keys<E> &keys, uint32_t T,
                                                    uint32_t tie_keep) {
     const int lane = lane_id();
     uint32_t *run = sm.run[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
@@ -713,6 +756,51 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &
     return cnt;
 }
 
+// The survivors (key > T) of one wave, as wave_survivors<E, false> leaves them, without a ballot
+// per element position. Every lane builds a bitmask of its surviving elements with packed 16-bit
+// operations (bit i: element 2i, bit 16 + i: element 2i + 1), an exclusive scan of the lanes'
+// counts gives each lane its first position in the run, and the lane writes its survivors one
+// set bit at a time (a lane holds a few), reading each survivor's key back from its keys stored
+// in workgroup memory. Returns the wave's survivor count; above 128 the run is left unwritten
+// (the caller takes the exact cut, which rewrites every run).
+template <int E>
+__device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const Keys<E> &keys,
+                                                          uint32_t T) {
+    static_assert(E / 2 <= 16, "one mask bit per element");
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t *run = sm.run[wave];
+    uint32_t *spill = sm.keys[wave];
+    const u16x2 tt = __builtin_bit_cast(u16x2, T | (T << 16));
+    const u16x2 one = {1, 1};
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+        // max(key - T, 0) is nonzero exactly when key > T; its minimum with 1 is that bit
+        const u16x2 d = __builtin_elementwise_min(
+            __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, keys.p[i]), tt), one);
+        mask |= __builtin_bit_cast(uint32_t, d) << i;
+        spill[i * 64 + lane] = keys.p[i];
+    }
+    const uint32_t n = (uint32_t)__popc(mask);
+    const uint32_t inc = wave_inclusive_sum(n);
+    const uint32_t total = lane_u32(inc, 63);
+    if (total > (uint32_t)SS_K) return total;
+    uint32_t pos = inc - n;
+    const uint32_t cb = 0xffffu - 4u * threadIdx.x;  // 0xffff - column of the lane's element 0
+    while (mask) {
+        const uint32_t b = (uint32_t)__builtin_ctz(mask);
+        mask &= mask - 1u;
+        const uint32_t i = b & 15u, hi = b >> 4;
+        const uint32_t key = (spill[i * 64 + lane] >> (hi << 4)) & 0xffffu;
+        const uint32_t j = 2u * i + hi;  // element index; its column offset in the tile
+        const uint32_t off = (j >> 2) * (SS_BLOCK * 4) + (j & 3u);
+        run[pos++] = ((key << 16) | cb) - off;
+    }
+    return total;
+}
+
 // Tile stage. Greedy rows store one u32 per tile: (key << 16) | (0xffff - column offset), whose
 // maximum picks the lowest column among equal maxima. Other rows store their exact top-128 as the
 // same composites, sorted in descending order (0 for absent entries), at scratch[tile * 128 ...].
@@ -733,7 +821,7 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem &sm, const Keys<E> &
 // 128 - #(key > T) of the ties: exactly the first 128 of the stable descending order, so no wave
 // can exceed 128.
 template <int E>
-__device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const Keys<E> &keys,
+__device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const Keys<E> &keys,
                                            uint32_t *scr, int tile) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
@@ -777,7 +865,21 @@ __device__ __forceinline__ void tile_stage(TileSmem &sm, bool greedy, const Keys
     __syncthreads();
     const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
     uint32_t T = lo ? lo - 1 : 0u;  // key 0 (absent) never survives
-    uint32_t cnt = wave_survivors<E, false>(sm, keys, T, 0u);
+    const uint32_t cnt = wave_survivors_masked<E>(sm, keys, T);
+    if (cnt <= 64) {
+        uint32_t *run = sm.run[wave];
+        uint32_t v = lane < (int)cnt ? run[lane] : 0u;
+        wave_sort64_desc(v);
+        run[lane] = v;
+        run[64 + lane] = 0u;
+    } else if (cnt <= (uint32_t)SS_K) {
+        uint32_t *run = sm.run[wave];
+        uint32_t a0 = 2 * lane < (int)cnt ? run[2 * lane] : 0u;
+        uint32_t a1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0u;
+        wave_bitonic128_desc<2>(a0, a1);
+        run[2 * lane] = a0;
+        run[2 * lane + 1] = a1;
+    }
     if (lane == 0) sm.cnt[wave] = cnt;
     __syncthreads();
     if (max(max(sm.cnt[0], sm.cnt[1]), max(sm.cnt[2], sm.cnt[3])) > (uint32_t)SS_K) {

@@ -23,6 +23,7 @@ c_u64 = ctypes.c_uint64
 
 SS_OK = 0
 SS_ERR_SCRATCH_LIMIT = 4
+STRATEGY_AUTO, STRATEGY_TILES, STRATEGY_ROWWISE = 0, 1, 2
 STATIC_SCRATCH_BYTES = 8 << 20   # SS_STATIC_SCRATCH_BYTES
 SS_DTYPE_BF16 = 0
 SS_DTYPE_F32 = 1
@@ -47,7 +48,7 @@ class SingularArgs(ctypes.Structure):
         ("logits", c_p), ("stride_logits", c_i64), ("rows", c_i32), ("vocab_size", c_i32),
         ("target_vocab", c_i32), ("block_n", c_i32), ("lookahead", c_i32), ("timestep", c_i32),
         ("max_top_logprobs", c_i32), ("is_prefill", c_i32), ("update_counts", c_i32),
-        ("return_logprobs", c_i32), ("return_probabilities", c_i32), ("reserved", c_i32),
+        ("return_logprobs", c_i32), ("return_probabilities", c_i32), ("strategy", c_i32),
         ("indicators", c_p), ("slot_mapping", c_p), ("d2t", c_p),
         ("grammar", c_p), ("stride_grammar", c_i64),
         ("context_counts", c_p), ("stride_context", c_i64),

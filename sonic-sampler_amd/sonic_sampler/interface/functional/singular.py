@@ -15,6 +15,9 @@ Additions to the reference's keywords (all optional):
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
 * ``tile_events`` -- a pair of timing ``torch.cuda.Event`` recorded by the tile kernel's own
   dispatch at its start and end (per-kernel timing without extra stream packets).
+* ``kernel_layout`` -- ``"tiles"`` (tile grid + row merge, two launches) or ``"rowwise"`` (one
+  workgroup per row, one launch, rows of at most 16 tiles); ``None`` lets the library choose
+  (currently the tile grid).
 * ``static_scratch`` -- keep the tiles' candidate lists in the library's static device array
   (``ss_fused_singular_noalloc``) instead of a scratchpad: no scratchpad is allocated or passed,
   for callers that cannot allocate. Calls of this kind on one device share the array, so they must
@@ -46,6 +49,10 @@ from sonic_sampler.interface.functional.base import (
     validate_count_update,
 )
 from sonic_sampler.ops.base import MAX_K
+
+
+KERNEL_LAYOUTS = {None: _native.STRATEGY_AUTO, "tiles": _native.STRATEGY_TILES,
+                  "rowwise": _native.STRATEGY_ROWWISE}
 
 
 def resolve_tokens(buffer: Optional[Tensor], batch_size: int, source: Tensor) -> Tensor:
@@ -115,11 +122,16 @@ def fused_singular(
     philox_offset: int = 0,
     philox_step: int = 0,
     tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
+    kernel_layout: Optional[str] = None,
     static_scratch: bool = False,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
     validate_block(block_n)
+
+    if kernel_layout not in KERNEL_LAYOUTS:
+
+        raise ValueError(f"kernel_layout must be one of {sorted(k for k in KERNEL_LAYOUTS if k)} or None")
 
     if world_size != 1 or local_rank != 0:
 
@@ -208,7 +220,7 @@ def fused_singular(
         max_top_logprobs=max_top_logprobs if top_values is not None else 0,
         is_prefill=int(is_prefill), update_counts=int(update_counts),
         return_logprobs=int(token_logprobs is not None),
-        return_probabilities=int(probabilities is not None), reserved=0,
+        return_probabilities=int(probabilities is not None), strategy=KERNEL_LAYOUTS[kernel_layout],
         indicators=p(indicators), slot_mapping=p(slot_mapping), d2t=p(d2t_mapping),
         grammar=p(grammar), stride_grammar=s(grammar),
         context_counts=p(context_counts), stride_context=s(context_counts),

@@ -93,10 +93,12 @@ class UnshardedFusedSingular(TwoStageTiling):
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
         tile_events=None,
+        kernel_layout: Optional[str] = None,
     ) -> Selection:
         """One decode step over `buffers.flags.target` with `gumbel.target[:, 0]` noise.
 
-        ``philox_seed`` switches the noise to the counter-based Philox stream (slot, timestep 0).
+        ``philox_seed`` switches the noise to the counter-based Philox stream (slot, timestep 0);
+        ``kernel_layout`` ("tiles" / "rowwise") overrides the library's choice of kernel layout.
         """
 
         penalties = buffers.repetition
@@ -133,6 +135,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             philox_offset=philox_offset,
             tile_events=tile_events,
             philox_step=0,
+            kernel_layout=kernel_layout,
         )
 
     def drafting(
@@ -151,10 +154,12 @@ class UnshardedFusedSingular(TwoStageTiling):
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
         tile_events=None,
+        kernel_layout: Optional[str] = None,
     ) -> Selection:
         """One draft step over `buffers.flags.draft` with `gumbel.draft[:, timestep]` noise.
 
-        For ``timestep > 0`` the first ``timestep`` columns of ``tokens`` count as decode history.
+        For ``timestep > 0`` the first ``timestep`` columns of ``tokens`` count as decode history;
+        ``kernel_layout`` ("tiles" / "rowwise") overrides the library's choice of kernel layout.
         """
 
         penalties = buffers.repetition
@@ -198,4 +203,5 @@ class UnshardedFusedSingular(TwoStageTiling):
             philox_offset=philox_offset,
             tile_events=tile_events,
             philox_step=timestep,
+            kernel_layout=kernel_layout,
         )

@@ -464,3 +464,117 @@ def test_graph_replay_verifier_config3():
                                         slot_mapping=slots.tolist(), probabilities=q, logprobs=True,
                                         max_top_logprobs=20)
             check_multistep(captured, expected, work.cu_seqlens, logprobs=True)
+
+
+# ------------------------------------------------------------------------------------------------
+# The two kernel layouts of the single-step path (tile grid + row merge, one workgroup per row)
+# ------------------------------------------------------------------------------------------------
+
+def layout_outputs(selection, probs, buffers, host, rows):
+    """Outputs both layouts must produce identically: tokens, logprobs, the written top
+    logprobs, the probability buffer and the decode counts."""
+
+    out = [selection.tokens.cpu(), buffers.repetition.counts.decode.cpu()]
+
+    if probs is not None:
+
+        out.append(probs.cpu())
+
+    if selection.logprobs is not None:
+
+        out.append(selection.logprobs.selected.cpu())
+        top = selection.logprobs.top_k
+
+        if top is not None:
+
+            written = torch.zeros(top.tokens.shape, dtype=torch.bool)
+
+            for r in range(rows):
+
+                ind = int(host.flags.indicators.target[r])
+
+                if ind & 0x400 and not ind & 0x40:
+
+                    written[r, :min(int(host.top_logprobs[r]), top.tokens.size(1))] = True
+
+            out += [top.tokens.cpu()[written], top.logprobs.cpu()[written]]
+
+    return out
+
+
+@pytest.mark.parametrize("vocab,block,indicator,seed", [
+    (16384, 2048, EVERY_PROCESSOR, 61), (32000, 4096, None, 62), (8191, 1024, None, 63),
+    (30720, 8192, EVERY_PROCESSOR, 64)])
+def test_layouts_agree_autoregressive(vocab, block, indicator, seed):
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    rows = 24
+    host = random_host(rows, 1, vocab, seed, indicator)
+    logits = spiked_logits(rows, vocab, seed=800 + seed).to(DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=5,
+                                                block_size=block, device=DEV)
+    results = {}
+
+    for layout in ("tiles", "rowwise"):
+
+        print(f"autoregressive V={vocab} block={block} layout={layout}", flush=True)
+        buffers = to_device(host, DEV)
+        selection = sampler.autoregressive(logits, buffers, update_counts=True, logprobs=True,
+                                           kernel_layout=layout)
+        torch.cuda.synchronize()
+        results[layout] = layout_outputs(selection, None, buffers, host, rows)
+
+        if layout == "rowwise":
+
+            state = oracle.State.from_buffers(host)
+            expected = oracle.singular(logits.cpu(), state, scope="target", logprobs=True, max_top_logprobs=5)
+            check_singular(selection, expected, logprobs=True)
+
+    for a, b in zip(results["tiles"], results["rowwise"]):
+
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("block", [4096, 8192])
+def test_layouts_agree_drafting_d2t_grammar(block):
+    """Config-4 shape at 64 rows: d2t into a 262144-token target vocabulary with a 5% grammar
+    mask; the rowwise layout stages each row's 32 KB of grammar words in workgroup memory."""
+
+    from bench import c4_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    work = c4_workload(rows=64, slots=128)
+    rows = work.logits.size(0)
+    slots = work.buffers.layout.rows
+    sampler = UnshardedFusedSingular.initialize(vocab_size=work.vocab, batch_size=rows, lookahead=4,
+                                                block_size=block, max_top_logprobs=5, device=DEV)
+    results = {}
+
+    for layout in ("tiles", "rowwise"):
+
+        print(f"drafting d2t+grammar block={block} layout={layout}", flush=True)
+        buffers = to_device(work.buffers, DEV)
+        probs = torch.zeros(slots, work.target_vocab, dtype=torch.bfloat16, device=DEV)
+        tokens = work.tokens.to(DEV)
+        selection = sampler.drafting(work.logits.to(DEV), buffers, timestep=work.timestep, tokens=tokens,
+                                     probabilities=probs, slot_mapping=work.slot_mapping.to(DEV),
+                                     d2t_mapping=work.d2t.to(DEV), target_vocab=work.target_vocab,
+                                     in_place=True, kernel_layout=layout)
+        torch.cuda.synchronize()
+        results[layout] = [selection.tokens.cpu(), probs.cpu(), tokens.cpu()]
+
+        if layout == "rowwise":
+
+            state = oracle.State.from_buffers(work.buffers)
+            expected = oracle.singular(work.logits, state, scope="draft", timestep=work.timestep,
+                                       slot_mapping=work.slot_mapping.tolist(), d2t=work.d2t,
+                                       drafted=work.tokens, history=work.timestep, probs=True,
+                                       max_top_logprobs=5)
+            check_singular(selection, expected, logprobs=False, probabilities=probs,
+                           slot_mapping=work.slot_mapping)
+
+    for a, b in zip(results["tiles"], results["rowwise"]):
+
+        assert torch.equal(a, b)

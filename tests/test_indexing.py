@@ -133,3 +133,72 @@ def test_row_merge_sample_reads_stay_inside_the_scratch_row(tiles):
             assert 0 <= lst * SS_K + pos < tiles * SS_K
 
     assert len(seen) == 4 * SS_K
+
+
+def masked_survivors(keys16, T):
+    """wave_survivors_masked for one wave: keys16[lane][j] (16-bit keys, E per lane) -> the run it
+    writes (composites (key << 16) | (0xffff - column)), in write order, or None on overflow."""
+
+    E = len(keys16[0])
+    masks, counts = [], []
+
+    for lane in range(WAVE):
+
+        mask = 0
+
+        for i in range(E // 2):
+
+            lo, hi = keys16[lane][2 * i], keys16[lane][2 * i + 1]
+            d = (min(max(lo - T, 0), 1)) | (min(max(hi - T, 0), 1) << 16)   # packed sat-sub, min 1
+            mask |= d << i
+
+        masks.append(mask & 0xffffffff)
+        counts.append(bin(mask).count("1"))
+
+    total = sum(counts)
+
+    if total > SS_K:
+
+        return None
+
+    run = [None] * RUN
+    pos = 0
+
+    for lane in range(WAVE):
+
+        mask, cb = masks[lane], 0xffff - 4 * lane
+
+        while mask:
+
+            b = (mask & -mask).bit_length() - 1
+            mask &= mask - 1
+            i, hi = b & 15, b >> 4
+            key = keys16[lane][2 * i + hi]
+            j = 2 * i + hi
+            off = (j >> 2) * (256 * 4) + (j & 3)
+            assert pos < RUN
+            run[pos] = ((key << 16) | cb) - off
+            pos += 1
+
+    return run[:pos]
+
+
+@pytest.mark.parametrize("E", [4, 8, 16, 32])
+def test_masked_survivors_are_the_keys_above_the_threshold(E):
+
+    rng = np.random.default_rng(100 + E)
+
+    for trial in range(200):
+
+        keys = rng.integers(0x7000, 0x9000, (WAVE, E)).tolist()
+        T = int(np.sort(np.array(keys).ravel())[-rng.integers(1, 150)])
+        run = masked_survivors(keys, T)
+        expected = sorted(((k << 16) | (0xffff - ((j >> 2) * 1024 + 4 * lane + (j & 3))))
+                          for lane in range(WAVE) for j, k in enumerate(keys[lane]) if k > T)
+
+        if len(expected) > SS_K:
+
+            assert run is None
+            continue
+
+        assert sorted(run) == expected

@@ -1,12 +1,24 @@
-"""Pure-torch sampling and verification over a ``SamplingBuffers`` (reference
-``core/naive.py:53-708``).
+"""Pure-PyTorch sampler over a ``SamplingBuffers``: the public ``sonic_sampler.core.NaiveSampler``
+(the reference exports a class of this name from ``core/naive.py:53-708`` for validation).
 
-This is the reference's validation API: the same processors, truncations, Gumbel-max selection
-and chain verification written as whole-batch torch operations, runnable on any device. As in the
-reference, a processor runs for the whole batch when any row's indicator enables it (buffers hold
-neutral values for rows that do not), and the bounded path keeps the top-128 of each row. The
-bounded top-128 is taken with a stable descending sort, so equal values keep the lowest index
-first (the reference's ``topk`` leaves the order of ties unspecified on the CPU).
+The computation is written as three batch stages that any torch device runs:
+
+* ``process`` -- grammar mask, repetition / frequency / presence penalties over the decode counts
+  (plus the drafted history), logit bias and temperature, each rounded to bf16 where the
+  reference's PyTorch path rounds, and each applied only to the rows whose indicator word enables
+  it (the reference enables a processor for the whole batch when any row asks for it, which gives
+  the same result when disabled rows hold neutral parameters);
+* ``candidates`` -- each row's 128 largest values by a stable descending sort (equal values keep
+  the lowest index first), then top-k, top-p and min-p in that order, each on the values the
+  previous one left;
+* ``select`` (one step: Gumbel-max over ``bf16(v - w)``, greedy rows by argmax) and ``verify``
+  (chain verification: accept draft i while ``bf16(u_i q_i(d_i)) <= p_i(d_i)``, resample the first
+  rejection from ``max(p - q, 0)``, or emit the bonus token after the last step).
+
+Where the reference disagrees with itself, this class follows the semantics of the fused kernels:
+greedy rows take the argmax of the processed logits, ``prefill=False`` reads the draft scope (the
+draft indicators and noise, as ``UnshardedFusedSingular.drafting`` does), and the top-128 ties go to
+the lowest index.
 """
 
 from __future__ import annotations
@@ -30,7 +42,6 @@ from sonic_sampler.core.buffer import SamplingBuffers
 from sonic_sampler.core.flags import Indicator
 from sonic_sampler.ops import MAX_K
 
-
 F32 = torch.float32
 I32 = torch.int32
 I64 = torch.int64
@@ -39,399 +50,304 @@ BF16 = torch.bfloat16
 ValueIndices = Tuple[Tensor, Tensor]
 
 
-def softmax(values: Tensor) -> Tuple[Tensor, Tensor]:
-    """(fp32 probabilities, bf16 log-probabilities) via fp32 log_softmax."""
+def _gate(bits: Tensor, flag: int, ndim: int) -> Tensor:
+    """Rows whose indicator word holds `flag`, shaped to broadcast over `ndim` dimensions."""
 
-    logprobs = torch.log_softmax(values, dim=-1, dtype=F32)
-
-    return logprobs.exp(), logprobs.to(BF16)
+    return ((bits & int(flag)) != 0).reshape(-1, *([1] * (ndim - 1)))
 
 
-def subset_select(values: Tensor, mapping: Optional[Tensor], dim: int = -1) -> Tensor:
+def _through(values: Tensor, mapping: Optional[Tensor]) -> Tensor:
+    """Target-vocabulary state seen through a draft -> target map (identity without one)."""
 
-    return values if mapping is None else values.index_select(dim, mapping)
-
-
-def remap(indices: Tensor, mapping: Optional[Tensor]) -> Tensor:
-
-    if mapping is None:
-
-        return indices
-
-    return mapping.gather(0, indices.flatten().to(I64)).reshape_as(indices)
+    return values if mapping is None else values.index_select(-1, mapping)
 
 
-@dataclass(eq=False)
+def _log_softmax(values: Tensor) -> Tuple[Tensor, Tensor]:
+    """fp32 (probabilities, log-probabilities) of bf16 values."""
+
+    logp = torch.log_softmax(values, dim=-1, dtype=F32)
+
+    return logp.exp(), logp
+
+
+@dataclass
 class NaiveSampler:
 
+    # The buffers every call reads: indicators, processor parameters, counts and noise.
     buffers: SamplingBuffers
+
+    # Keep each row's top-128 (True) or its full sorted row (False) as the candidate set.
     bounded: bool = True
+
+    # Top-k log-probabilities returned per row (Z).
     max_top_logprobs: int = DEFAULT_TOP_LOGPROBS
 
-    def is_enabled(self, flag: Indicator) -> bool:
+    # ---- indicator words ---------------------------------------------------------------------
 
-        return any(flag & value for value in self.buffers.indicators.target)
+    def _bits(self, scope: str, rows: int, device) -> Tensor:
 
-    @property
-    def is_greedy(self) -> bool:
+        words = getattr(self.buffers.flags.indicators, scope)
 
-        return self.buffers.flags.all_greedy
+        return torch.tensor([int(w) for w in words[:rows]], dtype=I64, device=device)
 
-    @property
-    def has_ordering(self) -> bool:
+    # ---- stage 1: logit processors --------------------------------------------------------------
 
-        return self.is_enabled(Indicator.cumulative())
+    def process(self, logits: Tensor, bits: Tensor, *, step: Optional[int] = None,
+                history: Optional[Tensor] = None, mapping: Optional[Tensor] = None) -> Tensor:
+        """Processed bf16 logits of [B, V] (one step, grammar row `step`) or [B, T, V] (chain,
+        grammar rows 0..T-1). `history` is [B, H] drafted tokens: a one-step call counts all of
+        them, a chain counts tokens[:, :i] at step i; token 0 never counts."""
 
-    @property
-    def return_top_logprobs(self) -> bool:
+        b = self.buffers
+        x = logits.to(BF16).clone()
+        chain = x.dim() == 3
+        nd = x.dim()
+        vocab = x.size(-1)
 
-        return self.max_top_logprobs > 0 and self.is_enabled(Indicator.TOP_K_LOGPROBS)
+        if bool((bits & Indicator.GRAMMAR).any()):
 
-    def grammar(self, logits: Tensor, bitmask: Tensor, mapping: Optional[Tensor] = None) -> Tensor:
+            words = b.grammar.view(I32)
+            words = words[:, :x.size(1)] if chain else words[:, step or 0]
+            allowed = (words[..., None].bitwise_right_shift(torch.arange(32, device=x.device, dtype=I32)) & 1)
+            allowed = _through(allowed.flatten(-2)[..., :b.repetition.counts.decode.size(-1)], mapping)[..., :vocab]
+            x = x.masked_fill(_gate(bits, Indicator.GRAMMAR, nd) & (allowed == 0), -inf)
 
-        if self.is_enabled(Indicator.GRAMMAR):
+        penalties = Indicator.MULTIPLICATIVE | Indicator.FREQUENCY | Indicator.PRESENCE
 
-            shifts = torch.arange(32, dtype=I32, device=logits.device)
-            bits = (bitmask.view(I32)[..., None] >> shifts).flatten(-2)[..., : self.buffers.vocab_size]
-            denied = (subset_select(bits, mapping) & 1) == 0
-            logits.masked_fill_(denied, -inf)
+        if bool((bits & penalties).any()):
 
-        return logits
+            rep = b.repetition
+            decode = rep.counts.decode[:x.size(0)]
+            own = decode[:, :1].clone()
 
-    def repetition(self, logits: Tensor, timestep: Optional[int] = None,
-                   tokens: Optional[Tensor] = None, mapping: Optional[Tensor] = None) -> Tensor:
+            if history is not None and history.numel():
 
-        if not self.is_enabled(Indicator.repetition()):
+                ones = torch.ones_like(history, dtype=decode.dtype)
 
-            return logits
+                if chain:
 
-        counts = self.buffers.repetition.counts
-        context, decode = counts.context, counts.decode
-        original = decode[..., 0].clone()
-        row_dims = (None,) * (logits.dim() - 1)
+                    # step i adds the drafts of steps < i (zero padding lands on token 0)
+                    steps = x.size(1)
+                    mask = torch.ones(steps, history.size(1), dtype=torch.bool, device=x.device).tril(-1)
+                    earlier = history[:, None, :].expand(-1, steps, -1).masked_fill(~mask, 0).to(I64)
+                    decode = decode[:, None].expand(-1, steps, -1).scatter_add(-1, earlier, ones[:, None].expand_as(earlier))
 
-        if tokens is not None:
+                else:
 
-            size, steps = tokens.shape
-            history = tokens[:, None].expand(-1, steps, steps).tril(diagonal=-1).to(I64)
+                    decode = decode.scatter_add(-1, history.to(I64), ones)
 
-            if timestep is None:
+                decode[..., :1] = own[:, None] if chain else own
 
-                decode = decode[:, None].expand(size, steps, -1).scatter_add(
-                    -1, history, torch.ones_like(history, dtype=I32))
-                context = context[:, None]
+            elif chain:
 
-            else:
+                decode = decode[:, None].expand(-1, x.size(1), -1)
 
-                decode = decode.scatter_add(-1, history[:, timestep], torch.ones_like(tokens, dtype=I32))
+            decode = _through(decode, mapping)[..., :vocab]
+            per_row = lambda t: t[:x.size(0)].reshape(-1, *([1] * (nd - 1)))  # noqa: E731
 
-            decode[..., 0].copy_(original[(slice(None),) + (None,) * (decode.dim() - 2)].expand_as(decode[..., 0]))
+            if bool((bits & Indicator.MULTIPLICATIVE).any()):
 
-        decode = subset_select(decode, mapping)
-        penalties = self.buffers.repetition
+                context = rep.counts.context[:x.size(0)]
+                context = _through(context[:, None] if chain else context, mapping)[..., :vocab]
+                seen = (context + decode) > 0
+                factor = per_row(rep.multiplicative).expand_as(x).masked_fill(~seen, 1.0)
+                scaled = torch.where(x < 0, x * factor, x / factor)
+                x = torch.where(_gate(bits, Indicator.MULTIPLICATIVE, nd), scaled, x)
 
-        if self.is_enabled(Indicator.MULTIPLICATIVE):
+            if bool((bits & Indicator.FREQUENCY).any()):
 
-            total = subset_select(context, mapping) + decode
-            scales = (
-                penalties.multiplicative[(slice(None), *row_dims)]
-                .expand_as(logits)
-                .masked_fill(total <= 0, 1.0)
-            )
-            logits = torch.where(logits < 0, logits * scales, logits / scales)
+                x = torch.where(_gate(bits, Indicator.FREQUENCY, nd),
+                                x.addcmul(decode, per_row(rep.frequency), value=-1), x)
 
-        if self.is_enabled(Indicator.FREQUENCY):
+            if bool((bits & Indicator.PRESENCE).any()):
 
-            logits.addcmul_(decode, penalties.frequency[(slice(None), *row_dims)], value=-1)
+                x = torch.where(_gate(bits, Indicator.PRESENCE, nd),
+                                x.addcmul(decode > 0, per_row(rep.presence), value=-1), x)
 
-        if self.is_enabled(Indicator.PRESENCE):
+        if bool((bits & Indicator.BIAS).any()):
 
-            logits.addcmul_(decode > 0, penalties.presence[(slice(None), *row_dims)], value=-1)
+            bias = _through(b.bias[:x.size(0)], mapping)[..., :vocab]
+            x = torch.where(_gate(bits, Indicator.BIAS, nd), x + (bias[:, None] if chain else bias), x)
 
-        return logits
+        if bool((bits & Indicator.TEMPERATURE).any()):
 
-    def bias(self, logits: Tensor, mapping: Optional[Tensor] = None) -> Tensor:
+            t = b.temperature[:x.size(0)].reshape(-1, *([1] * (nd - 1)))
+            x = torch.where(_gate(bits, Indicator.TEMPERATURE, nd), x / t, x)
 
-        if self.is_enabled(Indicator.BIAS):
+        return x
 
-            extra = (None,) * (logits.dim() - 2)
-            logits.add_(subset_select(self.buffers.bias, mapping)[(slice(None), *extra)])
+    # ---- stage 2: candidates and truncation -----------------------------------------------------
 
-        return logits
+    def candidates(self, x: Tensor, bits: Tensor) -> ValueIndices:
+        """Each row's candidates (values desc, ties to the lowest index) truncated by top-k, then
+        top-p (fp32 softmax, cumulative sum > p masked, position 0 kept), then min-p (bf16
+        softmax below bf16(min_p * max) masked)."""
 
-    def temperature(self, logits: Tensor) -> Tensor:
+        b = self.buffers
+        nd = x.dim()
+        values, indices = x.sort(dim=-1, stable=True, descending=True)
 
-        if self.is_enabled(Indicator.TEMPERATURE):
+        if self.bounded:
 
-            logits.div_(self.buffers.temperature[(slice(None),) + (None,) * (logits.dim() - 1)])
+            values, indices = values[..., :MAX_K].contiguous(), indices[..., :MAX_K]
 
-        return logits
+        per_row = lambda t: t[:x.size(0)].reshape(-1, *([1] * (nd - 1)))  # noqa: E731
+        position = torch.arange(values.size(-1), device=x.device, dtype=I32)
+        values = values.masked_fill(_gate(bits, Indicator.TOP_K, nd) & (position >= per_row(b.top_k)), -inf)
 
-    def top_k(self, values: Tensor) -> Tensor:
+        if bool((bits & Indicator.TOP_P).any()):
 
-        if self.is_enabled(Indicator.TOP_K):
+            over = values.softmax(dim=-1, dtype=F32).cumsum(dim=-1) > per_row(b.top_p)
+            over[..., 0] = False
+            values = values.masked_fill(_gate(bits, Indicator.TOP_P, nd) & over, -inf)
 
-            width = values.size(-1)
-            mask = torch.arange(width, dtype=I32, device=values.device)[None] >= self.buffers.top_k[:, None]
-            values.masked_fill_(mask[(slice(None),) + (None,) * (values.dim() - 2)], -inf)
-
-        return values
-
-    def top_p(self, values: Tensor) -> Tensor:
-
-        if self.is_enabled(Indicator.TOP_P):
-
-            upper = self.buffers.top_p[(slice(None),) + (None,) * (values.dim() - 1)]
-            mask = values.softmax(dim=-1, dtype=F32).cumsum_(dim=-1).gt(upper)
-            mask[..., 0] = False
-            values.masked_fill_(mask, -inf)
-
-        return values
-
-    def min_p(self, values: Tensor) -> Tensor:
-
-        if self.is_enabled(Indicator.MIN_P):
+        if bool((bits & Indicator.MIN_P).any()):
 
             scores = values.softmax(dim=-1)
-            lower = self.buffers.min_p[(slice(None),) + (None,) * (values.dim() - 1)].mul(scores[..., :1])
-            values.masked_fill_(scores < lower, -inf)
+            floor = per_row(b.min_p) * scores[..., :1]
+            values = values.masked_fill(_gate(bits, Indicator.MIN_P, nd) & (scores < floor), -inf)
 
-        return values
+        return values, indices.to(I32)
 
-    def cumulative(self, logits: Tensor) -> Optional[ValueIndices]:
+    # ---- stage 3a: one-step selection ----------------------------------------------------------
 
-        if self.is_greedy:
+    def select(self, x: Tensor, bits: Tensor, noise: Tensor, cand: ValueIndices,
+               mapping: Optional[Tensor], logprobs: bool, probs: bool) -> Selection:
+        """Gumbel-max over bf16(v - w) on the candidates (first position on ties); greedy rows
+        take the processed argmax. Noise and probabilities live in the target vocabulary."""
 
-            return None
+        values, indices = cand
+        rows = x.size(0)
+        greedy = (bits & Indicator.GREEDY) != 0
+        targets = indices.to(I64) if mapping is None else mapping.to(I64)[indices.to(I64)]
 
-        if self.bounded or self.has_ordering:
+        pick = (values - noise.gather(-1, targets)).argmax(dim=-1, keepdim=True)
+        argmax = x.argmax(dim=-1, keepdim=True)
+        argmax = argmax if mapping is None else mapping.to(I64)[argmax]
+        tokens = torch.where(greedy[:, None], argmax, targets.gather(-1, pick)).to(I32)
 
-            values, indices = logits.sort(dim=-1, stable=True, descending=True)
+        scores, logp = _log_softmax(values)
+        probabilities = None
 
-            if self.bounded:
+        if probs:
 
-                values, indices = values[..., :MAX_K].contiguous(), indices[..., :MAX_K]
+            probabilities = torch.zeros_like(self.buffers.weights.gumbel.target[:rows, 0])
+            stochastic = ~greedy
+            probabilities[stochastic] = probabilities[stochastic].scatter(
+                -1, targets[stochastic], scores[stochastic].to(BF16))
+            probabilities[greedy, argmax[greedy, 0]] = 1.0
 
-            values = self.min_p(self.top_p(self.top_k(values)))
+        log_probs = None
 
-            return values, indices.to(I32)
+        if logprobs:
 
-        return None
+            # with probabilities: log_softmax; without: v - logsumexp(v) (two fp32 roundings apart)
+            shifted = logp if probs else values.to(F32) - values.to(F32).logsumexp(dim=-1, keepdim=True)
+            selected = torch.where(greedy[:, None], 0.0, shifted.gather(-1, pick))
+            top = None
 
-    def probabilities(self, values: Tensor, indices: Optional[Tensor] = None,
-                      mapping: Optional[Tensor] = None) -> Tensor:
+            if self.max_top_logprobs > 0 and bool(((bits & Indicator.TOP_K_LOGPROBS) != 0).any()):
 
-        base = torch.zeros_like(self.buffers.weights.gumbel.target[:, 0])
+                z = self.max_top_logprobs
+                top = TopTargets(tokens=targets[:, :z].to(I32), logprobs=shifted[:, :z].to(BF16))
 
-        if indices is None:
-
-            return values if mapping is None else base.index_copy_(-1, mapping, values)
-
-        return base.scatter_(-1, remap(indices, mapping).to(I64), values)
-
-    def selection(self, logits: Tensor, weights: Tensor, pair: Optional[ValueIndices] = None,
-                  mapping: Optional[Tensor] = None, logprobs: bool = False,
-                  probs: bool = False) -> Selection:
-
-        log_probs = top = probabilities = None
-
-        if self.is_greedy:
-
-            tokens = remap(logits.argmax(dim=-1, keepdim=True), mapping).to(I32)
-
-            if logprobs:
-
-                log_probs = LogProbabilities(selected=logits.new_zeros(tokens.shape))
-
-            if probs:
-
-                probabilities = self.probabilities(logits.new_ones(tokens.shape), indices=tokens)
-
-        elif pair is None:
-
-            targets = (logits - subset_select(weights, mapping)).argmax(dim=-1, keepdim=True)
-            tokens = remap(targets, mapping).to(I32)
-
-            if probs:
-
-                scores, log_scores = softmax(logits)
-
-                if logprobs:
-
-                    selected = log_scores.gather(-1, targets)
-
-                    if self.return_top_logprobs:
-
-                        v, i = log_scores.topk(k=self.max_top_logprobs, dim=-1)
-                        top = TopTargets(tokens=remap(i, mapping).to(I32), logprobs=v)
-
-                    log_probs = LogProbabilities(selected=selected, top_k=top)
-
-                probabilities = self.probabilities(scores, mapping=mapping)
-
-            elif logprobs:
-
-                lse = logits.logsumexp(dim=-1, keepdim=True)
-                selected = logits.gather(-1, targets).sub_(lse)
-
-                if self.return_top_logprobs:
-
-                    v, i = logits.topk(k=self.max_top_logprobs, dim=-1)
-                    top = TopTargets(tokens=remap(i, mapping).to(I32), logprobs=v.sub_(lse))
-
-                log_probs = LogProbabilities(selected=selected, top_k=top)
-
-        else:
-
-            values, indices = pair
-            indices = remap(indices, mapping)
-            targets = (values - weights.gather(-1, indices.to(I64))).argmax(dim=-1, keepdim=True)
-            tokens = indices.gather(-1, targets).to(I32)
-            z = self.max_top_logprobs
-
-            if probs:
-
-                scores, log_scores = softmax(values)
-
-                if logprobs:
-
-                    selected = log_scores.gather(-1, targets)
-
-                    if self.return_top_logprobs:
-
-                        top = TopTargets(tokens=indices[:, :z].to(I32), logprobs=log_scores[:, :z])
-
-                    log_probs = LogProbabilities(selected=selected, top_k=top)
-
-                probabilities = self.probabilities(scores.to(BF16), indices=indices)
-
-            elif logprobs:
-
-                lse = values.to(F32).logsumexp(dim=-1, keepdim=True)
-                selected = values.gather(-1, targets).sub_(lse)
-
-                if self.return_top_logprobs:
-
-                    top = TopTargets(tokens=indices[:, :z].to(I32), logprobs=values[:, :z].sub_(lse))
-
-                log_probs = LogProbabilities(selected=selected, top_k=top)
+            log_probs = LogProbabilities(selected=selected.to(BF16), top_k=top)
 
         return Selection(tokens=tokens, probabilities=probabilities, logprobs=log_probs)
 
-    def verification(self, logits: Tensor, weights: Tensor, tokens: Tensor, probs: Tensor,
-                     pair: Optional[ValueIndices] = None, logprobs: bool = False) -> Verification:
+    # ---- stage 3b: chain verification ----------------------------------------------------------
 
-        log_probs = top = None
-        tokens64 = tokens.to(I64)
+    def verify(self, x: Tensor, bits: Tensor, tokens: Tensor, q: Tensor, cand: ValueIndices,
+               logprobs: bool) -> Verification:
+        """Greedy rows: accept while the processed argmax equals the draft. Stochastic rows:
+        accept step i while bf16(u_i q_i(d_i)) <= p_i(d_i) (p over the candidates, 0 outside),
+        resample the first rejection j from argmax log(max(p_j - q_j, 0)) - w_j, or after the last
+        draft take argmax log p - w at the bonus step. Returns the drafts with the correction or
+        bonus written at `offsets`."""
 
-        if self.is_greedy:
+        b = self.buffers
+        values, indices = cand
+        batch, steps = tokens.shape
+        drafts = tokens.to(I64)
+        last = torch.arange(steps, device=x.device) == steps - 1
+        greedy = (bits & Indicator.GREEDY) != 0
 
-            selections = logits.argmax(dim=-1).to(tokens.dtype)
-            acceptances = selections == tokens
-            acceptances[:, -1] = False
-            offsets = acceptances.int().argmin(dim=-1, keepdim=True)
+        # greedy chains
+        argmax = x.argmax(dim=-1)
+        g_accept = (argmax == drafts) & ~last
 
-            if logprobs:
+        # stochastic chains
+        scores, logp = _log_softmax(values)
+        hit = indices.to(I64) == drafts[..., None]
+        where = hit.int().argmax(dim=-1, keepdim=True)
+        p_draft = scores.gather(-1, where)[..., 0].masked_fill(~hit.any(dim=-1), 0.0)
+        q_draft = (q.gather(-1, drafts[..., None])[..., 0] * b.weights.uniform[:batch, :steps])
+        s_accept = (q_draft <= p_draft) & ~last
 
-                log_probs = LogProbabilities(selected=logits.new_zeros(tokens.shape))
+        accept = torch.where(greedy[:, None], g_accept, s_accept)
+        offsets = accept.int().argmin(dim=-1, keepdim=True)                       # first rejection
+        j = offsets[:, 0]
+        rows = torch.arange(batch, device=x.device)
 
-        elif pair is None:
+        cand_j = indices[rows, j].to(I64)                                          # [B, 128]
+        residual = (scores[rows, j] - q[rows, j].gather(-1, cand_j).to(F32)).clamp_min(0)
+        noise = b.weights.gumbel.target[:batch].to(x.device)[rows, j].gather(-1, cand_j)
+        pick = (residual.log() - noise.to(F32)).argmax(dim=-1)
+        resampled = cand_j.gather(-1, pick[:, None])[:, 0]
+        correction = torch.where(greedy, argmax[rows, j], resampled)
 
-            scores, log_scores = softmax(logits)
-            drafted = tokens64[..., None]
-            acceptances = (
-                probs.gather(-1, drafted)
-                .mul_(self.buffers.weights.uniform[..., None])
-                .le(scores.gather(-1, drafted))
-                .squeeze(-1)
-            )
-            acceptances[:, -1] = False
-            offsets = acceptances.int().argmin(dim=-1, keepdim=True)
-            rejected = offsets[..., None].expand(-1, 1, logits.size(-1)).to(I64)
-            sampled = (
-                scores.gather(1, rejected).sub_(probs.gather(1, rejected)).squeeze_(1)
-                .clamp_min_(0).log_().sub_(weights.gather(1, rejected).squeeze_(1))
-                .argmax(dim=-1, keepdim=True)
-            )
-            selections = tokens.scatter(-1, offsets.to(I64), sampled.to(tokens.dtype))
+        out = tokens.clone()
+        out[rows, j] = correction.to(out.dtype)
+        log_probs = None
 
-            if logprobs:
+        if logprobs:
 
-                selected = log_scores.gather(-1, selections.to(I64)[..., None]).squeeze_(-1)
+            position = where[..., 0].clone()
+            position[rows, j] = pick
+            selected = logp.gather(-1, position[..., None])[..., 0]
+            selected = torch.where(greedy[:, None], 0.0, selected)
+            top = None
 
-                if self.return_top_logprobs:
+            if self.max_top_logprobs > 0 and bool(((bits & Indicator.TOP_K_LOGPROBS) != 0).any()):
 
-                    v, i = log_scores.topk(k=self.max_top_logprobs, dim=-1)
-                    top = TopTargets(tokens=i.to(I32), logprobs=v)
+                z = self.max_top_logprobs
+                top = TopTargets(tokens=indices[..., :z], logprobs=logp[..., :z].to(BF16))
 
-                log_probs = LogProbabilities(selected=selected, top_k=top)
+            log_probs = LogProbabilities(selected=selected.to(BF16), top_k=top)
 
-        else:
+        return Verification(tokens=out, offsets=offsets.to(I32), logprobs=log_probs)
 
-            values, indices = pair
-            scores, log_scores = softmax(values)
-            drafted = tokens64[..., None]
-            matches = indices.to(I64) == drafted
-            positions = matches.int().argmax(dim=-1, keepdim=True)
-            targets = scores.gather(-1, positions).squeeze(-1).masked_fill_(~matches.any(dim=-1), 0)
-            acceptances = (
-                probs.gather(-1, drafted).squeeze(-1)
-                .mul_(self.buffers.weights.uniform)
-                .le(targets)
-            )
-            acceptances[:, -1] = False
-            offsets = acceptances.int().argmin(dim=-1, keepdim=True)
-            rejected = offsets[..., None].expand(-1, 1, MAX_K).to(I64)
-            candidates = indices.gather(1, rejected).squeeze_(1).to(I64)
-            nested = offsets.to(I64) * probs.size(-1) + candidates
-            marginals = probs.flatten(1, 2).gather(-1, nested)
-            sampled = (
-                scores.gather(1, rejected).squeeze_(1).sub_(marginals).clamp_min_(0).log_()
-                .sub_(weights.flatten(1, 2).gather(-1, nested))
-                .argmax(dim=-1, keepdim=True)
-            )
-            chosen = candidates.gather(-1, sampled).to(tokens.dtype)
-            selections = tokens.scatter(-1, offsets.to(I64), chosen)
-
-            if logprobs:
-
-                positions = positions.squeeze(-1).scatter(-1, offsets.to(I64), sampled).unsqueeze(-1)
-                selected = log_scores.gather(-1, positions).squeeze_(-1)
-
-                if self.return_top_logprobs:
-
-                    z = self.max_top_logprobs
-                    top = TopTargets(tokens=indices[..., :z].to(I32), logprobs=log_scores[..., :z])
-
-                log_probs = LogProbabilities(selected=selected, top_k=top)
-
-        return Verification(tokens=selections, offsets=offsets.to(I32), logprobs=log_probs)
-
-    def preamble(self, logits: Tensor, tokens: Optional[Tensor] = None,
-                 timestep: Optional[int] = None, mapping: Optional[Tensor] = None):
-
-        grammar = self.buffers.grammar if timestep is None else self.buffers.grammar[:, timestep]
-        drafted = None if timestep == 0 else tokens
-
-        masked = self.grammar(logits, grammar, mapping)
-        penalized = self.repetition(masked, timestep=timestep, tokens=drafted, mapping=mapping)
-
-        return self.cumulative(self.temperature(self.bias(penalized, mapping)))
+    # ---- entry points (reference signatures) ----------------------------------------------------
 
     def singular(self, logits: Tensor, tokens: Optional[Tensor], timestep: int, *,
                  mapping: Optional[Tensor] = None, prefill: bool = False, logprobs: bool = False,
                  probs: bool = False) -> Selection:
+        """One step over [B, V] logits: the target scope and noise with ``prefill``, otherwise the
+        draft scope with ``tokens[:, :timestep]`` as extra history and the draft noise of
+        ``timestep``; ``mapping`` is the draft -> target (d2t) map."""
 
-        pair = self.preamble(logits, tokens=tokens, timestep=timestep, mapping=mapping)
-        noise = self.buffers.weights.gumbel.target if prefill else self.buffers.weights.gumbel.draft
+        scope = "target" if prefill else "draft"
+        bits = self._bits(scope, logits.size(0), logits.device)
+        history = None if (tokens is None or timestep == 0) else tokens[:, :timestep]
+        x = self.process(logits, bits, step=timestep, history=history, mapping=mapping)
+        noise = getattr(self.buffers.weights.gumbel, scope)[:logits.size(0), timestep]
+        cand = self.candidates(x, bits)
 
-        return self.selection(logits, noise[:, timestep], pair, mapping, logprobs, probs)
+        return self.select(x, bits, noise.to(BF16), cand, mapping, logprobs, probs)
 
     def multistep(self, logits: Tensor, tokens: Tensor, probs: Tensor, *,
-                  logprobs: bool = False):
+                  logprobs: bool = False) -> Tuple[Verification, Optional[ValueIndices]]:
+        """Chain verification of [B, gamma + 1, V] logits against [B, gamma + 1] drafts with draft
+        probabilities [B, gamma (+ 1), V]; returns the verification and each row's candidates."""
 
-        pair = self.preamble(logits, tokens=tokens)
-        verification = self.verification(logits, self.buffers.weights.gumbel.target, tokens,
-                                         probs, pair, logprobs)
+        bits = self._bits("target", logits.size(0), logits.device)
+        x = self.process(logits, bits, history=tokens)
+        cand = self.candidates(x, bits)
+        steps = tokens.size(1)
 
-        return verification, pair
+        if probs.size(1) < steps:
+
+            pad = probs.new_zeros(probs.size(0), steps - probs.size(1), probs.size(2))
+            probs = torch.cat([probs, pad], dim=1)
+
+        return self.verify(x, bits, tokens, probs, cand, logprobs), cand

@@ -602,3 +602,72 @@ def test_logprob_tolerance_floor():
     # away from 0 the relative band governs
     assert oracle.bf16_within(-3.0, -3.0000001, floor=oracle.LOGPROB_FLOOR)
     assert not oracle.bf16_within(-3.015625, -3.0, floor=oracle.LOGPROB_FLOOR)
+
+
+@pytest.mark.parametrize("seed", [3, 4])
+def test_naive_drafting_with_d2t_matches_per_row(seed):
+
+    from sonic_sampler.core import NaiveSampler
+    from sonic_sampler.core.buffer import SamplingBuffers
+
+    rows, gamma, t, vd, vt = 6, 3, 2, 1024, 4096
+    g = torch.Generator().manual_seed(seed)
+    b = SamplingBuffers.random(size=rows, timesteps=gamma + 1, vocab_size=vt, device="cpu", seed=seed,
+                               max_top_logprobs=5)
+    d2t = torch.randperm(vt, generator=g)[:vd]
+    logits = (torch.randn(rows, vd, generator=g) * 3).to(BF16)
+    tokens = torch.randint(1, vt, (rows, gamma + 1), generator=g).to(I32)
+
+    got = NaiveSampler(buffers=b, max_top_logprobs=5).singular(logits, tokens, t, mapping=d2t, probs=True)
+    st = oracle.State.from_buffers(b)
+    res = oracle.singular(logits, st, scope="draft", timestep=t, d2t=d2t, drafted=tokens, history=t,
+                          probs=True, max_top_logprobs=5)
+    assert got.tokens[:, 0].tolist() == [r.token for r in res]
+
+    for r, rec in enumerate(res):
+
+        if rec.probs:
+
+            for tok, v in rec.probs.items():
+
+                assert float(got.probabilities[r, tok]) == float(torch.tensor(v).to(BF16))
+
+
+@pytest.mark.parametrize("indicator", [None, 0x041, 0x4A0, 0x5BE])
+def test_naive_multistep_matches_per_row(indicator):
+
+    from sonic_sampler.core import NaiveSampler
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Indicator
+
+    batch, gamma, vocab = 5, 3, 2048
+    n = gamma + 1
+    seed = 9 if indicator is None else indicator
+    g = torch.Generator().manual_seed(seed)
+    b = SamplingBuffers.random(size=batch, timesteps=n, vocab_size=vocab, device="cpu", seed=seed,
+                               indicators=None if indicator is None else Indicator(indicator),
+                               max_top_logprobs=4)
+    logits = (torch.randn(batch, n, vocab, generator=g) * 3).to(BF16)
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch, n, generator=g) < 0.6, argmax,
+                          torch.randint(1, vocab, (batch, n), generator=g)).to(I32)
+    q = torch.softmax(torch.randn(batch, gamma, vocab, generator=g) * 2, dim=-1).to(BF16)
+
+    ver, _ = NaiveSampler(buffers=b, max_top_logprobs=4).multistep(logits, drafted, q, logprobs=True)
+    st = oracle.State.from_buffers(b)
+    res = oracle.multistep(logits.view(batch * n, vocab), st, drafted.view(-1), list(range(0, batch * n + 1, n)),
+                           probabilities=q, logprobs=True, max_top_logprobs=4)
+
+    for r, rec in enumerate(res):
+
+        if rec.knife:
+
+            continue
+
+        off = int(ver.offsets[r, 0])
+        assert off == rec.offset, (r, off, rec.offset)
+        assert ver.tokens[r, :off + 1].tolist() == rec.tokens
+
+        for i, lp in enumerate(rec.logprobs):
+
+            assert oracle.bf16_within(float(ver.logprobs.selected[r, i]), lp, floor=oracle.LOGPROB_FLOOR)

@@ -75,6 +75,16 @@ typedef struct ss_philox {
     int32_t enabled;
 } ss_philox;
 
+/* Kernel layout of ss_fused_singular and ss_topk. TILES: a tile grid (rows x tiles) writes every tile's
+ * top-128 to the scratchpad, then one workgroup per row merges and selects (two launches).
+ * ROWWISE: one workgroup per row streams the row tile by tile and selects in the same launch
+ * (rows of at most 16 tiles; the scratchpad is not touched). AUTO currently picks TILES. */
+typedef enum ss_strategy {
+    SS_STRATEGY_AUTO = 0,
+    SS_STRATEGY_TILES = 1,
+    SS_STRATEGY_ROWWISE = 2
+} ss_strategy;
+
 /* ---------------------------------------------------------------------------------------------
  * Bounded top-k over [rows, vocab] logits, ties broken to the lowest index.
  * Replaces UnshardedBoundedTopK.__call__ (reference interface/topk.py:98-161).
@@ -89,7 +99,7 @@ typedef struct ss_topk_args {
     int32_t vocab_size;
     int32_t k;           /* power of two, 1 <= k <= 128 */
     int32_t block_n;     /* tile width: 1024, 2048, 4096 or 8192 */
-    int32_t reserved;
+    int32_t strategy;    /* ss_strategy: 0 automatic (tile grid), 2 one workgroup per row (V <= 32768) */
     void *scratch;       /* rows * stride_scratch elements (uint32 or uint64) */
     int64_t stride_scratch;
     void *values;        /* [rows, k] bf16 or fp32 */
@@ -98,16 +108,6 @@ typedef struct ss_topk_args {
 } ss_topk_args;
 
 int ss_topk(const ss_topk_args *args);
-
-/* Kernel layout of ss_fused_singular. TILES: a tile grid (rows x tiles) writes every tile's
- * top-128 to the scratchpad, then one workgroup per row merges and selects (two launches).
- * ROWWISE: one workgroup per row streams the row tile by tile and selects in the same launch
- * (rows of at most 16 tiles; the scratchpad is not touched). AUTO currently picks TILES. */
-typedef enum ss_strategy {
-    SS_STRATEGY_AUTO = 0,
-    SS_STRATEGY_TILES = 1,
-    SS_STRATEGY_ROWWISE = 2
-} ss_strategy;
 
 /* ---------------------------------------------------------------------------------------------
  * Fused single-step sampling: logit processors -> bounded top-128 -> truncation -> Gumbel-max,

@@ -6,7 +6,7 @@
 // Merge stage, grid rows: selects the row's top-k among the tiles * k candidates, sorts them by
 // (value desc, column asc) with a wave64 bitonic network and writes values / indices densely as
 // [rows, k].
-#include "ss_select.h"
+#include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
 
 namespace ss {
@@ -44,43 +44,6 @@ struct TopkTraits<true> {
     __device__ static uint32_t cand_key(Cand c) { return (uint32_t)(c >> 32); }
     __device__ static int cand_li(Cand c) { return (int)(c & 0xffffffffu); }
 };
-
-// Tile stage: grid rows * tiles.
-template <bool F32, int E>
-__global__ __launch_bounds__(SS_BLOCK) void topk_tiles_kernel(ss_topk_args a, int tiles) {
-    using Tr = TopkTraits<F32>;
-    using Cand = typename Tr::Cand;
-    constexpr int CH = 4;
-    __shared__ TopkSmem sm;
-
-    const int row = blockIdx.x / tiles;
-    const int tile = blockIdx.x - row * tiles;
-    const int V = a.vocab_size;
-    const int k = a.k;
-    const int64_t base = (int64_t)row * a.stride_logits;
-    const int col0 = tile * a.block_n;
-
-    // ---- tile stage ---------------------------------------------------------------------------
-    uint32_t keys[E];
-#pragma unroll
-    for (int j = 0; j < E; ++j) {
-        const int li = order_pos<E, CH>(0, j);
-        const int col = col0 + li;
-        keys[j] = col < V ? Tr::key_of(a.logits, base + col) : 0u;
-    }
-    auto tile_load = [&](int, uint32_t(&out)[E]) {
-#pragma unroll
-        for (int j = 0; j < E; ++j) out[j] = keys[j];
-    };
-    uint32_t thi, margin;
-    int level;
-    radix_threshold<E, Tr::KEYBITS>(sm.sel, 1, tile_load, (uint32_t)k, thi, level, margin);
-    Cand *scr = (Cand *)a.scratch + (int64_t)row * a.stride_scratch;
-    compact<E, CH>(sm.sel, 1, tile_load, thi, level, margin, [&](uint32_t pos, int, int j) {
-        if (pos < (uint32_t)k) scr[tile * k + (int)pos] = Tr::pack(keys[j], order_pos<E, CH>(0, j));
-    });
-
-}
 
 // Merge stage: grid rows.
 template <bool F32>
@@ -195,17 +158,216 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Block selection: one workgroup holds a block of SS_BLOCK * E columns (E values per thread,
+// element j of thread t at column (j / 4) * 1024 + 4 t + j % 4 of the block, loaded as 16-byte fp32
+// / 8-byte bf16 chunks) and selects its top-k. TILED: the block is tile blockIdx.x % tiles of row
+// blockIdx.x / tiles and its top-k goes to the scratch row as packed candidates for the merge
+// kernel; otherwise the block is the whole row (one launch) and the top-k is the output.
+//
+// Lower bound: every wave sorts its 64 lane maxima; at least k / 4 of its lanes hold a value >= the
+// (k / 4)-th largest of them, so with lo the smallest of the four waves' bounds the row holds at
+// least k values >= lo. The survivors (values >= lo: a few dozen on unstructured rows) are
+// collected per wave by a ballot at each element position, skipped uniformly where no lane of the
+// wave survives, as composites (key32 << 32) | ~column. Every wave sorts its survivors, two rounds
+// of bitonic merges keep the top-128 of the four runs, and the first k are written. A wave with more
+// than 128 survivors (long runs of equal values) sends the row to the exact radix selection.
+// ---------------------------------------------------------------------------------------------
+constexpr int TOPK_ROW_E = 128;  // whole rows of at most SS_BLOCK * 128 = 32768 columns
+
+struct TopkRowSmem {
+    SelectSmem sel;                 // exact fallback
+    uint64_t runs[SS_WAVES][SS_K];  // each wave's survivors, then its sorted run
+    uint64_t cand[SS_K];            // exact fallback: the selected composites
+    uint32_t red[SS_WAVES];
+};
+
+// Order-preserving 32-bit key of a float (-0 and +0 share the key of +0).
+__device__ __forceinline__ uint32_t float_key(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+template <bool F32, bool VEC, int E, bool TILED>
+__global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, int tiles) {
+    __shared__ TopkRowSmem sm;
+    const int row = TILED ? (int)blockIdx.x / tiles : (int)blockIdx.x;
+    const int tile = TILED ? (int)blockIdx.x - row * tiles : 0;
+    const int col0 = tile * a.block_n;  // first column of the block
+    const int V = TILED ? min(a.block_n, a.vocab_size - col0) : a.vocab_size;  // columns of the block
+    const int k = a.k;
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane4 = 4 * (int)threadIdx.x;
+    const int64_t bytes = (int64_t)V * (F32 ? 4 : 2);
+    const char *base = (const char *)a.logits + ((int64_t)row * a.stride_logits + col0) * (F32 ? 4 : 2);
+    const __amdgpu_buffer_rsrc_t rb = row_buffer(base, bytes);
+    // the block's top-k: packed candidates of the merge kernel (tiled) or the row's output
+    auto emit = [&](int e, uint32_t key, int col) {
+        if (TILED) {
+            using Tr = TopkTraits<F32>;
+            typename Tr::Cand *scr = (typename Tr::Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+            // absent elements (key 0) keep key 0 in the 16-bit packing too
+            const uint32_t pk = F32 ? key : key ? key16(__float_as_uint(__uint_as_float(unkey32(key))) >> 16) : 0u;
+            scr[tile * k + e] = Tr::pack(pk, col);
+        } else {
+            const float val = __uint_as_float(unkey32(key));
+            const int64_t o = (int64_t)row * k + e;
+            if (F32) ((float *)a.values)[o] = val;
+            else ((uint16_t *)a.values)[o] = (uint16_t)(__float_as_uint(val) >> 16);
+            a.indices[o] = col < V ? col : V - 1;
+        }
+    };
+
+    // ---- the row, every load issued before any is used; columns past V read -inf -----------------
+    float v[E];
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        const int col = c * (SS_BLOCK * 4) + lane4;
+        uint32_t w[4];
+        if (VEC) {
+            if (F32) {
+                const i32x4 q = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, col * 4, 0, NT));
+                w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+            } else {
+                const u32x2 q = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rb, col * 2, 0, NT));
+                w[0] = q.x << 16; w[1] = q.x & 0xffff0000u; w[2] = q.y << 16; w[3] = q.y & 0xffff0000u;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[i] = F32 ? __builtin_amdgcn_raw_buffer_load_b32(rb, (col + i) * 4, 0, NT)
+                           : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, (col + i) * 2, 0, NT) << 16;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * c + i] = col + i < V ? __uint_as_float(w[i]) : -INFINITY;
+    }
+    auto col_of = [&](int j) { return (j >> 2) * (SS_BLOCK * 4) + lane4 + (j & 3); };
+    auto composite = [&](int j) {
+        return ((uint64_t)float_key(v[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)col_of(j));
+    };
+
+    // ---- lower bound from the waves' sorted lane maxima ------------------------------------------
+    float m = v[0];
+#pragma unroll
+    for (int j = 1; j < E; ++j) m = fmaxf(m, v[j]);
+    uint32_t mk = float_key(m);
+    wave_sort64_desc(mk);
+    const int need = (k + SS_WAVES - 1) / SS_WAVES;
+    if (lane == need - 1) sm.red[wave] = mk;
+    __syncthreads();
+    const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
+    // the float whose key is lo (lo is the key of a lane maximum, so it is a value of the row)
+    const float lo_f = __uint_as_float((lo & 0x80000000u) ? (lo & 0x7fffffffu) : ~lo);
+    __syncthreads();
+
+    // ---- survivors per wave ----------------------------------------------------------------------
+    uint64_t *run = sm.runs[wave];
+    uint32_t cnt = 0;  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const bool p = v[j] >= lo_f;
+        const uint64_t msk = __ballot(p);
+        if (msk) {
+            const uint32_t pos = cnt + mbcnt64(msk);
+            if (p && pos < (uint32_t)SS_K) run[pos] = composite(j);
+            cnt += (uint32_t)__popcll(msk);
+        }
+    }
+    if (lane == 0) sm.red[wave] = cnt;
+    __syncthreads();
+    const bool overflow = max(max(sm.red[0], sm.red[1]), max(sm.red[2], sm.red[3])) > (uint32_t)SS_K ||
+                          V < k;
+    if (!overflow) {
+        uint64_t c0 = 2 * lane < (int)cnt ? run[2 * lane] : 0ull;
+        uint64_t c1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0ull;
+        wave_sort128_desc(c0, c1);
+        run[2 * lane] = c0;
+        run[2 * lane + 1] = c1;
+        __syncthreads();
+        if (wave < 2) {
+            const uint64_t *A = sm.runs[2 * wave], *B = sm.runs[2 * wave + 1];
+            uint64_t x0 = max_u64(A[2 * lane], B[127 - 2 * lane]);
+            uint64_t x1 = max_u64(A[2 * lane + 1], B[126 - 2 * lane]);
+            wave_bitonic128_desc<128>(x0, x1);
+            sm.runs[2 * wave][2 * lane] = x0;
+            sm.runs[2 * wave][2 * lane + 1] = x1;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint64_t f[2];
+            f[0] = max_u64(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
+            f[1] = max_u64(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
+            wave_bitonic128_desc<128>(f[0], f[1]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int e = 2 * lane + i;
+                if (e < k) emit(e, (uint32_t)(f[i] >> 32), (int)(0xffffffffu - (uint32_t)f[i]));
+            }
+        }
+        return;
+    }
+
+    // ---- exact selection over the whole row (ties at the k-th value kept in column order) ---------
+    auto keys_of = [&](int, uint32_t(&out)[E]) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) out[j] = col_of(j) < V ? float_key(v[j]) : 0u;
+    };
+    uint32_t thi, margin;
+    int level;
+    radix_threshold<E, 32>(sm.sel, 1, keys_of, (uint32_t)k, thi, level, margin);
+    compact<E, 4>(sm.sel, 1, keys_of, thi, level, margin, [&](uint32_t pos, int, int j) {
+        if (pos < (uint32_t)k) sm.cand[pos] = col_of(j) < V ? composite(j) : (uint64_t)(0xffffffffu - (uint32_t)col_of(j));
+    });
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t c0 = 2 * lane < k ? sm.cand[2 * lane] : 0ull;
+        uint64_t c1 = 2 * lane + 1 < k ? sm.cand[2 * lane + 1] : 0ull;
+        wave_sort128_desc(c0, c1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 2 * lane + i;
+            const uint64_t c = i ? c1 : c0;
+            if (e < k) emit(e, (uint32_t)(c >> 32), (int)(0xffffffffu - (uint32_t)c));
+        }
+    }
+}
+
+template <bool F32>
+static bool topk_vec(const ss_topk_args *a) {
+    const int esz = F32 ? 4 : 2;
+    return (a->vocab_size % 4) == 0 && (a->stride_logits % 4) == 0 && ((uintptr_t)a->logits % (4 * esz)) == 0;
+}
+
+template <bool F32>
+static int launch_topk_rows(const ss_topk_args *a) {
+    dim3 grid((unsigned)a->rows), block(SS_BLOCK);
+    hipStream_t s = (hipStream_t)a->stream;
+    if (topk_vec<F32>(a)) hipLaunchKernelGGL((topk_block_kernel<F32, true, TOPK_ROW_E, false>), grid, block, 0, s, *a, 1);
+    else hipLaunchKernelGGL((topk_block_kernel<F32, false, TOPK_ROW_E, false>), grid, block, 0, s, *a, 1);
+    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
+}
+
+template <bool F32, bool VEC>
+static int launch_topk_tiles(const ss_topk_args *a, int tiles, dim3 grid, dim3 block, hipStream_t s) {
+    switch (a->block_n) {
+        case 1024: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 4, true>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8, true>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16, true>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32, true>), grid, block, 0, s, *a, tiles); break;
+        default: return SS_ERR_UNSUPPORTED;
+    }
+    return SS_OK;
+}
+
 template <bool F32>
 static int launch_topk(const ss_topk_args *a, int tiles) {
     dim3 grid((unsigned)(a->rows * tiles)), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
-    switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((topk_tiles_kernel<F32, 4>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((topk_tiles_kernel<F32, 8>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((topk_tiles_kernel<F32, 16>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((topk_tiles_kernel<F32, 32>), grid, block, 0, s, *a, tiles); break;
-        default: return SS_ERR_UNSUPPORTED;
-    }
+    // tiles start at multiples of block_n, so the 16 / 8-byte chunks of every tile stay aligned
+    const int st = topk_vec<F32>(a) ? launch_topk_tiles<F32, true>(a, tiles, grid, block, s)
+                                    : launch_topk_tiles<F32, false>(a, tiles, grid, block, s);
+    if (st != SS_OK) return st;
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, *a, tiles);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
@@ -226,6 +388,13 @@ extern "C" int ss_topk(const ss_topk_args *a) {
     if ((int64_t)tiles * a->k > a->stride_scratch) return SS_ERR_INVALID_ARGUMENT;
     if (a->stride_logits < a->vocab_size) return SS_ERR_INVALID_ARGUMENT;
     if (a->rows == 0) return SS_OK;
+    if (a->strategy < SS_STRATEGY_AUTO || a->strategy > SS_STRATEGY_ROWWISE) return SS_ERR_INVALID_ARGUMENT;
+    // One workgroup per row (one launch) serves rows of at most 32768 columns on request; AUTO
+    // takes the tile grid: one CU keeps too few cache lines in flight to stream a long row quickly
+    // (config 0, 8 rows of 128 KB: 12.7 us in one launch).
+    if (a->strategy == SS_STRATEGY_ROWWISE && a->vocab_size > SS_BLOCK * ss::TOPK_ROW_E) return SS_ERR_UNSUPPORTED;
+    if (a->strategy == SS_STRATEGY_ROWWISE)
+        return a->dtype == SS_DTYPE_F32 ? ss::launch_topk_rows<true>(a) : ss::launch_topk_rows<false>(a);
     return a->dtype == SS_DTYPE_F32 ? ss::launch_topk<true>(a, tiles)
                                     : ss::launch_topk<false>(a, tiles);
 }

@@ -37,7 +37,7 @@ class Philox(ctypes.Structure):
 class TopKArgs(ctypes.Structure):
     _fields_ = [
         ("logits", c_p), ("stride_logits", c_i64), ("dtype", c_i32), ("rows", c_i32),
-        ("vocab_size", c_i32), ("k", c_i32), ("block_n", c_i32), ("reserved", c_i32),
+        ("vocab_size", c_i32), ("k", c_i32), ("block_n", c_i32), ("strategy", c_i32),
         ("scratch", c_p), ("stride_scratch", c_i64), ("values", c_p),
         ("indices", c_p), ("stream", c_p),
     ]

@@ -160,7 +160,7 @@ class UnshardedBoundedTopK(TwoStageTiling):
 
         args = _native.TopKArgs(
             logits=flat.data_ptr(), stride_logits=flat.stride(0), dtype=dtype, rows=n_rows,
-            vocab_size=flat.size(-1), k=self.k, block_n=block_n, reserved=0,
+            vocab_size=flat.size(-1), k=self.k, block_n=block_n, strategy=0,
             scratch=scratch.data_ptr(), stride_scratch=scratch.stride(0),
             values=values.data_ptr(),
             indices=self.indices.data_ptr(), stream=_native.stream_of(flat),

@@ -77,3 +77,59 @@ def test_signed_zeros_and_infinities():
         ev, ei = oracle_topk(x.to(dtype), 128)
         assert torch.equal(indices, ei)
         assert torch.equal(values.float().abs(), ev.float().abs())
+
+
+@pytest.mark.parametrize("vocab,k,dtype", [
+    (32000, 1, torch.float32), (32000, 128, torch.float32), (30001, 64, torch.float32),
+    (32768, 16, torch.bfloat16), (20001, 128, torch.bfloat16), (1500, 8, torch.float32)])
+def test_one_launch_rows(vocab, k, dtype):
+    """Rows of at most 32768 columns take the one-workgroup-per-row kernel: several k, a
+    vocabulary that is not a multiple of 4 (per-element loads), 64 rows."""
+
+    from bench import spiked_logits
+
+    logits = spiked_logits(64, vocab, seed=vocab + k, dtype=dtype)
+    print(f"one-launch rows V={vocab} k={k} {dtype}", flush=True)
+    check(logits, k, 1024)
+
+
+def test_one_launch_rows_concentrated_values():
+    """One wave holding more than 128 values at or above the bound takes the exact selection."""
+
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(4, 32000, generator=g)
+    logits[:, 4 * 64 * 3:4 * 64 * 3 + 600] = 50.0 + torch.rand(4, 600, generator=g)   # wave 0's columns
+    print("one-launch rows, concentrated", flush=True)
+    check(logits, 128, 1024)
+
+
+@pytest.mark.parametrize("vocab,k,dtype", [(32000, 32, torch.float32), (30001, 128, torch.bfloat16),
+                                           (8192, 8, torch.float32)])
+def test_one_workgroup_per_row_strategy(vocab, k, dtype):
+    """ss_topk with strategy ROWWISE (one launch, one workgroup per row), called through the
+    C-ABI: bit-exact against the oracle, including a heavily tied row that takes the exact path."""
+
+    import ctypes
+
+    from bench import spiked_logits
+    from sonic_sampler import _native
+
+    rows = 8
+    logits = spiked_logits(rows, vocab, seed=vocab, dtype=dtype)
+    logits[1] = torch.randint(-3, 4, (vocab,), generator=torch.Generator().manual_seed(1)).to(dtype)
+    x = logits.to(DEV)
+    values = torch.empty(rows, k, dtype=dtype, device=DEV)
+    indices = torch.empty(rows, k, dtype=torch.int32, device=DEV)
+    scratch = torch.empty(rows, 64 * k, dtype=torch.int64, device=DEV)   # not used by this layout
+    args = _native.TopKArgs(
+        logits=x.data_ptr(), stride_logits=x.stride(0),
+        dtype=_native.SS_DTYPE_F32 if dtype == torch.float32 else _native.SS_DTYPE_BF16,
+        rows=rows, vocab_size=vocab, k=k, block_n=1024, strategy=_native.STRATEGY_ROWWISE,
+        scratch=scratch.data_ptr(), stride_scratch=scratch.stride(0) * (2 if dtype == torch.float32 else 4),
+        values=values.data_ptr(), indices=indices.data_ptr(), stream=_native.stream_of(x))
+    print(f"ss_topk rowwise V={vocab} k={k} {dtype}", flush=True)
+    _native.check(_native.load().ss_topk(ctypes.byref(args)), "ss_topk")
+    torch.cuda.synchronize()
+    ev, ei = oracle_topk(logits, k)
+    assert torch.equal(indices.cpu(), ei)
+    assert torch.equal(values.cpu().float(), ev.float())

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 1
+#define SS_ABI_VERSION 2
 
 /* Upper bound on top-k and the width of every candidate block (reference ops/base.py:24). */
 #define SS_MAX_K 128
@@ -151,7 +151,7 @@ typedef struct ss_singular_args {
     const uint16_t *gumbel; int64_t stride_gumbel;  /* [slots, target_vocab] bf16 */
     ss_philox philox;            /* used instead of gumbel when enabled */
     int32_t philox_step;         /* timestep index used in the Philox counter */
-    int32_t reserved2;
+    int32_t stages;              /* SS_STAGE_* bits to launch; 0 = both */
     /* outputs */
     int32_t *tokens; int64_t stride_tokens;
     uint16_t *logprobs; int64_t stride_logprobs;           /* [rows, 1] bf16 or NULL */
@@ -163,7 +163,21 @@ typedef struct ss_singular_args {
     /* timing: hipEvent_t pair recorded by the tile kernel's own dispatch (start, end), or NULL */
     void *tile_start;
     void *tile_end;
+    /* Sharded vocabulary (reference interface/functional/singular.py:80-83,129-133): `logits` holds
+     * columns [local_rank * shard_size, + vocab_size) of a vocabulary split over world_size shards.
+     * The tile stage writes this shard's candidate lists to slice local_rank of every scratch row
+     * ([world_size, tiles, 128], tiles = ceil(vocab_size / block_n), the same on every shard); the
+     * row stage merges all world_size slices, so an engine runs SS_STAGE_TILES, exchanges the
+     * slices (all-gather) and then runs SS_STAGE_ROWS. world_size = 1 (or 0): unsharded. */
+    int32_t world_size;
+    int32_t local_rank;
+    int32_t shard_size;
+    int32_t reserved;
 } ss_singular_args;
+
+/* ss_singular_args.stages */
+#define SS_STAGE_TILES 1
+#define SS_STAGE_ROWS 2
 
 int ss_fused_singular(const ss_singular_args *args);
 

@@ -84,6 +84,7 @@ __device__ __forceinline__ RowState multistep_row_state(const ss_multistep_args 
     rs.vt = a.vocab_size;
     rs.nhist = 0;
     rs.glds = nullptr;
+    rs.shard = 0;
     return rs;
 }
 
@@ -129,8 +130,9 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     touch_kernargs<sizeof(ss_multistep_args)>();
     const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     const int pivot = request_pivot(a);
+    const ListMap lm = make_list_map(tiles, 0, a.block_n);
     RowSamples smp;
-    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued early
+    load_samples(scr, tiles, lm, smp);  // depends on the row only: issued early
     const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     int32_t *irow = a.indices + (int64_t)row * SS_K;
     if (ind & IND_GREEDY) {
         if (threadIdx.x < 64) {
-            const int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, smp.greedy);
+            const int token = greedy_merge(scr, tiles, lm, a.vocab_size, smp.greedy);
             if (threadIdx.x == 0) {
                 irow[0] = token;
                 vrow[0] = 0.0f;
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     }
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
-    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    merge_row(sm, scr, smp, tiles, lm, a.vocab_size, v0, v1, i0, i1);
     if (threadIdx.x >= 64) return;
     truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
              __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);

@@ -43,6 +43,7 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
     rs.vt = a.target_vocab > 0 ? a.target_vocab : a.vocab_size;
     rs.nhist = 0;
     rs.glds = nullptr;
+    rs.shard = a.world_size > 1 ? a.local_rank * a.shard_size : 0;
     return rs;
 }
 
@@ -80,15 +81,18 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
     if (sync) __syncthreads();
     Keys<E> keys;
     prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
-    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
+    // this shard's slice of the row's [world_size, tiles, 128] lists
+    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch + (a.world_size > 1 ? a.local_rank * tiles * SS_K : 0);
+    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, scr, tile);
 }
 
 // Greedy row (wave 0): the argmax over the tiles' maxima, d2t remap, count update, outputs.
 // `first` is scr[lane], read ahead by load_samples.
 __device__ __forceinline__ void singular_greedy(const ss_singular_args &a, const uint32_t *scr,
-                                                int tiles, int row, int slot, uint32_t first) {
+                                                int lists, const ListMap &lm, int V, int row, int slot,
+                                                uint32_t first) {
     if (threadIdx.x >= 64) return;
-    int token = greedy_merge(scr, tiles, a.block_n, a.vocab_size, first);
+    int token = greedy_merge(scr, lists, lm, V, first);
     if (a.d2t) token = a.d2t[token];
     if (threadIdx.x == 0) {
         if (a.update_counts && a.decode_counts) {
@@ -183,31 +187,34 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
     if (lane == 0) a.tokens[(int64_t)row * a.stride_tokens] = token;
 }
 
-// Row stage of one row: merge of the tiles' candidates (`scr`, global scratch or workgroup
-// memory) and the selection. All threads call.
+// Row stage of one row: merge of the row's `lists` candidate lists (`scr`, global scratch or
+// workgroup memory; list l starts at column lm.base(l) of a V-column vocabulary) and the
+// selection. All threads call.
 __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSmem &sm, int row,
-                                             int tiles, const uint32_t *scr) {
+                                             int lists, const ListMap &lm, int V, const uint32_t *scr) {
     RowSamples smp;
-    load_samples(scr, tiles, a.block_n, smp);  // depends on the row only: issued first
+    load_samples(scr, lists, lm, smp);  // depends on the row only: issued first
     const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, row) : row;
     const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
                                     a.max_top_logprobs);
     if (lane_u32(prm, RP_IND) & IND_GREEDY) {
-        singular_greedy(a, scr, tiles, row, slot, smp.greedy);
+        singular_greedy(a, scr, lists, lm, V, row, slot, smp.greedy);
         return;
     }
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
-    merge_row(sm, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    merge_row(sm, scr, smp, lists, lm, V, v0, v1, i0, i1);
     singular_select(a, sm, row, slot, prm, v0, v1, i0, i1);
 }
 
-// Row stage: grid rows.
-__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int tiles) {
+// Row stage: grid rows; `lists` = world_size * tiles candidate lists per row, `V` the width of
+// the column space they index (all shards).
+__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int lists,
+                                                                ListMap lm, int V) {
     __shared__ SampleSmem sm;
     touch_kernargs<sizeof(ss_singular_args)>();
     const int row = blockIdx.x;
-    singular_row(a, sm, row, tiles, a.scratch + (int64_t)row * a.stride_scratch);
+    singular_row(a, sm, row, lists, lm, V, a.scratch + (int64_t)row * a.stride_scratch);
 }
 
 // Workgroup memory of the one-launch form. The tile stage's and the row stage's memory share
@@ -269,17 +276,18 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rowwise_kernel(ss_singular_
         }
     }
     const uint32_t *scr = sm.lists;
+    const ListMap lm = make_list_map(tiles, 0, a.block_n);
     RowSamples smp;
-    load_samples(scr, tiles, a.block_n, smp);
+    load_samples(scr, tiles, lm, smp);
     const uint32_t prm = row_params(a.indicators, a.top_k, a.top_p, a.min_p, a.top_logprobs, slot,
                                     a.max_top_logprobs);
     if (greedy) {
-        singular_greedy(a, scr, tiles, row, slot, smp.greedy);
+        singular_greedy(a, scr, tiles, lm, a.vocab_size, row, slot, smp.greedy);
         return;
     }
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
-    merge_row(sm.sample, scr, smp, tiles, a.block_n, a.vocab_size, v0, v1, i0, i1);
+    merge_row(sm.sample, scr, smp, tiles, lm, a.vocab_size, v0, v1, i0, i1);
     singular_select(a, sm.sample, row, slot, prm, v0, v1, i0, i1);
 }
 
@@ -312,16 +320,26 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     hipStream_t s = (hipStream_t)a->stream;
     const int stage = staged_grammar_words(a);
     const size_t dyn = (size_t)((stage + 3) & ~3) * sizeof(uint32_t);
-    switch (a->block_n) {
-        case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-        case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-        case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-        case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-        default: return SS_ERR_UNSUPPORTED;
+    const int stages = a->stages ? a->stages : (SS_STAGE_TILES | SS_STAGE_ROWS);
+    if (stages & SS_STAGE_TILES) {
+        switch (a->block_n) {
+            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            default: return SS_ERR_UNSUPPORTED;
+        }
+        if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     }
-    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
-    return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
+    if (stages & SS_STAGE_ROWS) {
+        const int world = a->world_size > 1 ? a->world_size : 1;
+        const int shard = world > 1 ? a->shard_size : 0;
+        const ListMap lm = make_list_map(tiles, shard, a->block_n);
+        const int V = world > 1 ? world * a->shard_size : a->vocab_size;
+        hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, world * tiles, lm, V);
+        if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    }
+    return SS_OK;
 }
 
 static bool aligned(const void *p, int64_t stride, int bytes_per_vec) {
@@ -341,7 +359,12 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
         return SS_ERR_UNSUPPORTED;
     if (a->rows > 65535) return SS_ERR_UNSUPPORTED;  // rows are the tile grid's y dimension
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
-    if (tiles < 2 || (int64_t)tiles * SS_K > a->stride_scratch || tiles > 0xffff)
+    const int world = a->world_size > 1 ? a->world_size : 1;
+    if (a->world_size < 0 || a->local_rank < 0 || a->local_rank >= world) return SS_ERR_INVALID_ARGUMENT;
+    if (world > 1 && a->shard_size < a->vocab_size) return SS_ERR_INVALID_ARGUMENT;
+    if (world > 1 && (int64_t)world * a->shard_size > 0x7fffffff) return SS_ERR_INVALID_ARGUMENT;
+    if (a->stages < 0 || a->stages > (SS_STAGE_TILES | SS_STAGE_ROWS)) return SS_ERR_INVALID_ARGUMENT;
+    if (tiles < 2 || (int64_t)world * tiles * SS_K > a->stride_scratch || (int64_t)world * tiles > 0xffff)
         return SS_ERR_INVALID_ARGUMENT;
     // candidate lists move as 16-byte vectors
     if ((uintptr_t)a->scratch % 16 != 0 || a->stride_scratch % 4 != 0) return SS_ERR_INVALID_ARGUMENT;
@@ -351,13 +374,16 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
     if (a->return_logprobs && a->max_top_logprobs > 0 && a->top_values && !a->top_tokens)
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows == 0) return SS_OK;
-    const bool direct = a->d2t == nullptr;
+    // a shard whose offset is not a multiple of 32 columns cannot read grammar words and counts as
+    // aligned vectors: it takes the per-element gather layout
+    const bool direct = a->d2t == nullptr && (world == 1 || (a->local_rank * a->shard_size) % 32 == 0);
     const bool vec = (a->vocab_size % 4) == 0 && aligned(a->logits, a->stride_logits, 8) &&
                      (!direct || (aligned(a->decode_counts, a->stride_decode, 16) &&
                                   aligned(a->context_counts, a->stride_context, 16) &&
                                   aligned(a->logit_bias, a->stride_bias, 8)));
     if (a->strategy < SS_STRATEGY_AUTO || a->strategy > SS_STRATEGY_ROWWISE) return SS_ERR_INVALID_ARGUMENT;
-    if (a->strategy == SS_STRATEGY_ROWWISE && tiles > ROWWISE_MAX_TILES) return SS_ERR_UNSUPPORTED;
+    if (a->strategy == SS_STRATEGY_ROWWISE && (tiles > ROWWISE_MAX_TILES || world > 1 || a->stages))
+        return SS_ERR_UNSUPPORTED;
     // AUTO takes the tile grid: one workgroup per row leaves a CU with a single workgroup (one
     // wave per SIMD) working through its tiles one after another, which measured slower on every
     // shape tried (config 4: 36 us for the row kernel against 23 + 7 us for the two launches).
@@ -402,7 +428,8 @@ extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
     if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
         return SS_ERR_UNSUPPORTED;
     const int64_t tiles = ((int64_t)a->vocab_size + a->block_n - 1) / a->block_n;
-    if ((int64_t)a->rows * tiles * SS_K * (int64_t)sizeof(uint32_t) > (int64_t)SS_STATIC_SCRATCH_BYTES)
+    const int64_t world = a->world_size > 1 ? a->world_size : 1;
+    if ((int64_t)a->rows * world * tiles * SS_K * (int64_t)sizeof(uint32_t) > (int64_t)SS_STATIC_SCRATCH_BYTES)
         return SS_ERR_SCRATCH_LIMIT;
     uint32_t *ptr = static_scratch();
     if (!ptr) return SS_ERR_LAUNCH;
@@ -410,6 +437,6 @@ extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
     // row's merge samples are read but ignored), so the array needs no clearing between calls.
     ss_singular_args b = *a;
     b.scratch = ptr;
-    b.stride_scratch = tiles * SS_K;
+    b.stride_scratch = world * tiles * SS_K;
     return ss_fused_singular(&b);
 }

@@ -65,9 +65,40 @@ struct RowState {
     // The row's grammar words staged in workgroup memory (gather layout only), or NULL: the
     // gathers through d2t then read LDS instead of scattered global words.
     const uint32_t *glds;
+    // Column of the logits' first column in the target vocabulary (sharded vocabulary: the
+    // shard's offset), added to every column that addresses a side plane, d2t or the history.
+    int shard;
 };
 
 typedef const __attribute__((address_space(3))) uint32_t *lds_cu32p;
+
+// First column of candidate list `l` of a row: lists are the tiles of `per` tiles per shard, shard
+// w covering target columns [w * shard, ...), so list l is tile l % per of shard l / per. The
+// division is a multiply-high by magic = ceil(2^32 / per), exact for l < 2^16 and 2 <= per < 2^16.
+// Unsharded rows use per = the row's tile count, so l / per is 0.
+struct ListMap {
+    uint32_t magic;
+    int per, shard, block_n;
+    __device__ __forceinline__ int base(int l) const {
+        const int w = (int)__umulhi((uint32_t)l, magic);
+        return w * shard + (l - w * per) * block_n;
+    }
+    // Scratch entry holding greedy list l's composite: a shard's tiles store theirs densely at
+    // the start of the shard's slice (tile t of shard w at w * per * 128 + t).
+    __device__ __forceinline__ int greedy_entry(int l) const {
+        const int w = (int)__umulhi((uint32_t)l, magic);
+        return w * per * SS_K + (l - w * per);
+    }
+};
+
+__host__ __device__ inline ListMap make_list_map(int per, int shard, int block_n) {
+    ListMap m;
+    m.magic = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)per - 1) / (uint64_t)per);
+    m.per = per;
+    m.shard = shard;
+    m.block_n = block_n;
+    return m;
+}
 
 __device__ __forceinline__ int tile_col(int j) {  // column offset of element j inside a tile
     return (j >> 2) * (SS_BLOCK * 4) + (int)threadIdx.x * 4 + (j & 3);
@@ -475,7 +506,7 @@ __device__ __forceinline__ void direct_keys(const RowState &rs, const Uses &u, i
         // restores the original count of token 0 (core/naive.py:179-203).
         // Offset of the token from the lane's element 0, compared with each element's constant
         // offset (j / 4) * 1024 + j % 4, so no per-element column is kept live.
-        const int base = col0 + 4 * (int)threadIdx.x;
+        const int base = rs.shard + col0 + 4 * (int)threadIdx.x;
         for (int h = 0; h < rs.nhist; ++h) {
             const int t = hist[h];
             if (t == 0) continue;
@@ -571,15 +602,15 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
     if (u.g || u.rep || u.bias) {
         int tcol[E];
 #pragma unroll
-        for (int j = 0; j < E; ++j) tcol[j] = col0 + tile_col(j);
+        for (int j = 0; j < E; ++j) tcol[j] = rs.shard + col0 + tile_col(j);
         if (u.remap) {
-            const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)V * 4);
+            const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)(rs.shard + V) * 4);
             if (VEC) {
                 // the 4 columns of a chunk are consecutive (and V % 4 == 0): one 16-byte load
 #pragma unroll
                 for (int c = 0; c < NCH; ++c) {
                     const i32x4 t = __builtin_bit_cast(
-                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(m, lane4 * 4, (col0 + c * (SS_BLOCK * 4)) * 4, 0));
+                        i32x4, __builtin_amdgcn_raw_buffer_load_b128(m, lane4 * 4, (rs.shard + col0 + c * (SS_BLOCK * 4)) * 4, 0));
                     tcol[4 * c + 0] = t.x; tcol[4 * c + 1] = t.y; tcol[4 * c + 2] = t.z; tcol[4 * c + 3] = t.w;
                 }
             } else {
@@ -687,7 +718,7 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             for (int h = 0; h < 2; ++h) {
                 const u32x2 lh[4] = {lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]};
                 Planes<16> pl;
-                issue_planes<16>(rs, u, true, col0 + 4 * 4 * SS_BLOCK * h, pl);
+                issue_planes<16>(rs, u, true, rs.shard + col0 + 4 * 4 * SS_BLOCK * h, pl);
                 Keys<16> kh;
                 direct_keys<16>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, pl, kh);
 #pragma unroll
@@ -695,7 +726,7 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             }
         } else {
             Planes<E> pl;
-            issue_planes<E>(rs, u, true, col0, pl);
+            issue_planes<E>(rs, u, true, rs.shard + col0, pl);
             direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
         }
     } else {
@@ -960,12 +991,12 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
 }
 
 // Greedy merge over the tiles' maxima (wave 0): the largest value, lowest column on ties.
-// `first` is scr[lane], read ahead by load_samples.
-__device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int block_n, int V,
+// `first` is the composite of list `lane`, read ahead by load_samples.
+__device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, const ListMap &lm, int V,
                                             uint32_t first) {
     uint64_t best = 0;
     for (int t = lane_id(); t < tiles; t += 64) {
-        const uint32_t c = t < 64 ? first : scr[t];
+        const uint32_t c = t < 64 ? first : scr[lm.greedy_entry(t)];
         const uint64_t c64 = ((uint64_t)(c >> 16) << 32) | ((uint64_t)(0xffffu - (uint32_t)t) << 16) |
                              (uint64_t)(c & 0xffffu);
         best = best > c64 ? best : c64;
@@ -973,7 +1004,7 @@ __device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int 
     best = wave_max_u64(best);
     const int tile = (int)(0xffffu - (uint32_t)((best >> 16) & 0xffffu));
     const int off = (int)(0xffffu - (uint32_t)(best & 0xffffu));
-    const int idx = tile * block_n + off;
+    const int idx = lm.base(tile) + off;
     return idx < V ? idx : V - 1;
 }
 
@@ -981,7 +1012,7 @@ __device__ __forceinline__ int greedy_merge(const uint32_t *scr, int tiles, int 
 // as (key << 8 | 127 - pos) composites and column indices in sm.cand / sm.idx.
 template <bool HELD, int EM, class Load, class Cand>
 __device__ __forceinline__ void merge_select(SampleSmem &sm, int nsc, Load load, Cand cand,
-                                             int block_n, int V) {
+                                             const ListMap &lm, int V) {
     uint32_t thi, margin;
     int level;
     radix_threshold<EM, 16>(sm.sel, nsc, load, (uint32_t)SS_K, thi, level, margin);
@@ -989,7 +1020,7 @@ __device__ __forceinline__ void merge_select(SampleSmem &sm, int nsc, Load load,
         if (pos >= (uint32_t)SS_K) return;
         const int p = order_pos<EM, 4>(sc, j);
         const uint32_t c = cand(sc, j);
-        const int idx = (p / SS_K) * block_n + (int)(0xffffu - (c & 0xffffu));
+        const int idx = lm.base(p / SS_K) + (int)(0xffffu - (c & 0xffffu));
         sm.cand[pos] = ((uint64_t)(c >> 16) << 8) | (uint64_t)(127u - pos);
         sm.idx[pos] = idx < V ? idx : V - 1;  // only an absent-element sentinel can exceed V
     });
@@ -1000,7 +1031,7 @@ __device__ __forceinline__ void merge_select(SampleSmem &sm, int nsc, Load load,
 // e = 2 * lane + i as (v_i, idx_i). Up to 4096 candidates are read once with 16-byte loads and
 // kept in registers; larger rows stream them from the scratch per pass.
 __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *scr, int tiles,
-                                                int block_n, int V, float &v0, float &v1, int &i0,
+                                                const ListMap &lm, int V, float &v0, float &v1, int &i0,
                                                 int &i1) {
     constexpr int EM = 16;
     const int ncand = tiles * SS_K;
@@ -1019,7 +1050,7 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
 #pragma unroll
                 for (int j = 0; j < EM; ++j) out[j] = held[j] >> 16;
             },
-            [&](int, int j) { return held[j]; }, block_n, V);
+            [&](int, int j) { return held[j]; }, lm, V);
     } else {
         merge_select<false, EM>(
             sm, nsc,
@@ -1030,7 +1061,7 @@ __device__ __forceinline__ void merge_row_radix(SampleSmem &sm, const uint32_t *
                     out[j] = p < ncand ? (scr[p] >> 16) : 0u;
                 }
             },
-            [&](int sc, int j) { return scr[order_pos<EM, 4>(sc, j)]; }, block_n, V);
+            [&](int sc, int j) { return scr[order_pos<EM, 4>(sc, j)]; }, lm, V);
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -1071,7 +1102,7 @@ __device__ __forceinline__ int merge_run(int kp) {
     return (kp >= 8 && kp <= 64 && (kp & (kp - 1)) == 0) ? kp : 1;
 }
 
-__device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int block_n,
+__device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, const ListMap &lm,
                                              RowSamples &smp) {
     const int kp = merge_prefix(tiles);
     smp.kp = kp;
@@ -1096,14 +1127,14 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int
             list = slot_list(smp, s);
         }
         smp.slot[i] = s;
-        smp.base[i] = list * block_n;
+        smp.base[i] = lm.base(list);
         smp.raw[i] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
     }
     const int t = (int)threadIdx.x;
     smp.next = (t < 64 && t < tiles && kp < SS_K) ? scr[t * SS_K + kp] : 0u;
     // read before the row's indicator is known, so that a greedy row's merge waits for no
     // further load
-    smp.greedy = (t < 64 && t < tiles) ? scr[t] : 0u;
+    smp.greedy = (t < 64 && t < tiles) ? scr[lm.greedy_entry(t)] : 0u;
 }
 
 // Row merge over the tiles' sorted candidate lists, from the samples of load_samples. All threads
@@ -1118,7 +1149,7 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, int
 // i.e. unless a list's first unmerged entry beats the 128th merged one; that case (rare: 17 of the
 // top-128 in one of 32 tiles) falls back to the radix merge over every candidate.
 __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
-                                          const RowSamples &smp, int tiles, int block_n, int V,
+                                          const RowSamples &smp, int tiles, const ListMap &lm, int V,
                                           float &v0, float &v1, int &i0, int &i1) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
@@ -1183,7 +1214,7 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
     }
     __syncthreads();
     if (sm.flag) {
-        merge_row_radix(sm, scr, tiles, block_n, V, v0, v1, i0, i1);
+        merge_row_radix(sm, scr, tiles, lm, V, v0, v1, i0, i1);
         return;
     }
     if (wave == 0) {

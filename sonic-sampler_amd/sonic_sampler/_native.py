@@ -24,10 +24,11 @@ c_u64 = ctypes.c_uint64
 SS_OK = 0
 SS_ERR_SCRATCH_LIMIT = 4
 STRATEGY_AUTO, STRATEGY_TILES, STRATEGY_ROWWISE = 0, 1, 2
+STAGE_TILES, STAGE_ROWS = 1, 2
 STATIC_SCRATCH_BYTES = 8 << 20   # SS_STATIC_SCRATCH_BYTES
 SS_DTYPE_BF16 = 0
 SS_DTYPE_F32 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Philox(ctypes.Structure):
@@ -58,13 +59,14 @@ class SingularArgs(ctypes.Structure):
         ("logit_bias", c_p), ("stride_bias", c_i64),
         ("temperature", c_p), ("top_k", c_p), ("top_p", c_p), ("min_p", c_p),
         ("top_logprobs", c_p), ("gumbel", c_p), ("stride_gumbel", c_i64),
-        ("philox", Philox), ("philox_step", c_i32), ("reserved2", c_i32),
+        ("philox", Philox), ("philox_step", c_i32), ("stages", c_i32),
         ("tokens", c_p), ("stride_tokens", c_i64),
         ("logprobs", c_p), ("stride_logprobs", c_i64),
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("probabilities", c_p), ("stride_probabilities", c_i64),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
         ("tile_start", c_p), ("tile_end", c_p),
+        ("world_size", c_i32), ("local_rank", c_i32), ("shard_size", c_i32), ("reserved", c_i32),
     ]
 
 

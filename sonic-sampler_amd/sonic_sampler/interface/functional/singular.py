@@ -15,6 +15,10 @@ Additions to the reference's keywords (all optional):
   from torch's default generator, replacing the reference's fresh ``exponential_().log_()`` plane.
 * ``tile_events`` -- a pair of timing ``torch.cuda.Event`` recorded by the tile kernel's own
   dispatch at its start and end (per-kernel timing without extra stream packets).
+* ``stage`` -- ``"tiles"`` launches only the tile stage (with ``world_size > 1``: this shard's
+  candidate lists into slice ``local_rank`` of every scratchpad row), ``"rows"`` only the row stage
+  (merge of all ``world_size`` slices and selection); ``None`` both. A tensor-parallel engine runs
+  ``"tiles"``, all-gathers the scratchpad slices, then ``"rows"``.
 * ``kernel_layout`` -- ``"tiles"`` (tile grid + row merge, two launches) or ``"rowwise"`` (one
   workgroup per row, one launch, rows of at most 16 tiles); ``None`` lets the library choose
   (currently the tile grid).
@@ -43,7 +47,6 @@ from sonic_sampler.interface.functional.base import (
     I32,
     fresh_seed,
     philox,
-    resolve_scratchpad,
     unit_stride,
     validate_block,
     validate_count_update,
@@ -53,6 +56,8 @@ from sonic_sampler.ops.base import MAX_K
 
 KERNEL_LAYOUTS = {None: _native.STRATEGY_AUTO, "tiles": _native.STRATEGY_TILES,
                   "rowwise": _native.STRATEGY_ROWWISE}
+
+STAGES = {None: 0, "tiles": _native.STAGE_TILES, "rows": _native.STAGE_ROWS}
 
 
 def resolve_tokens(buffer: Optional[Tensor], batch_size: int, source: Tensor) -> Tensor:
@@ -124,6 +129,7 @@ def fused_singular(
     tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
     kernel_layout: Optional[str] = None,
     static_scratch: bool = False,
+    stage: Optional[str] = None,
 ) -> Selection:
 
     validate_count_update(update_counts, decode_counts)
@@ -133,10 +139,17 @@ def fused_singular(
 
         raise ValueError(f"kernel_layout must be one of {sorted(k for k in KERNEL_LAYOUTS if k)} or None")
 
-    if world_size != 1 or local_rank != 0:
+    if world_size < 1 or not 0 <= local_rank < world_size:
 
-        raise ValueError("sharded-vocabulary scratchpads are not supported by the gfx950 path "
-                         "(gather the logits first)")
+        raise ValueError(f"local rank {local_rank} outside a world of {world_size} shards")
+
+    if stage not in STAGES:
+
+        raise ValueError(f"stage must be one of {sorted(k for k in STAGES if k)} or None")
+
+    if logits.dim() == 2 and (shard_size or 0) and shard_size < min(logits.size(1), local_vocab or logits.size(1)):
+
+        raise ValueError(f"shard size {shard_size} is smaller than the local vocabulary")
 
     if logits.dtype != BF16 or logits.dim() != 2:
 
@@ -157,18 +170,30 @@ def fused_singular(
 
     batch_size, vocab_size = logits.shape
     vocab_size = min(vocab_size, local_vocab or vocab_size)
+    shard_size = shard_size or vocab_size
+
+    vocab_blocks = -(-vocab_size // block_n)
+
+    if vocab_blocks <= 1:
+
+        raise ValueError(f"total vocab blocks must be greater than 1, got {vocab_blocks} instead")
 
     if static_scratch:
 
         bitpacked = None
 
-        if -(-logits.size(1) // block_n) <= 1:
+    elif scratchpad is None:
 
-            raise ValueError("total vocab blocks must be greater than 1")
+        bitpacked = logits.new_empty(batch_size, world_size * vocab_blocks * MAX_K, dtype=I32).view(torch.uint32)
 
     else:
 
-        _, _, bitpacked, vocab_blocks = resolve_scratchpad(logits, block_n, scratchpad)
+        bitpacked = scratchpad
+
+        if (bitpacked.size(0) < batch_size or bitpacked.stride(-1) != 1
+                or bitpacked.stride(0) < world_size * vocab_blocks * MAX_K):
+
+            raise ValueError("scratchpad too small for the given logits, block_n and world size")
 
     final_tokens = resolve_tokens(output_tokens, batch_size, logits)
 
@@ -215,7 +240,7 @@ def fused_singular(
     args = _native.SingularArgs(
         logits=p(logits), stride_logits=logits.stride(0), rows=batch_size,
         vocab_size=vocab_size,
-        target_vocab=target_vocab or (logit_bias.size(-1) if logit_bias is not None else vocab_size),
+        target_vocab=target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size),
         block_n=block_n, lookahead=lookahead, timestep=history,
         max_top_logprobs=max_top_logprobs if top_values is not None else 0,
         is_prefill=int(is_prefill), update_counts=int(update_counts),
@@ -233,7 +258,7 @@ def fused_singular(
         top_logprobs=p(top_k_logprobs),
         gumbel=p(gumbel_noise) if philox_seed is None else None,
         stride_gumbel=s(gumbel_noise) if philox_seed is None else 0,
-        philox=philox(philox_seed, philox_offset), philox_step=philox_step, reserved2=0,
+        philox=philox(philox_seed, philox_offset), philox_step=philox_step, stages=STAGES[stage],
         tokens=p(final_tokens), stride_tokens=final_tokens.stride(0),
         logprobs=p(token_logprobs), stride_logprobs=s(token_logprobs),
         top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
@@ -242,6 +267,7 @@ def fused_singular(
         stream=_native.stream_of(logits),
     )
     args.tile_start, args.tile_end = _native.event_pair(tile_events)
+    args.world_size, args.local_rank, args.shard_size = world_size, local_rank, shard_size
 
     lib = _native.load()
     entry = "ss_fused_singular_noalloc" if static_scratch else "ss_fused_singular"

@@ -193,8 +193,12 @@ def test_fused_singular_argument_errors():
         fused_singular(logits, flags, block_n=1000)
     with pytest.raises(ValueError, match="top logprobs"):
         fused_singular(logits, flags, block_n=1024, max_top_logprobs=129)
-    with pytest.raises(ValueError, match="sharded"):
-        fused_singular(logits, flags, block_n=1024, world_size=2)
+    with pytest.raises(ValueError, match="local rank"):
+        fused_singular(logits, flags, block_n=1024, world_size=2, local_rank=2)
+    with pytest.raises(ValueError, match="shard size"):
+        fused_singular(logits, flags, block_n=1024, world_size=2, shard_size=4096)
+    with pytest.raises(ValueError, match="stage"):
+        fused_singular(logits, flags, block_n=1024, stage="merge")
     with pytest.raises(ValueError):
         fused_singular(logits, flags, block_n=1024, update_counts=True)   # counts required
 

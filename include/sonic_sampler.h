@@ -19,6 +19,7 @@
  *                          (launches K1 ops/prologue.py:272-472 + K4 ops/singular.py:154-358)
  *   ss_fused_multistep  <- fused_multistep, src/sonic_sampler/interface/functional/multistep.py:175-461
  *                          (launches K1 + K5 ops/multistep.py:76-226 + K6 ops/verify.py:244-434)
+ *   ss_indexed_copy     <- indexed_copy, src/sonic_sampler/ops/copy.py:21-127 (noise staging)
  *   ss_gumbel_materialize / ss_philox_raw  <- no kernel counterpart: the reference draws its noise
  *                          with torch (`exponential_().log_()`, src/sonic_sampler/core/buffer.py:118);
  *                          these write the counter-based Philox noise the fused kernels can generate
@@ -252,6 +253,26 @@ typedef struct ss_multistep_args {
 int ss_fused_multistep(const ss_multistep_args *args);
 
 /* ---------------------------------------------------------------------------------------------
+ * Indexed copy of noise rows: for i < count, slot = indices[i]; when indicators is NULL or
+ * (indicators[slot] & SS_GREEDY) == 0, copy source[slot * stride_source + c] into
+ * target[slot * stride_target + c] for c < cols (bf16 elements; a slot outside [0, slots) is
+ * skipped). Replaces indexed_copy (reference ops/copy.py:21-127), which stages the drafter's
+ * Gumbel noise into the verifier's (GumbelNoise.stage_weights, core/buffer.py:151-159).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct ss_indexed_copy_args {
+    const uint16_t *source; int64_t stride_source;  /* [slots, >= cols] */
+    uint16_t *target; int64_t stride_target;        /* [slots, >= cols] */
+    const int64_t *indices;                          /* [count] slots to copy */
+    const uint16_t *indicators;                      /* [slots] or NULL */
+    int64_t cols;
+    int32_t count;
+    int32_t slots;
+    void *stream;
+} ss_indexed_copy_args;
+
+int ss_indexed_copy(const ss_indexed_copy_args *args);
+
+/* ---------------------------------------------------------------------------------------------
  * Philox noise, written out so that the in-register noise of the fused kernels is observable.
  * out[s * stride_slot + t * stride_step + v] = bf16(log(bf16(-log(u)))),  u in (0, 1),
  * for s < slots, t < timesteps, v < vocab, u drawn at counter (v, s, t, offset).
@@ -267,7 +288,8 @@ int ss_philox_raw(uint64_t seed, uint32_t offset, int32_t slots, int32_t timeste
 /* Introspection. */
 int ss_abi_version(void);
 const char *ss_status_string(int status);
-/* sizeof of each argument struct, by index 0=topk, 1=singular, 2=multistep (ABI self-check). */
+/* sizeof of each argument struct, by index 0=topk, 1=singular, 2=multistep, 3=indexed copy
+ * (ABI self-check). */
 int64_t ss_args_size(int which);
 
 #ifdef __cplusplus

@@ -21,6 +21,7 @@ extern "C" int64_t ss_args_size(int which) {
         case 0: return (int64_t)sizeof(ss_topk_args);
         case 1: return (int64_t)sizeof(ss_singular_args);
         case 2: return (int64_t)sizeof(ss_multistep_args);
+        case 3: return (int64_t)sizeof(ss_indexed_copy_args);
         default: return -1;
     }
 }

@@ -95,6 +95,14 @@ class MultistepArgs(ctypes.Structure):
     ]
 
 
+class IndexedCopyArgs(ctypes.Structure):
+    _fields_ = [
+        ("source", c_p), ("stride_source", c_i64), ("target", c_p), ("stride_target", c_i64),
+        ("indices", c_p), ("indicators", c_p), ("cols", c_i64), ("count", c_i32), ("slots", c_i32),
+        ("stream", c_p),
+    ]
+
+
 _lib: ctypes.CDLL | None = None
 
 
@@ -128,7 +136,7 @@ def load() -> ctypes.CDLL:
 
     for name, struct in (("ss_topk", TopKArgs), ("ss_fused_singular", SingularArgs),
                          ("ss_fused_singular_noalloc", SingularArgs),
-                         ("ss_fused_multistep", MultistepArgs)):
+                         ("ss_fused_multistep", MultistepArgs), ("ss_indexed_copy", IndexedCopyArgs)):
         fn = getattr(lib, name)
         fn.restype = c_i32
         fn.argtypes = [ctypes.POINTER(struct)]
@@ -142,7 +150,7 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"sonic_sampler ABI mismatch: library {lib.ss_abi_version()}, "
                            f"bindings {ABI_VERSION}")
 
-    for which, struct in enumerate((TopKArgs, SingularArgs, MultistepArgs)):
+    for which, struct in enumerate((TopKArgs, SingularArgs, MultistepArgs, IndexedCopyArgs)):
         if lib.ss_args_size(which) != ctypes.sizeof(struct):
             raise RuntimeError(f"sonic_sampler ABI mismatch in {struct.__name__}: "
                                f"{lib.ss_args_size(which)} != {ctypes.sizeof(struct)} bytes")
@@ -211,3 +219,27 @@ def require_device(*tensors: torch.Tensor | None) -> None:
             raise ValueError(
                 f"sonic_sampler kernels run on the GPU only; got a tensor on {tensor.device}"
             )
+
+
+def indexed_copy(source: torch.Tensor, target: torch.Tensor, indices: torch.Tensor,
+                 indicators: torch.Tensor | None) -> None:
+    """ss_indexed_copy over bf16 rows: target[i] = source[i] for every i in `indices` whose
+    indicator is stochastic (bit 0x40 clear), on the current stream."""
+
+    require_device(source, target, indices, indicators)
+
+    if source.dtype != torch.bfloat16 or target.dtype != torch.bfloat16:
+        raise ValueError("indexed_copy copies bfloat16 rows")
+
+    src, dst = source.flatten(1), target.flatten(1)
+
+    if src.stride(-1) != 1 or dst.stride(-1) != 1 or src.size(1) != dst.size(1) or src.size(0) != dst.size(0):
+        raise ValueError("indexed_copy needs equally shaped source and target with contiguous rows")
+
+    idx = indices.to(torch.int64).contiguous()
+    args = IndexedCopyArgs(
+        source=src.data_ptr(), stride_source=src.stride(0), target=dst.data_ptr(), stride_target=dst.stride(0),
+        indices=idx.data_ptr(), indicators=None if indicators is None else indicators.data_ptr(),
+        cols=src.size(1), count=idx.numel(), slots=src.size(0), stream=stream_of(src),
+    )
+    check(load().ss_indexed_copy(ctypes.byref(args)), "ss_indexed_copy")

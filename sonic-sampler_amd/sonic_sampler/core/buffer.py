@@ -74,6 +74,77 @@ def _device(device) -> torch.device:
     return torch.device("cpu")
 
 
+def _rows(positions: Optional[List[int]], size: int) -> List[int]:
+    """The rows an update touches: `positions`, or every row in order."""
+
+    return list(positions) if positions else list(range(size))
+
+
+def _send(device_rows: Tensor, host_rows: Tensor, positions: Optional[List[int]], stream=None) -> None:
+    """Non-blocking host -> device copy of rows `positions` (all rows when None) on `stream`."""
+
+    with (stream or nullcontext()):
+
+        if positions:
+
+            for i in positions:
+
+                device_rows[i].copy_(host_rows[i], non_blocking=True)
+
+        else:
+
+            device_rows.copy_(host_rows, non_blocking=True)
+
+
+def _stage(host_rows: Tensor, values: Tensor, positions: Optional[List[int]]) -> None:
+    """Writes `values` ([n, ...], host) into the staging rows `positions` (all rows when None)."""
+
+    if positions:
+
+        host_rows.index_copy_(0, torch.tensor(positions, dtype=I64), values.to(host_rows.dtype))
+
+    else:
+
+        host_rows.copy_(values)
+
+
+def initialize_generator(seed: Optional[int], device) -> Optional[Generator]:
+    """A generator on `device` seeded with `seed` (which also seeds Python's `random`), or None
+    (reference ``core/buffer.py:673-682``)."""
+
+    if seed is None:
+
+        return None
+
+    _random.seed(seed)
+
+    return torch.Generator(device).manual_seed(seed)
+
+
+def resolve_updates(size: int, generator=None, selectors=None, positions=None, prefill=False):
+    """The weight refreshes one update performs, as (row or None, generator, (target, draft),
+    prefill) tuples (reference ``core/buffer.py:166-192``): one whole-batch refresh for a shared
+    generator without positions or selectors, else one refresh per row of `positions` (or of the
+    batch) with its own generator, selector pair and prefill flag when lists are given."""
+
+    shared = generator is None or isinstance(generator, Generator)
+
+    if shared and not positions and not selectors and not isinstance(prefill, list):
+
+        return [(None, generator, (True, True), bool(prefill))]
+
+    if shared and not positions and not selectors and isinstance(prefill, list) and not prefill:
+
+        return [(None, generator, (True, True), False)]
+
+    rows = _rows(positions, size)
+    gens = generator if isinstance(generator, list) else [generator] * len(rows)
+    pairs = selectors if selectors else [(True, True)] * len(rows)
+    flags = prefill if isinstance(prefill, list) and prefill else [bool(prefill)] * len(rows)
+
+    return list(zip(rows, gens, pairs, flags))
+
+
 @dataclass(eq=False, kw_only=True)
 class GumbelNoise(SliceBuffer):
 
@@ -141,14 +212,23 @@ class GumbelNoise(SliceBuffer):
     def stage_weights(self, indices: Tensor, indicator: Tensor, stream=None):
         """Copies draft noise into target noise for the rows in ``indices`` whose draft indicator
         is stochastic, so verification sees the noise the drafter used (reference
-        ``core/buffer.py:151-159``, ``ops/copy.py:21-127``)."""
+        ``core/buffer.py:151-159``, ``ops/copy.py:21-127``). On the GPU this is the library's
+        ``ss_indexed_copy`` kernel; host-resident buffers are copied with torch."""
 
         with (stream or nullcontext()):
 
-            rows = indices.to(I64)
-            stochastic = (indicator.to(I32).index_select(0, rows) & int(Indicator.GREEDY)) == 0
-            keep = rows[stochastic]
-            self.target.index_copy_(0, keep, self.draft.index_select(0, keep))
+            if self.target.device.type == "cuda":
+
+                from sonic_sampler import _native
+
+                _native.indexed_copy(self.draft, self.target, indices, indicator)
+
+            else:
+
+                rows = indices.to(I64)
+                stochastic = (indicator.to(I32).index_select(0, rows) & int(Indicator.GREEDY)) == 0
+                keep = rows[stochastic]
+                self.target.index_copy_(0, keep, self.draft.index_select(0, keep))
 
         return self
 
@@ -204,6 +284,46 @@ class StochasticWeights(SliceBuffer):
 
             self.uniform[row].uniform_(TINY, 1.0, generator=generator)
 
+    def update(self, generator=None, selectors=None, targets=None, positions=None, prefill=False,
+               stream=None, event=None) -> "StochasticWeights":
+        """Redraws the noise between iterations (reference ``core/buffer.py:252-311``): every
+        refresh of ``resolve_updates`` whose target selector is set redraws its row (prefill: the
+        target noise of step 0, plus the draft noise when drafting is stochastic; decode: the
+        selected plane and the uniforms), then ``targets`` (device noise rows from the drafter, at
+        ``positions`` or in order) replace the target noise outside prefill."""
+
+        with (stream or nullcontext()):
+
+            for row, rng, (target, draft), initial in resolve_updates(
+                    self.layout.rows, generator, selectors, positions, prefill):
+
+                if target:
+
+                    self.refresh(position=row, generator=rng, prefill=initial, draft=draft)
+
+            if targets and not prefill:
+
+                self.gumbel.update(targets=targets, positions=positions, stream=stream)
+
+            if event is not None:
+
+                event.record(stream)
+
+        return self
+
+    def step(self, positions: List[int], scoped: ScopedIndicators, indicator: Tensor,
+             indices: Optional[Tensor] = None, generator=None, stream=None, event=None) -> None:
+        """After a decode iteration (reference ``core/buffer.py:313-344``): stage the draft noise
+        of the device rows ``indices`` into the target noise when some drafting is stochastic,
+        then redraw the noise of ``positions``."""
+
+        if indices is not None and scoped.has_stochastic_draft:
+
+            self.gumbel.stage_weights(indices=indices, indicator=indicator, stream=stream)
+
+        self.update(generator=generator, selectors=scoped.stochastic_selectors, positions=positions,
+                    stream=stream, event=event)
+
 
 @dataclass(eq=False, kw_only=True)
 class TokenCounts(SliceBuffer):
@@ -224,6 +344,40 @@ class TokenCounts(SliceBuffer):
 
         return cls(context=both[0], decode=both[1], pinned=_pinned((size, vocab_size), I32),
                    layout=Layout(size, timesteps))
+
+    @classmethod
+    def random(cls, size: int, timesteps: int, vocab_size: int, generator=None) -> "TokenCounts":
+        """Counts drawn uniformly from [0, 32) (reference ``core/buffer.py:359-375``)."""
+
+        both = torch.randint(0, 32, (2, size, vocab_size), dtype=I32, generator=generator)
+
+        return cls(context=both[0], decode=both[1], pinned=_pinned((size, vocab_size), I32),
+                   layout=Layout(size, timesteps))
+
+    def populate(self, encodings: List[Tensor], positions: List[int]) -> "TokenCounts":
+        """Histograms each prompt (host int64 token ids) into the staging row of its position."""
+
+        for i, tokens in zip(positions, encodings):
+
+            row = self.pinned[i].zero_()
+            row.scatter_add_(0, tokens.to(I64), torch.ones(tokens.numel(), dtype=I32))
+
+        return self
+
+    def allocate(self, encodings: List[Tensor], positions: List[int], stream=None) -> "TokenCounts":
+        """Request admission (reference ``core/buffer.py:434-457``): the prompts' histograms become
+        the context counts of `positions` and their decode counts restart at zero."""
+
+        self.populate(encodings, positions)
+
+        with (stream or nullcontext()):
+
+            for i in positions:
+
+                self.context[i].copy_(self.pinned[i], non_blocking=True)
+                self.decode[i].zero_()
+
+        return self
 
     def subset(self, indices: Tensor) -> "TokenCounts":
 
@@ -278,6 +432,64 @@ class RepetitionPenalties(SliceBuffer):
             layout=Layout(size, timesteps),
         )
 
+    @classmethod
+    def random(cls, size: int, timesteps: int, vocab_size: int, generator=None,
+               flags: Optional[Flags] = None) -> "RepetitionPenalties":
+        """Random counts and penalties (reference ``core/buffer.py:493-532``); with `flags`, rows
+        whose indicator leaves a penalty off get its neutral value."""
+
+        freq_pres = torch.empty((2, size), dtype=BF16).uniform_(-2, 2, generator=generator)
+        mult = torch.empty(size, dtype=BF16).uniform_(0.5, 1.5, generator=generator)
+
+        if flags is not None:
+
+            freq_pres[0].masked_fill_(~flags.selectors(Indicator.FREQUENCY), 0)
+            freq_pres[1].masked_fill_(~flags.selectors(Indicator.PRESENCE), 0)
+            mult.masked_fill_(~flags.selectors(Indicator.MULTIPLICATIVE), 1)
+
+        return cls(counts=TokenCounts.random(size, timesteps, vocab_size, generator),
+                   frequency=freq_pres[0], presence=freq_pres[1], multiplicative=mult,
+                   pinned=_pinned((3, size), BF16).T, layout=Layout(size, timesteps))
+
+    def populate(self, multiplicative: List[float], frequency: List[float], presence: List[float],
+                 positions: Optional[List[int]] = None) -> "RepetitionPenalties":
+        """Stages (multiplicative, frequency, presence) per row in the pinned relay."""
+
+        values = torch.tensor([multiplicative, frequency, presence], dtype=BF16).T
+        _stage(self.pinned, values, positions)
+
+        return self
+
+    def transfer(self, positions: Optional[List[int]], stream=None) -> "RepetitionPenalties":
+        """Sends the staged penalties of `positions` (all rows when None) to the device."""
+
+        for column, member in enumerate((self.multiplicative, self.frequency, self.presence)):
+
+            _send(member, self.pinned[:, column], positions, stream)
+
+        return self
+
+    def update(self, counts: List[Tuple[Tensor, Tensor]], multiplicative: List[float],
+               frequency: List[float], presence: List[float], positions: Optional[List[int]] = None,
+               stream=None) -> "RepetitionPenalties":
+        """Between iterations (reference ``core/buffer.py:606-637``): new penalties and the given
+        (context, decode) count rows at `positions` (or in order)."""
+
+        self.populate(multiplicative, frequency, presence, positions).transfer(positions, stream)
+        self.counts.update(counts, positions, stream)
+
+        return self
+
+    def allocate(self, encodings: List[Tensor], multiplicative: List[float], frequency: List[float],
+                 presence: List[float], positions: List[int], stream=None) -> "RepetitionPenalties":
+        """Request admission (reference ``core/buffer.py:639-670``): penalties plus the prompts'
+        context histograms at `positions`."""
+
+        self.populate(multiplicative, frequency, presence, positions).transfer(positions, stream)
+        self.counts.allocate(encodings, positions, stream)
+
+        return self
+
     def subset(self, indices: Tensor) -> "RepetitionPenalties":
 
         return RepetitionPenalties(
@@ -306,6 +518,31 @@ class PinnedRelay(SliceBuffer):
             int_values=_pinned((2, size), I32).T,
             layout=Layout(size, timesteps),
         )
+
+    def update_bias(self, biases: List[Optional[dict]], positions: Optional[List[int]]) -> "PinnedRelay":
+        """Rebuilds the staged bias row of every position with a bias map ({token: bias}): the row
+        is cleared, then the map's entries are written (rows without a map are left alone)."""
+
+        for i, mapping in zip(_rows(positions, len(biases)), biases):
+
+            if mapping:
+
+                row = self.bias[i].zero_()
+                row.index_copy_(0, torch.tensor(list(mapping.keys()), dtype=I64),
+                                torch.tensor(list(mapping.values()), dtype=BF16))
+
+        return self
+
+    def populate(self, biases: List[Optional[dict]], temperature: List[float], top_k: List[int],
+                 top_p: List[float], min_p: List[float], top_logprobs: List[int],
+                 positions: Optional[List[int]] = None) -> "PinnedRelay":
+        """Stages (temperature, top_p, min_p), (top_k, top_logprobs) and the bias maps of the
+        given rows (reference ``core/buffer.py:738-764``)."""
+
+        _stage(self.float_values, torch.tensor([temperature, top_p, min_p], dtype=BF16).T, positions)
+        _stage(self.int_values, torch.tensor([top_k, top_logprobs], dtype=I32).T, positions)
+
+        return self.update_bias(biases, positions) if any(biases) else self
 
 
 def ensure_top_logprobs(indicators, maximum: int):
@@ -545,3 +782,124 @@ class SamplingBuffers(SliceBuffer):
                     event.record(stream)
 
         return self
+
+    def step_weights(self, positions: List[int], indices: Optional[Tensor] = None, generator=None,
+                     stream=None, event=None) -> "SamplingBuffers":
+        """After each decode iteration (reference ``core/buffer.py:1054-1096``): when some of
+        `positions` samples stochastically, stage the drafter's noise of the device rows `indices`
+        into the verifier's and redraw the noise of `positions`; a no-op for greedy targets."""
+
+        scoped = self.flags.indicators.subset(positions)
+
+        if scoped.has_stochastic_target:
+
+            self.weights.step(positions=positions, scoped=scoped, indicator=self.flags.draft,
+                              indices=indices, generator=generator, stream=stream, event=event)
+
+        return self
+
+    def transfer(self, positions: Optional[List[int]], stream=None, event=None) -> "SamplingBuffers":
+        """Sends the staged bias rows, (temperature, top_p, min_p) and (top_k, top_logprobs) of
+        `positions` (all rows when None) to the device, then records `event`."""
+
+        relay = self.pinned
+        _send(self.bias, relay.bias, positions, stream)
+
+        for column, member in enumerate((self.temperature, self.top_p, self.min_p)):
+
+            _send(member, relay.float_values[:, column], positions, stream)
+
+        for column, member in enumerate((self.top_k, self.top_logprobs)):
+
+            _send(member, relay.int_values[:, column], positions, stream)
+
+        if event is not None:
+
+            event.record(stream)
+
+        return self
+
+    def _admit(self, scoped: ScopedIndicators, positions, stream, biases, temperature, top_k, top_p,
+               min_p, top_logprobs) -> None:
+        """Indicators and the non-repetition parameters of `positions` into the relays."""
+
+        self.flags.update(indicators=scoped, positions=positions, stream=stream)
+        self.pinned.populate(biases=biases, temperature=temperature, top_k=top_k, top_p=top_p,
+                             min_p=min_p, top_logprobs=top_logprobs, positions=positions)
+
+    def update(self, counts: List[Tuple[Tensor, Tensor]], target_gumbel: List[Optional[Tensor]],
+               multiplicative: List[float], frequency: List[float], presence: List[float],
+               biases: List[Optional[dict]], temperature: List[float], top_k: List[int],
+               top_p: List[float], min_p: List[float], top_logprobs: List[int],
+               positions: Optional[List[int]] = None, indicators=None, greedy_drafts=False,
+               prefill=False, bitmasks: Optional[List[Optional[Tensor]]] = None, stream=None,
+               generator=None):
+        """Refreshes every parameter of `positions` (or of the first len(counts) rows) between
+        iterations (reference ``core/buffer.py:1139-1237``), for engines that compose the batch
+        anew each step: grammar, indicators (from the parameters unless given as (target, draft)
+        pairs), biases, sampling parameters, penalties with their counts and, for stochastic
+        targets, fresh noise (``target_gumbel`` rows replace the verifier's noise). With a
+        `stream` the copies run on it and the returned event marks their end."""
+
+        event = torch.cuda.Event() if stream is not None else None
+        self.step_grammar(bitmasks, positions, stream=stream)
+
+        if indicators is None:
+
+            scoped = ScopedIndicators.from_params(
+                size=len(counts), timesteps=self.layout.cols, multiplicative=multiplicative,
+                frequency=frequency, presence=presence, biases=biases, temperature=temperature,
+                top_k=top_k, top_p=top_p, min_p=min_p, top_logprobs=top_logprobs, bitmasks=bitmasks,
+                greedy_drafts=greedy_drafts)
+
+        else:
+
+            scoped = ScopedIndicators.from_pairs(indicators, timesteps=self.layout.cols)
+
+        self._admit(scoped, positions, stream, biases, temperature, top_k, top_p, min_p, top_logprobs)
+        self.repetition.update(counts=counts, multiplicative=multiplicative, frequency=frequency,
+                               presence=presence, positions=positions, stream=stream)
+
+        if scoped.has_stochastic_target:
+
+            self.weights.update(generator=generator, selectors=scoped.stochastic_selectors,
+                                targets=target_gumbel, positions=positions, prefill=prefill, stream=stream)
+
+        self.transfer(positions, stream=stream, event=event)
+
+        return event
+
+    def allocate(self, encodings: List[Tensor], multiplicative: List[float], frequency: List[float],
+                 presence: List[float], biases: List[Optional[dict]], temperature: List[float],
+                 top_k: List[int], top_p: List[float], min_p: List[float], top_logprobs: List[int],
+                 positions: List[int], indicators: Optional[ScopedIndicators] = None,
+                 greedy_drafts=False, bitmasks: Optional[List[Optional[Tensor]]] = None, stream=None,
+                 generator=None):
+        """Admits requests into the slots `positions` (reference ``core/buffer.py:1239-1352``), all
+        inputs host-resident: the prompts' token histograms (`encodings`, int64 ids) become the
+        context counts and the decode counts restart at zero, step 0 of the grammar takes
+        `bitmasks`, the indicators follow from the parameters (unless given), and stochastic
+        targets get their prefill noise. With a `stream` the copies run on it and the returned
+        event marks their end."""
+
+        event = torch.cuda.Event() if stream is not None else None
+        self.step_grammar(bitmasks, positions, timestep=0, stream=stream)
+
+        scoped = indicators if indicators is not None else ScopedIndicators.from_params(
+            size=len(encodings), timesteps=self.layout.cols, multiplicative=multiplicative,
+            frequency=frequency, presence=presence, biases=biases, temperature=temperature,
+            top_k=top_k, top_p=top_p, min_p=min_p, top_logprobs=top_logprobs, bitmasks=bitmasks,
+            greedy_drafts=greedy_drafts)
+
+        self._admit(scoped, positions, stream, biases, temperature, top_k, top_p, min_p, top_logprobs)
+        self.repetition.allocate(encodings=encodings, multiplicative=multiplicative, frequency=frequency,
+                                 presence=presence, positions=positions, stream=stream)
+
+        if scoped.has_stochastic_target:
+
+            self.weights.update(generator=generator, selectors=scoped.stochastic_selectors,
+                                positions=positions, prefill=True, stream=stream)
+
+        self.transfer(positions, stream=stream, event=event)
+
+        return event

@@ -44,7 +44,7 @@ def test_header_declares_the_entry_points():
 
     names = declared_functions()
 
-    for required in ("ss_topk", "ss_fused_singular", "ss_fused_multistep", "ss_gumbel_materialize",
+    for required in ("ss_topk", "ss_fused_singular", "ss_fused_multistep", "ss_indexed_copy", "ss_gumbel_materialize",
                      "ss_philox_raw", "ss_abi_version", "ss_status_string", "ss_args_size"):
 
         assert required in names
@@ -67,7 +67,8 @@ def test_abi_version_and_struct_sizes():
     assert lib.ss_args_size(0) == ctypes.sizeof(_native.TopKArgs)
     assert lib.ss_args_size(1) == ctypes.sizeof(_native.SingularArgs)
     assert lib.ss_args_size(2) == ctypes.sizeof(_native.MultistepArgs)
-    assert lib.ss_args_size(3) == -1
+    assert lib.ss_args_size(3) == ctypes.sizeof(_native.IndexedCopyArgs)
+    assert lib.ss_args_size(4) == -1
 
 
 def test_status_strings():

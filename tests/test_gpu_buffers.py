@@ -1,0 +1,66 @@
+"""ss_indexed_copy (the reference's indexed_copy, ops/copy.py:21-127) and the GPU weight step of
+SamplingBuffers against torch's indexing."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+BF16 = torch.bfloat16
+
+
+@pytest.mark.parametrize("vocab", [4096, 1001])
+def test_indexed_copy_stages_stochastic_slots(vocab):
+    """16-byte rows (V = 4096) and rows of an odd width (3 x 1001 elements, element copies);
+    greedy slots keep their target rows and indices outside the slots are skipped."""
+
+    from sonic_sampler import _native
+
+    slots, steps = 10, 3
+    g = torch.Generator().manual_seed(vocab)
+    draft = torch.randn(slots, steps, vocab, generator=g).to(BF16)
+    target = torch.randn(slots, steps, vocab, generator=g).to(BF16)
+    indicators = torch.tensor([0x40 if i % 3 == 0 else 0x80 for i in range(slots)], dtype=torch.int32)
+    indices = torch.tensor([7, 3, 0, 9, 5, 12, -1], dtype=torch.int64)
+    expected = target.clone()
+
+    for i in indices.tolist():
+
+        if 0 <= i < slots and not indicators[i] & 0x40:
+
+            expected[i] = draft[i]
+
+    got = target.to(DEV)
+    print(f"indexed copy V={vocab}", flush=True)
+    _native.indexed_copy(draft.to(DEV), got, indices.to(DEV), indicators.to(torch.uint16).to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), expected)
+
+
+def test_step_weights_on_device_buffers():
+
+    from bench import to_device
+    from sonic_sampler.core.buffer import SamplingBuffers
+
+    host = SamplingBuffers.random(size=8, timesteps=3, vocab_size=2048, device="cpu", seed=4)
+    b = to_device(host, DEV)
+    positions = [6, 1, 3]
+    draft = b.weights.gumbel.draft.clone()
+    target = b.weights.gumbel.target.clone()
+    print("step_weights on device buffers", flush=True)
+    b.step_weights(positions=positions, indices=torch.tensor(positions, device=DEV),
+                   generator=torch.Generator(DEV).manual_seed(1))
+    torch.cuda.synchronize()
+    scoped = host.flags.indicators
+
+    for i in range(8):
+
+        if i not in positions:
+
+            assert torch.equal(b.weights.gumbel.target[i], target[i])
+            assert torch.equal(b.weights.gumbel.draft[i], draft[i])
+
+        elif int(scoped.draft[i]) & 0x40 == 0:
+
+            assert torch.equal(b.weights.gumbel.target[i], draft[i])

@@ -219,3 +219,24 @@ def test_fused_multistep_layout_errors():
                         cu_seqlens=torch.tensor([0, 5, 10], dtype=torch.int32))
     with pytest.raises(ValueError, match="63"):
         fused_multistep(torch.zeros(2, 65, 8192, dtype=torch.bfloat16), flags, drafted, block_n=1024)
+
+
+def test_autotune_ranks_widths_and_round_trips(tmp_path):
+    """The table the autotune harness writes ranks each bucket's widths by the measured time,
+    skips widths that leave a single tile, and reads back through DispatchSummary."""
+
+    from sonic_sampler.interface.autotune import autotune
+    from sonic_sampler.interface.dispatch import DispatchSummary
+
+    best = {8192: 1024, 131072: 4096}
+    fake = lambda v, b, w: abs(w - (8192 if b >= 256 else best[v])) + 1.0  # noqa: E731
+    summary = autotune([8192, 131072], [1, 64, 512], measure=fake, arch="gfx950")
+    path = tmp_path / "gfx950_k128.toml"
+    summary.save(path)
+    back = DispatchSummary.read(path)
+
+    small = back.vocab.get(8192)
+    assert [c.block_n for c in small.batch.get(1).config] == [1024, 2048, 4096]   # 8192 leaves one tile
+    assert back.vocab.get(131072).batch.get(64).best.block_n == 4096
+    assert back.vocab.get(131072).batch.get(300).best.block_n == 8192
+    assert [c.priority for c in back.vocab.get(131072).batch.get(1).config] == [0, 1, 2, 3]

@@ -273,36 +273,6 @@ __device__ __forceinline__ void wave_sort128_desc(uint64_t &a0, uint64_t &a1) {
     wave_bitonic128_desc<2>(a0, a1);
 }
 
-// One merge size of the 256-element network of wave_sort256_desc.
-template <int SIZE>
-__device__ __forceinline__ void bitonic256_size(uint32_t (&v)[4]) {
-    const int lane = lane_id();
-    if constexpr (SIZE >= 8) {
-        bitonic_lane_steps<SIZE / 8, SIZE / 4>(v);
-    }
-#pragma unroll
-    for (int dist = (SIZE >= 4 ? 2 : 1); dist > 0; dist >>= 1) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int p = r ^ dist;
-            if (p > r) {
-                const bool desc = ((4 * lane + r) & SIZE) == 0;
-                const uint32_t hi = max(v[r], v[p]), lo = min(v[r], v[p]);
-                v[r] = desc ? hi : lo;
-                v[p] = desc ? lo : hi;
-            }
-        }
-    }
-}
-
-template <int SIZE = 2>
-__device__ __forceinline__ void bitonic256_from(uint32_t (&v)[4]) {
-    if constexpr (SIZE <= 256) {
-        bitonic256_size<SIZE>(v);
-        bitonic256_from<SIZE * 2>(v);
-    }
-}
-
 // Sorts 64 values held by one wave (one per lane, element = lane) in descending order.
 __device__ __forceinline__ void wave_sort64_desc(uint32_t &v) {
     uint32_t a[1] = {v};
@@ -314,10 +284,5 @@ __device__ __forceinline__ void wave_sort64_desc(uint32_t &v) {
     bitonic_lane_steps<32, 64>(a);
     v = a[0];
 }
-
-// Sorts 256 32-bit values held by one wave (element e = 4 * lane + r in v[r]) in descending
-// order with a bitonic network: in-lane exchanges for element distances 1 and 2, lane
-// permutations for the larger ones.
-__device__ __forceinline__ void wave_sort256_desc(uint32_t (&v)[4]) { bitonic256_from<2>(v); }
 
 }  // namespace ss

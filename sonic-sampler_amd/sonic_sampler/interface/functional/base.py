@@ -12,7 +12,7 @@ from torch import Tensor
 
 from sonic_sampler import _native
 from sonic_sampler.interface.base import SUPPORTED_BLOCK_N
-from sonic_sampler.ops.base import MAX_K, next_power_of_2
+from sonic_sampler.ops.base import MAX_K
 
 U32 = torch.uint32
 I32 = torch.int32
@@ -58,22 +58,6 @@ def resolve_scratchpad(logits: Tensor, block_n: int, buffer: Optional[Tensor] = 
         raise ValueError("scratchpad too small for the given logits and block_n")
 
     return (rows, vocab_blocks), (rows,), scratchpad, vocab_blocks
-
-
-def conditional_stride(*data: Optional[Tensor]) -> Optional[int]:
-
-    for tensor in data:
-
-        if tensor is not None:
-
-            return tensor.stride(0)
-
-    return None
-
-
-def resolve_block(data: Optional[Tensor], dim: int) -> Optional[int]:
-
-    return next_power_of_2(data.size(dim)) if data is not None else None
 
 
 def collapse_2d(value: Tensor) -> Tensor:

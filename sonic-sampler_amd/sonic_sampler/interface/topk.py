@@ -1,7 +1,8 @@
 """Standalone bounded top-k (reference ``interface/topk.py:39-161``).
 
-One launch of ``ss_topk``: tile-local exact top-k for every (row, tile) workgroup, merged and
-sorted by the last workgroup of each row. Ties go to the lowest column. bfloat16 and float32 logits
+``ss_topk`` makes two launches: a tile stage that writes the exact top-k of every (row, tile)
+workgroup as a sorted candidate list, then a merge stage that takes the row's top-k from those
+lists in descending order. Ties go to the lowest column. bfloat16 and float32 logits
 are accepted; values come back in the logits' dtype.
 
 Returned ``values`` / ``indices`` are dense ``[..., k]`` views of the interface's buffers. (The

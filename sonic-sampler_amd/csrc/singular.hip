@@ -67,7 +67,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
     if (MODE != MODE_DIRECT && stage_words > 0) {
         const Uses u = row_uses(rs);
         if (u.g && u.remap) {
-            stage_grammar(rs.grammar, stage_words, grammar_words);
+            stage_grammar(rs.grammar, rs.vt, grammar_words);
             rs.glds = grammar_words;
             sync = true;
         }
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rowwise_kernel(ss_singular_
     RowState rs = singular_row_state(a, row, slot, ind);
     const Uses u = row_uses(rs);
     if (stage_words > 0 && u.g && u.remap) {
-        stage_grammar(rs.grammar, stage_words, grammar_words);
+        stage_grammar(rs.grammar, rs.vt, grammar_words);
         rs.glds = grammar_words;
     }
     if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
@@ -297,10 +297,16 @@ static int staged_grammar_words(const ss_singular_args *a) {
     return (a->d2t && a->grammar && words <= SS_STAGE_MAX_WORDS) ? words : 0;
 }
 
+// Workgroup memory of a staged grammar row (stage_grammar): its quads and one quad of zeros.
+static size_t staged_grammar_bytes(const ss_singular_args *a) {
+    const int vt = a->target_vocab > 0 ? a->target_vocab : a->vocab_size;
+    return staged_grammar_words(a) ? (size_t)(stage_quads(vt) + 1) * 16 : 0;
+}
+
 template <int MODE>
 static int launch_rowwise(const ss_singular_args *a, int tiles) {
     const int stage = staged_grammar_words(a);
-    const size_t dyn = (size_t)((stage + 3) & ~3) * sizeof(uint32_t);
+    const size_t dyn = staged_grammar_bytes(a);
     dim3 grid((unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
@@ -319,7 +325,7 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     const int stage = staged_grammar_words(a);
-    const size_t dyn = (size_t)((stage + 3) & ~3) * sizeof(uint32_t);
+    const size_t dyn = staged_grammar_bytes(a);
     const int stages = a->stages ? a->stages : (SS_STAGE_TILES | SS_STAGE_ROWS);
     if (stages & SS_STAGE_TILES) {
         switch (a->block_n) {

@@ -556,6 +556,12 @@ __device__ __forceinline__ void plain_keys(const RowState &rs, const Uses &u, in
 }
 
 // General layout: d2t-remapped columns (gathers through the target vocabulary) or unaligned rows.
+// Largest grammar row that stage_grammar copies into workgroup memory, and the 16-byte quads it
+// stages for a vt-token vocabulary.
+constexpr int SS_STAGE_MAX_WORDS = 8192;
+
+__host__ __device__ __forceinline__ int stage_quads(int vt) { return (((vt + 31) >> 5) + 3) >> 2; }
+
 template <int E, bool VEC>
 __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, int col0, int V,
                                             const int32_t *hist, const u32x2 (&lw)[E / 4],
@@ -618,15 +624,31 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                 for (int j = 0; j < E; ++j) tcol[j] = __builtin_amdgcn_raw_buffer_load_b32(m, tcol[j] * 4, 0, 0);
             }
         }
-        if (u.g) {
-            const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
+        // a masked element becomes bf16 -inf (0xff80) in place; a column outside the target
+        // vocabulary (negative, or at or past it) reads 0 (masked) on either path
+        if (u.g && rs.glds) {
+            // Staged row (stage_grammar): a column is clamped to lim, the first bit of the zero
+            // words past the row, and the bits past the vocabulary in its last word are clear,
+            // so the lookup needs no range branch. The pair's two keep bits become a 16-bit mask
+            // per half that selects between the pair and two -inf halves.
             const lds_cu32p gl = (lds_cu32p)rs.glds;
+            const uint32_t lim = (uint32_t)(stage_quads(rs.vt) * 128);
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i) {
+                const uint32_t t0 = min((uint32_t)tcol[2 * i], lim), t1 = min((uint32_t)tcol[2 * i + 1], lim);
+                const uint32_t b0 = (gl[t0 >> 5] >> (t0 & 31)) & 1u;
+                const uint32_t b1 = (gl[t1 >> 5] >> (t1 & 31)) & 1u;
+                const uint32_t keep = ((b1 << 16) | b0) * 0xffffu;
+                const uint32_t p = (i & 1) ? lv[i >> 1].y : lv[i >> 1].x;
+                const uint32_t m = (p & keep) | (0xff80ff80u & ~keep);
+                if (i & 1) lv[i >> 1].y = m; else lv[i >> 1].x = m;
+            }
+        } else if (u.g) {
+            const __amdgpu_buffer_rsrc_t g = row_buffer(rs.grammar, (int64_t)((rs.vt + 31) >> 5) * 4);
 #pragma unroll
             for (int j = 0; j < E; ++j) {
-                // a masked element becomes bf16 -inf (0xff80) in place; a column outside the
-                // target vocabulary reads 0 (masked) on either path
-                const uint32_t w = rs.glds ? ((uint32_t)tcol[j] < (uint32_t)rs.vt ? gl[tcol[j] >> 5] : 0u)
-                                           : __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0);
+                const uint32_t w = (uint32_t)tcol[j] < (uint32_t)rs.vt
+                                       ? __builtin_amdgcn_raw_buffer_load_b32(g, (tcol[j] >> 5) * 4, 0, 0) : 0u;
                 const bool keep = ((w >> (tcol[j] & 31)) & 1u) != 0u;
                 uint32_t p = (j & 2) ? lv[j >> 2].y : lv[j >> 2].x;
                 p = keep ? p : (j & 1) ? ((p & 0x0000ffffu) | 0xff800000u) : ((p & 0xffff0000u) | 0xff80u);
@@ -670,14 +692,19 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                    dec, ctx, bb, bw, keys);
 }
 
-// Copies the row's `words` grammar words into workgroup memory `dst` (16-byte aligned, at least
-// `words` rounded up to 4 entries): one round of 16-byte loads, at most 8 per thread (words <= 8192),
-// all issued before any is stored. The caller synchronizes the workgroup before reading `dst`.
-constexpr int SS_STAGE_MAX_WORDS = 8192;
-
-__device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int words, uint32_t *dst) {
+// Copies the grammar row of a `vt`-token vocabulary (ceil(vt / 32) words) into workgroup memory
+// `dst` (16-byte aligned, 4 * (stage_quads(vt) + 1) words): one round of 16-byte loads, at most 8
+// per thread (at most SS_STAGE_MAX_WORDS words), all issued before any is stored. The bits past
+// the vocabulary in the last word are cleared, the words past it up to the next multiple of 4
+// read 0 (the load's range check) and one more quad of zeros follows, so every column at or past
+// vt clamped to 128 * stage_quads(vt) reads a clear bit. The caller synchronizes the workgroup
+// before reading `dst`.
+__device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int vt, uint32_t *dst) {
+    const int words = (vt + 31) >> 5;
     const __amdgpu_buffer_rsrc_t g = row_buffer(grammar, (int64_t)words * 4);
-    const int quads = (words + 3) >> 2;
+    const int quads = stage_quads(vt);
+    const int last = vt >> 5;                               // the word holding bit vt
+    const uint32_t keep = (1u << (vt & 31)) - 1u;           // its bits below vt (0: vt % 32 == 0)
     i32x4 q[SS_STAGE_MAX_WORDS / 4 / SS_BLOCK];
 #pragma unroll
     for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
@@ -687,8 +714,17 @@ __device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int words
 #pragma unroll
     for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
         const int w4 = (int)threadIdx.x + i * SS_BLOCK;
+        if (w4 == last >> 2) {
+            // a word past the row (vt % 32 == 0) reads 0 already
+            const int c = last & 3;
+            q[i].x = c == 0 ? q[i].x & keep : q[i].x;
+            q[i].y = c == 1 ? q[i].y & keep : q[i].y;
+            q[i].z = c == 2 ? q[i].z & keep : q[i].z;
+            q[i].w = c == 3 ? q[i].w & keep : q[i].w;
+        }
         if (w4 < quads) *(i32x4 *)(dst + 4 * w4) = q[i];
     }
+    if (threadIdx.x == 0) *(i32x4 *)(dst + 4 * quads) = i32x4{0, 0, 0, 0};
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:
@@ -1137,6 +1173,66 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, con
     smp.greedy = (t < 64 && t < tiles) ? scr[lm.greedy_entry(t)] : 0u;
 }
 
+// Lists that merge_refill merges whole; a row with more lists beating its sampled top-128 takes
+// the radix merge.
+constexpr int SS_REFILL_LISTS = 16;
+
+// Completes an inexact sampled merge (wave 0; `f0`/`f1` hold the sorted top-128 of the samples as
+// slot composites). They are rewritten as entry composites (key << 16) | (0xffff - g) with
+// g = list * 128 + position (< 2^16 for tiles <= 512), whose order is again (value desc, column
+// asc). Then, list by list in tile order, a list whose first unmerged entry beats the current
+// 128th element has its remaining 128 - kp entries merged in: the elementwise maximum of the
+// sorted top-128 and the list's entries in reverse order is bitonic and holds the top-128 of
+// both. The 128th element only rises, so a list that does not beat it when visited never does
+// later, and every list that did is merged whole: the result is the row's exact top-128.
+__device__ __forceinline__ void merge_refill(const uint32_t *scr, const RowSamples &smp, int tiles,
+                                             const ListMap &lm, int V, uint32_t f0, uint32_t f1,
+                                             float &v0, float &v1, int &i0, int &i1) {
+    const int lane = lane_id();
+    const int kp = smp.kp;
+    auto to_entry = [&](uint32_t f) -> uint32_t {
+        if (!f) return 0u;
+        const int s = (int)(0xffffu - (f & 0xffffu));
+        const int l = slot_list(smp, s);
+        return (f & 0xffff0000u) | (0xffffu - (uint32_t)(l * SS_K + s - l * kp));
+    };
+    f0 = to_entry(f0);
+    f1 = to_entry(f1);
+    for (int t0 = 0; t0 < tiles; t0 += 64) {
+        const int t = t0 + lane;
+        const uint32_t nx = t >= tiles ? 0u : t < 64 ? smp.next : scr[t * SS_K + kp];
+        const uint32_t cn = nx ? (nx & 0xffff0000u) | (0xffffu - (uint32_t)(t * SS_K + kp)) : 0u;
+        uint64_t m = __ballot(cn > lane_u32(f1, 63));
+        while (m) {
+            const int l = t0 + (int)__builtin_ctzll(m);
+            uint32_t r[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                // element e pairs with entry kp + 127 - e of list l (entries kp .. 127 exist)
+                const int e = 2 * lane + i;
+                const int g = l * SS_K + kp + 127 - e;
+                const uint32_t raw = e >= kp ? scr[g] : 0u;
+                r[i] = raw ? (raw & 0xffff0000u) | (0xffffu - (uint32_t)g) : 0u;
+            }
+            f0 = max(f0, r[0]);
+            f1 = max(f1, r[1]);
+            wave_bitonic128_desc<128>(f0, f1);
+            m &= m - 1;
+            m &= __ballot(cn > lane_u32(f1, 63));
+        }
+    }
+    auto column = [&](uint32_t f) -> int {
+        if (!f) return V - 1;
+        const int g = (int)(0xffffu - (f & 0xffffu));
+        const int idx = lm.base(g >> 7) + (int)(0xffffu - (scr[g] & 0xffffu));
+        return idx < V ? idx : V - 1;
+    };
+    v0 = bf2f(unkey16(f0 >> 16));
+    v1 = bf2f(unkey16(f1 >> 16));
+    i0 = column(f0);
+    i1 = column(f1);
+}
+
 // Row merge over the tiles' sorted candidate lists, from the samples of load_samples. All threads
 // call; on return wave 0 holds the row's top-128 sorted by (value desc, column asc), element
 // e = 2 * lane + i as (v_i, idx_i).
@@ -1145,9 +1241,11 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, con
 // slot s = list * kp + position, as composites (key << 16) | (0xffff - s), whose order is the
 // (value desc, column asc) order because lists are in tile order and equal keys of one list are
 // in column order. Each wave sorts 128 slots (from merge size 2 kp when whole lists fill its
-// elements, see merge_run), and two rounds of bitonic merges keep the top-128 of the four runs. The result is exact unless some list holds more than kp of the row's top-128,
-// i.e. unless a list's first unmerged entry beats the 128th merged one; that case (rare: 17 of the
-// top-128 in one of 32 tiles) falls back to the radix merge over every candidate.
+// elements, see merge_run), and two rounds of bitonic merges keep the top-128 of the four runs.
+// The result is exact unless some list holds more than kp of the row's top-128, i.e. unless a
+// list's first unmerged entry beats the 128th merged one. Up to SS_REFILL_LISTS such lists are
+// merged whole by merge_refill; more (or tiles > 512) fall back to the radix merge over every
+// candidate.
 __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
                                           const RowSamples &smp, int tiles, const ListMap &lm, int V,
                                           float &v0, float &v1, int &i0, int &i1) {
@@ -1191,6 +1289,7 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
     }
     __syncthreads();
     uint32_t f0 = 0, f1 = 0;
+    int beats = 0;
     if (wave == 0) {
         f0 = max(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
         f1 = max(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
@@ -1201,23 +1300,26 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
         const uint32_t last = lane_u32(f1, 63);
         const uint32_t klast = last >> 16;
         const int llast = last ? slot_list(smp, (int)(0xffffu - (last & 0xffffu))) : tiles;
-        bool beat = false;
         if (kp < SS_K) {
-            for (int t = lane; t < tiles; t += 64) {
-                const uint32_t nx = t < 64 ? smp.next : scr[t * SS_K + kp];
+            for (int t0 = 0; t0 < tiles; t0 += 64) {
+                const int t = t0 + lane;
+                const uint32_t nx = t >= tiles ? 0u : t < 64 ? smp.next : scr[t * SS_K + kp];
                 const uint32_t kn = nx >> 16;
-                beat |= nx != 0u && (kn > klast || (kn == klast && t < llast));
+                beats += __popcll(__ballot(nx != 0u && (kn > klast || (kn == klast && t < llast))));
             }
         }
-        const bool any = __ballot(beat) != 0;
-        if (lane == 0) sm.flag = any ? 1 : 0;
+        if (lane == 0) sm.flag = beats > SS_REFILL_LISTS || (beats > 0 && kp == 0) ? 1 : 0;
+    }
+    if (beats > 0 && beats <= SS_REFILL_LISTS && kp > 0) {
+        // wave 0 only (beats is 0 in the other waves)
+        merge_refill(scr, smp, tiles, lm, V, f0, f1, v0, v1, i0, i1);
     }
     __syncthreads();
     if (sm.flag) {
         merge_row_radix(sm, scr, tiles, lm, V, v0, v1, i0, i1);
         return;
     }
-    if (wave == 0) {
+    if (wave == 0 && beats == 0) {
         v0 = bf2f(unkey16(f0 >> 16));
         v1 = bf2f(unkey16(f1 >> 16));
         i0 = f0 ? sm.col[0xffffu - (f0 & 0xffffu)] : V - 1;

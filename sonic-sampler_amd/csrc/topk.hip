@@ -3,9 +3,11 @@
 //
 // Tile stage, grid rows * tiles: each workgroup turns block_n logits into order-preserving keys
 // and writes its exact top-k (ties to the lowest column) to the scratch row in column order.
-// Merge stage, grid rows: selects the row's top-k among the tiles * k candidates, sorts them by
-// (value desc, column asc) with a wave64 bitonic network and writes values / indices densely as
-// [rows, k].
+// Merge stage, grid rows: selects the row's top-k among the tiles * k candidates from a sample of
+// at most 512 (the first entries of every sorted list), completed list by list where the sample
+// was not exact and by a radix selection over every candidate where many lists were cut short;
+// sorts them by (value desc, column asc) with wave64 bitonic networks and writes values / indices
+// densely as [rows, k].
 #include "ss_sampling.h"
 #include "../../include/sonic_sampler.h"
 
@@ -16,7 +18,11 @@ struct TopkSmem {
     uint64_t cand[SS_K];
     int32_t idx[SS_K];
     uint64_t runs[SS_WAVES][SS_K];  // merge of up to 512 candidates: the waves' sorted runs
+    int32_t flag;                   // the sampled merge was not exact: take the radix merge
 };
+
+// Lists that the merge stage merges whole after its sampled merge before it takes the radix merge.
+constexpr int TOPK_REFILL_LISTS = 16;
 
 template <bool F32>
 struct TopkTraits;
@@ -58,24 +64,28 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
     const int k = a.k;
     const Cand *scr = (const Cand *)a.scratch + (int64_t)row * a.stride_scratch;
     const int ncand = tiles * k;
-    if (ncand <= 2 * SS_BLOCK) {
-        // Up to 512 candidates, two per thread, as composites (key << 32) | (~column): their
+    // Samples: the first kp entries of every sorted list, kp = k when all tiles * k candidates
+    // fit in 512 slots, else the largest power of two <= 512 / tiles (0 above 512 tiles).
+    const int kp = ncand <= 2 * SS_BLOCK ? k
+                   : tiles <= 2 * SS_BLOCK ? 1 << (31 - __builtin_clz((unsigned)(2 * SS_BLOCK / tiles))) : 0;
+    if (kp > 0) {
+        // Up to 512 samples, two per thread, as composites (key << 32) | (~column): their
         // descending order is (value desc, column asc). Every wave sorts its 128, and two rounds
         // of bitonic merges keep the top-128 of the four runs (the elementwise maximum of a run
         // and its reversed partner is a bitonic sequence holding the top-128 of both).
         const int lane = lane_id(), wave = (int)threadIdx.x >> 6;
-        const int lk = __builtin_ctz((unsigned)k);  // k is a power of two
+        const int lk = __builtin_ctz((unsigned)k), lkp = __builtin_ctz((unsigned)kp);  // powers of two
+        auto composite = [&](int p) {
+            const Cand cd = scr[p];
+            const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
+            return ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
+        };
         uint64_t c[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int p = 2 * (int)threadIdx.x + i;
-            uint64_t v = 0;
-            if (p < ncand) {
-                const Cand cd = scr[p];
-                const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
-                v = ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
-            }
-            c[i] = v;
+            const int s = 2 * (int)threadIdx.x + i;
+            const int list = s >> lkp;
+            c[i] = list < tiles ? composite(list * k + (s & (kp - 1))) : 0ull;
         }
         wave_sort128_desc(c[0], c[1]);
         sm.runs[wave][2 * lane] = c[0];
@@ -95,23 +105,67 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
             f[0] = max_u64(sm.runs[0][2 * lane], sm.runs[2][127 - 2 * lane]);
             f[1] = max_u64(sm.runs[0][2 * lane + 1], sm.runs[2][126 - 2 * lane]);
             wave_bitonic128_desc<128>(f[0], f[1]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int e = 2 * lane + i;
-                if (e < k) {
-                    const uint32_t key = (uint32_t)(f[i] >> 32);
-                    const int col = (int)(0xffffffffu - (uint32_t)f[i]);
-                    const int64_t o = (int64_t)row * k + e;
-                    if (F32) {
-                        ((float *)a.values)[o] = __uint_as_float(unkey32(key));
-                    } else {
-                        ((uint16_t *)a.values)[o] = (uint16_t)unkey16(key);
-                    }
-                    a.indices[o] = col < V ? col : V - 1;
+            // the k-th merged composite (element k - 1)
+            auto kth = [&]() {
+                const uint64_t x = ((k - 1) & 1) ? f[1] : f[0];
+                const int src = (k - 1) >> 1;
+                return ((uint64_t)__builtin_amdgcn_readlane((int)(x >> 32), src) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, src);
+            };
+            // Exactness: no list's first unsampled entry may beat the k-th merged composite. Up
+            // to TOPK_REFILL_LISTS lists that do are merged whole, in list order, each against
+            // the current k-th (which only rises, so a list passed over never beats it later):
+            // the elementwise maximum of the sorted top-128 and the list's remaining k - kp
+            // entries in reverse order is bitonic and holds the top-128 of both.
+            int beats = 0;
+            if (kp < k) {
+                const uint64_t last = kth();
+                for (int t0 = 0; t0 < tiles; t0 += 64) {
+                    const int t = t0 + lane;
+                    beats += __popcll(__ballot(t < tiles && composite(t * k + kp) > last));
                 }
             }
+            if (beats > TOPK_REFILL_LISTS) {
+                if (lane == 0) sm.flag = 1;
+            } else {
+                for (int t0 = 0; beats > 0 && t0 < tiles; t0 += 64) {
+                    const int t = t0 + lane;
+                    const uint64_t nx = t < tiles ? composite(t * k + kp) : 0ull;
+                    uint64_t m = __ballot(nx > kth());
+                    while (m) {
+                        const int l = t0 + (int)__builtin_ctzll(m);
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) {
+                            // element e pairs with entry kp + 127 - e of list l (kp .. k - 1 exist)
+                            const int e = 2 * lane + i;
+                            const uint64_t r = e >= SS_K - k + kp ? composite(l * k + kp + 127 - e) : 0ull;
+                            f[i] = max_u64(f[i], r);
+                        }
+                        wave_bitonic128_desc<128>(f[0], f[1]);
+                        m &= m - 1;
+                        m &= __ballot(nx > kth());
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int e = 2 * lane + i;
+                    if (e < k) {
+                        const uint32_t key = (uint32_t)(f[i] >> 32);
+                        const int col = (int)(0xffffffffu - (uint32_t)f[i]);
+                        const int64_t o = (int64_t)row * k + e;
+                        if (F32) {
+                            ((float *)a.values)[o] = __uint_as_float(unkey32(key));
+                        } else {
+                            ((uint16_t *)a.values)[o] = (uint16_t)unkey16(key);
+                        }
+                        a.indices[o] = col < V ? col : V - 1;
+                    }
+                }
+                if (lane == 0) sm.flag = 0;
+            }
         }
-        return;
+        __syncthreads();
+        if (!sm.flag) return;
     }
     uint32_t thi, margin;
     int level;
@@ -165,9 +219,10 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
 // blockIdx.x / tiles and its top-k goes to the scratch row as packed candidates for the merge
 // kernel; otherwise the block is the whole row (one launch) and the top-k is the output.
 //
-// Lower bound: every wave sorts its 64 lane maxima; at least k / 4 of its lanes hold a value >= the
-// (k / 4)-th largest of them, so with lo the smallest of the four waves' bounds the row holds at
-// least k values >= lo. The survivors (values >= lo: a few dozen on unstructured rows) are
+// Lower bound: every wave sorts its 64 lane maxima; at least need_w of its lanes hold a value >= the
+// need_w-th largest of them, with need_w the wave's share of k (k / 4 in a full block, in
+// proportion to its valid columns in a partial one, summing to at least k), so with lo the
+// smallest of the waves' bounds the block holds at least k values >= lo. The survivors (values >= lo: a few dozen on unstructured rows) are
 // collected per wave by a ballot at each element position, skipped uniformly where no lane of the
 // wave survives, as composites (key32 << 32) | ~column. Every wave sorts its survivors, two rounds
 // of bitonic merges keep the top-128 of the four runs, and the first k are written. A wave with more
@@ -253,10 +308,20 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
     for (int j = 1; j < E; ++j) m = fmaxf(m, v[j]);
     uint32_t mk = float_key(m);
     wave_sort64_desc(mk);
-    const int need = (k + SS_WAVES - 1) / SS_WAVES;
-    if (lane == need - 1) sm.red[wave] = mk;
+    // The wave's share of k is proportional to the valid columns it holds (chunk c gives it
+    // columns c * 1024 + 256 * wave .. + 255), so a partial last tile, whose columns sit in its
+    // first waves, still gets a bound; a wave without columns takes no part in the minimum, and
+    // a share above its 64 lanes leaves the bound to the exact selection.
+    int nw = 0;
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) nw += min(max(V - (c * (SS_BLOCK * 4) + 256 * wave), 0), 256);
+    const int need = nw ? (k * nw + V - 1) / V : 0;
+    if (need == 0 && lane == 0) sm.red[wave] = 0xffffffffu;
+    if (need > 64 && lane == 0) sm.red[wave] = 0u;
+    if (need > 0 && need <= 64 && lane == need - 1) sm.red[wave] = mk;
     __syncthreads();
     const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
+    const bool no_bound = lo == 0u;
     // the float whose key is lo (lo is the key of a lane maximum, so it is a value of the row)
     const float lo_f = __uint_as_float((lo & 0x80000000u) ? (lo & 0x7fffffffu) : ~lo);
     __syncthreads();
@@ -277,7 +342,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
     if (lane == 0) sm.red[wave] = cnt;
     __syncthreads();
     const bool overflow = max(max(sm.red[0], sm.red[1]), max(sm.red[2], sm.red[3])) > (uint32_t)SS_K ||
-                          V < k;
+                          V < k || no_bound;
     if (!overflow) {
         uint64_t c0 = 2 * lane < (int)cnt ? run[2 * lane] : 0ull;
         uint64_t c1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0ull;

@@ -1,11 +1,24 @@
-"""Measures a dispatch table for this GPU: for every (vocabulary, batch) bucket, the fused
-single-step call (every processor on, logprobs) is timed at each compiled tile width and the widths
-are written fastest first, as the priorities of the bucket's configurations. The table has the
-schema of the reference's generated tables (``resources/dispatch/sm100_k128.toml``, read by
-``interface/dispatch.py``); ``UnshardedFusedSingular`` / ``UnshardedFusedMultistep.initialize``
-pick the priority-0 width of the bucket of their row count.
+"""Measures a dispatch table for this GPU. For every (vocabulary, batch) bucket, each call kind
+that the table serves (``KINDS``: the fused single step with every processor on and logprobs, the
+drafting step through d2t into an 8x wider target vocabulary under a grammar mask, timed in the
+buckets of draft vocabularies (at most ``DRAFT_VOCAB_MAX`` columns), and the multistep
+verification at lookahead 3; ``"topk"``, the bounded top-128, on request) is timed at each
+compiled tile width. A width's score is its worst slowdown over the kinds (time / the
+kind's fastest time), and the bucket gets the widest width whose score is within ``TOLERANCE`` of
+the best (run-to-run noise is about that size, and a wider tile means a smaller scratchpad). The
+standalone top-k reads the same table, as in the reference; at k = 128 its tile kernel prefers
+wider tiles than the fused calls, so scoring it by default would slow the fused path it shares
+buckets with.
+
+The table has the schema of the reference's generated tables (``resources/dispatch/
+sm100_k128.toml``, read by ``interface/dispatch.py``), whose priorities rank one configuration per
+selection strategy; the gfx950 kernels have a single exact selection, so each bucket holds one
+configuration (priority 0) and the measured times go to the log. ``TwoStageTiling`` sizes its
+scratchpad for the smallest width of the vocabulary bucket and launches each call at the width of
+the bucket of its row count.
 
     python -m sonic_sampler.interface.autotune --out gfx950_k128.toml [--vocab 8192,32768 --batch 1,64]
+    [--kinds singular,multistep,topk]
 
 Tile strategies and warp counts are recorded with fixed values: the gfx950 kernels have one exact
 selection and 256-thread workgroups, so the tile width is the only tuned parameter.
@@ -37,48 +50,41 @@ from sonic_sampler.ops.base import MAX_K
 VOCAB_BUCKETS = (8192, 32768, 131072, 262144)
 BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
 WIDTHS = (1024, 2048, 4096, 8192)
+TOLERANCE = 0.02
 
-Measure = Callable[[int, int, int], float]
+KINDS = ("singular", "drafting", "multistep")
+ALL_KINDS = ("singular", "drafting", "multistep", "topk")
+LOOKAHEAD = 3
+DRAFT_VOCAB_MAX = 32768
+
+Measure = Callable[[str, int, int, int], float]
 
 
 @functools.lru_cache(maxsize=1)
-def _workload(vocab: int, batch: int, device: str, seed: int):
-    """Logits and buffers of one bucket (the last one is kept, so the widths of a bucket share
-    them): N(0, 3^2) logits, every processor but the grammar on, logprobs."""
+def _workload(vocab: int, rows: int, device: str, seed: int):
+    """Logits, drafted tokens and buffers of one bucket (the last one is kept, so the widths and
+    kinds of a bucket share them): N(0, 3^2) logits, every processor but the grammar on."""
 
     from sonic_sampler.core.buffer import SamplingBuffers
     from sonic_sampler.core.flags import Indicator
 
     gen = torch.Generator(device).manual_seed(seed)
-    logits = (torch.randn(batch, vocab, generator=gen, device=device) * 3).to(torch.bfloat16)
-    buffers = SamplingBuffers.random(size=batch, timesteps=1, vocab_size=vocab, device=device, seed=seed,
-                                     indicators=Indicator(0x7BE), max_top_logprobs=5)
+    logits = (torch.randn(rows, vocab, generator=gen, device=device) * 3).to(torch.bfloat16)
+    drafted = torch.randint(1, vocab, (rows,), generator=gen, device=device, dtype=torch.int32)
+    buffers = SamplingBuffers.random(size=rows, timesteps=LOOKAHEAD + 1, vocab_size=vocab, device=device,
+                                     seed=seed, indicators=Indicator(0x7BE), max_top_logprobs=5)
 
-    return logits, buffers
+    return logits, drafted, buffers
 
 
-def measure_fused(vocab: int, batch: int, block_n: int, *, device="cuda", steps: int = 50,
-                  warmup: int = 5, seed: int = 0) -> float:
-    """Median microseconds of one fused autoregressive call at (vocab, batch, block_n): the timed
-    calls are queued behind a GPU sleep, so they run back to back and each event pair brackets the
-    GPU's work on one call, not the host's time to issue it."""
-
-    from sonic_sampler.interface.functional import fused_singular
-
-    logits, buffers = _workload(vocab, batch, str(device), seed)
-    rep = buffers.repetition
-    kw = dict(
-        indicators=buffers.flags.target, max_top_logprobs=5, return_logprobs=True, block_n=block_n,
-        grammar=buffers.grammar[:, 0], context_counts=rep.counts.context, decode_counts=rep.counts.decode,
-        repetition_penalties=rep.multiplicative, frequency_penalties=rep.frequency,
-        presence_penalties=rep.presence, logit_bias=buffers.bias, temperature=buffers.temperature,
-        top_k=buffers.top_k, top_p=buffers.top_p, min_p=buffers.min_p, top_k_logprobs=buffers.top_logprobs,
-        philox_seed=1, kernel_layout="tiles",
-    )
+def _time(call: Callable[[], object], steps: int, warmup: int) -> float:
+    """Median microseconds of one `call()`: the timed calls are queued behind a GPU sleep, so they
+    run back to back and each event pair brackets the GPU's work on one call, not the host's time
+    to issue it."""
 
     for _ in range(warmup):
 
-        fused_singular(logits, **kw)
+        call()
 
     stream = torch.cuda.current_stream()
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
@@ -88,7 +94,7 @@ def measure_fused(vocab: int, batch: int, block_n: int, *, device="cuda", steps:
     for start, end in events:
 
         start.record(stream)
-        fused_singular(logits, **kw)
+        call()
         end.record(stream)
 
     torch.cuda.synchronize()
@@ -96,13 +102,97 @@ def measure_fused(vocab: int, batch: int, block_n: int, *, device="cuda", steps:
     return statistics.median(a.elapsed_time(b) * 1e3 for a, b in events)
 
 
-def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[int] = BATCH_BUCKETS,
-             widths: Iterable[int] = WIDTHS, measure: Optional[Measure] = None, k: int = MAX_K,
-             arch: Optional[str] = None, log=None) -> DispatchSummary:
-    """The dispatch table measured by `measure(vocab, batch, block_n) -> microseconds` (by default
-    `measure_fused` on the current GPU). Widths that leave fewer than two tiles are skipped."""
+def measure_kind(kind: str, vocab: int, batch: int, block_n: int, *, device="cuda", steps: int = 30,
+                 warmup: int = 3, seed: int = 0) -> Optional[float]:
+    """Median microseconds of one call of `kind` over `batch` rows at (vocab, block_n), or None
+    where the kind has no call of that size (a verification needs two rows per request; drafting
+    is timed for draft vocabularies, at most DRAFT_VOCAB_MAX columns)."""
 
-    measure = measure or measure_fused
+    from sonic_sampler.interface import UnshardedBoundedTopK, UnshardedFusedMultistep, UnshardedFusedSingular
+    from sonic_sampler.interface.functional import fused_singular
+
+    logits, drafted, buffers = _workload(vocab, max(batch, 2), str(device), seed)
+
+    if kind == "singular":
+
+        rep = buffers.repetition
+        kw = dict(
+            indicators=buffers.flags.target, max_top_logprobs=5, return_logprobs=True, block_n=block_n,
+            grammar=buffers.grammar[:, 0], context_counts=rep.counts.context, decode_counts=rep.counts.decode,
+            repetition_penalties=rep.multiplicative, frequency_penalties=rep.frequency,
+            presence_penalties=rep.presence, logit_bias=buffers.bias, temperature=buffers.temperature,
+            top_k=buffers.top_k, top_p=buffers.top_p, min_p=buffers.min_p, top_k_logprobs=buffers.top_logprobs,
+            philox_seed=1, kernel_layout="tiles",
+        )
+        return _time(lambda: fused_singular(logits[:batch], **kw), steps, warmup)
+
+    if kind == "multistep":
+
+        if batch < 2:
+
+            return None
+
+        n = min(LOOKAHEAD + 1, batch)
+        requests = batch // n
+        rows = requests * n
+        verifier = UnshardedFusedMultistep.initialize(vocab_size=vocab, lookahead=n - 1, batch_size=requests,
+                                                      block_size=block_n, max_top_logprobs=5, device=device)
+        view = logits[:rows].view(requests, n, vocab)
+        tokens = drafted[:rows].view(requests, n)
+        return _time(lambda: verifier(view, tokens, buffers, logprobs=True, philox_seed=1), steps, warmup)
+
+    if kind == "topk":
+
+        topk = UnshardedBoundedTopK.initialize(vocab_size=vocab, block_size=block_n, batch_size=batch,
+                                               device=device)
+        return _time(lambda: topk(logits[:batch]), steps, warmup)
+
+    if kind == "drafting":
+
+        if vocab > DRAFT_VOCAB_MAX:
+
+            return None
+
+        target, d2t, grammar = _drafting(vocab, batch, str(device), seed)
+        sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=batch, lookahead=LOOKAHEAD,
+                                                    block_size=block_n, max_top_logprobs=5, device=device)
+        return _time(lambda: sampler.drafting(logits[:batch], grammar, timestep=1, tokens=None, d2t_mapping=d2t,
+                                              target_vocab=target, philox_seed=1), steps, warmup)
+
+    raise ValueError(f"unknown call kind {kind!r}")
+
+
+@functools.lru_cache(maxsize=1)
+def _drafting(vocab: int, rows: int, device: str, seed: int):
+    """d2t into a target vocabulary 8x wider (at most 262144) and buffers whose rows allow about
+    6% of it (each bit the AND of four random bits) through their grammar mask, the only processor
+    on."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    target = min(8 * vocab, 262144)
+    gen = torch.Generator(device).manual_seed(seed + 1)
+    d2t = torch.randperm(target, generator=gen, device=device)[:vocab].to(torch.int32)
+    buffers = SamplingBuffers.default(size=rows, timesteps=LOOKAHEAD + 1, vocab_size=target, device=device,
+                                      noise=False)
+    buffers.flags = Flags.from_values(rows, LOOKAHEAD + 1, Indicator.GRAMMAR, Indicator.GRAMMAR, device=device)
+    grammar = buffers.grammar.view(torch.int32)
+    draw = lambda: torch.randint(-2 ** 31, 2 ** 31, grammar.shape, generator=gen, device=device,  # noqa: E731
+                                 dtype=torch.int32)
+    grammar.copy_(draw() & draw() & draw() & draw())
+
+    return target, d2t, buffers
+
+
+def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[int] = BATCH_BUCKETS,
+             widths: Iterable[int] = WIDTHS, measure: Optional[Measure] = None, kinds: Iterable[str] = KINDS,
+             k: int = MAX_K, arch: Optional[str] = None, log=None) -> DispatchSummary:
+    """The dispatch table measured by `measure(kind, vocab, batch, block_n) -> microseconds or
+    None` (by default `measure_kind` on the current GPU). Widths that leave fewer than two tiles
+    are skipped."""
+
+    measure = measure or measure_kind
     arch = arch or resolve_arch(None)
     vocab = PriorityBucket()
 
@@ -112,16 +202,35 @@ def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[i
 
         for b in sorted(batch_sizes):
 
-            times: Dict[int, float] = {w: measure(v, b, w) for w in widths if -(-v // w) >= 2}
-            ranked: List[int] = sorted(times, key=lambda w: (times[w], w))
+            usable = [w for w in widths if -(-v // w) >= 2]
+            score = {w: 1.0 for w in usable}
+            lines = []
+
+            for kind in kinds:
+
+                times = {w: measure(kind, v, b, w) for w in usable}
+
+                if any(t is None for t in times.values()):
+
+                    continue
+
+                best = min(times.values())
+
+                for w in usable:
+
+                    score[w] = max(score[w], times[w] / best)
+
+                lines.append(f"{kind} " + " ".join(f"{w}:{times[w]:.2f}" for w in usable))
+
+            low = min(score.values())
+            pick = max(w for w in usable if score[w] <= low * (1 + TOLERANCE))
 
             if log is not None:
 
-                log(f"vocab {v} batch {b}: " + ", ".join(f"{w}: {times[w]:.2f} us" for w in ranked))
+                log(f"vocab {v} batch {b}: {pick} | " + " | ".join(lines))
 
-            configs = [RuntimeConfig(priority=i, block_n=w, strategy="radix", first_warps=4, second_warps=4)
-                       for i, w in enumerate(ranked)]
-            batches.append(BatchBucket(size=b, config=configs))
+            config = RuntimeConfig(priority=0, block_n=pick, strategy="radix", first_warps=4, second_warps=4)
+            batches.append(BatchBucket(size=b, config=[config]))
 
         vocab.append(VocabBucket(size=v, batch=batches))
 
@@ -138,14 +247,15 @@ def main(argv=None) -> int:
     parser.add_argument("--vocab", default=",".join(map(str, VOCAB_BUCKETS)))
     parser.add_argument("--batch", default=",".join(map(str, BATCH_BUCKETS)))
     parser.add_argument("--widths", default=",".join(map(str, WIDTHS)))
+    parser.add_argument("--kinds", default=",".join(KINDS))
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
     args = parser.parse_args(argv)
 
     ints = lambda text: [int(x) for x in text.split(",") if x]  # noqa: E731
     summary = autotune(ints(args.vocab), ints(args.batch), ints(args.widths),
-                       measure=lambda v, b, w: measure_fused(v, b, w, steps=args.steps, warmup=args.warmup),
-                       log=lambda line: print(line, flush=True))
+                       measure=lambda *key: measure_kind(*key, steps=args.steps, warmup=args.warmup),
+                       kinds=[x for x in args.kinds.split(",") if x], log=lambda line: print(line, flush=True))
     summary.save(args.out)
     print(f"wrote {args.out}", flush=True)
 

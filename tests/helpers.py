@@ -155,3 +155,34 @@ def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, bl
     torch.cuda.synchronize()
 
     return verification, buffers, verifier
+
+
+def merge_path_logits(rows: int, vocab: int, block: int, seed: int):
+    """bf16 logits whose rows take each path of the row merge at tiles = vocab / block (kp = 4 at
+    128 tiles): r % 5 == 0 plain spiked values (sampled merge), 1: 60 large values in each of 3
+    tiles and 4: 6 in each of 16 tiles (lists merged whole, up to the bound of 16), 2: 8 in each
+    of 24 tiles and 3: every logit equal (radix merge)."""
+
+    from bench import spiked_logits
+
+    g = torch.Generator().manual_seed(seed)
+    logits = spiked_logits(rows, vocab, seed=seed + 1).float()
+    tiles = vocab // block
+
+    for r in range(rows):
+
+        kind = r % 5
+
+        if kind == 3:
+
+            logits[r] = 0.25
+            continue
+
+        hot, per = {1: (3, 60), 2: (24, 8), 4: (16, 6)}.get(kind, (0, 0))
+
+        for t in torch.randperm(tiles, generator=g)[:hot].tolist():
+
+            cols = t * block + torch.randperm(block, generator=g)[:per]
+            logits[r, cols] = 20.0 + torch.rand(per, generator=g) * 8.0
+
+    return logits.to(torch.bfloat16)

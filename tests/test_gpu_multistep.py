@@ -112,3 +112,42 @@ def test_all_accepted_emits_bonus_from_last_step():
     verification, _, _ = run_verifier(work, block_size=1024, logprobs=False)
     assert verification.offsets.cpu().flatten().tolist() == [gamma] * batch
     assert torch.equal(verification.tokens.cpu().flatten(), drafted)
+
+
+def test_merge_paths_at_128_tiles():
+    """Multistep rows at V = 131072, block 1024 (128 lists, 4 sampled per list) whose top-128
+    crowds into a few lists, into more lists than the whole-list bound, or ties everywhere: the
+    per-row top-128 ids and the verification must match the oracle."""
+
+    from bench import MultistepWorkload
+    from helpers import merge_path_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+
+    batch, gamma, vocab, block = 5, 3, 131072, 1024
+    n = gamma + 1
+    g = torch.Generator().manual_seed(63)
+    host = SamplingBuffers.random(size=batch, timesteps=n, vocab_size=vocab, device="cpu", seed=64,
+                                  max_top_logprobs=4)
+    logits = merge_path_logits(batch * n, vocab, block, seed=65)
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch * n, generator=g) < 0.5, argmax,
+                          torch.randint(1, vocab, (batch * n,), generator=g)).to(torch.int32)
+    probabilities = torch.softmax(torch.randn(batch, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print(f"multistep merge paths at 128 tiles: rows={batch * n}", flush=True)
+    verification, _, verifier = run_verifier(work, update_counts=True, block_size=block)
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, probabilities=probabilities,
+                                logprobs=True, max_top_logprobs=4)
+    check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
+
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i)

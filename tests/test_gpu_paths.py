@@ -131,6 +131,45 @@ def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
                    slot_mapping=slot_mapping)
 
 
+@pytest.mark.parametrize("seed", [44, 45])
+def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed):
+    """Drafting through d2t into a 8197-token target vocabulary (its last grammar word holds 5
+    tokens) with every processor on: the tile kernel stages each row's 257 grammar words in
+    workgroup memory, clears the bits past the vocabulary and reads a zero quad for clamped
+    columns. Half the rows allow every token, including garbage bits past the vocabulary; d2t
+    reaches the last target ids."""
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    slots, rows, gamma, t = 10, 8, 3, 1
+    draft_vocab, target_vocab = 6144, 8197
+    g = torch.Generator().manual_seed(seed)
+    host = random_host(slots, gamma + 1, target_vocab, seed, indicator=EVERY_PROCESSOR)
+    host.grammar.view(torch.int32)[::2] = -1
+    logits = spiked_logits(rows, draft_vocab, seed=610 + seed)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(torch.int32)
+    d2t = torch.cat([torch.arange(target_vocab - 64, target_vocab),
+                     torch.randperm(target_vocab - 64, generator=g)[:draft_vocab - 64]])
+    d2t = d2t[torch.randperm(draft_vocab, generator=g)].to(torch.int32)
+    tokens = torch.randint(1, target_vocab, (rows, gamma + 1), generator=g).to(torch.int32)
+    buffers = to_device(host, DEV)
+    print(f"staged grammar V_t={target_vocab} seed={seed}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=draft_vocab, batch_size=rows, lookahead=gamma,
+                                                block_size=2048, max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, target_vocab, dtype=torch.bfloat16, device=DEV)
+    selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=tokens.to(DEV),
+                                 probabilities=probs, slot_mapping=slot_mapping.to(DEV),
+                                 d2t_mapping=d2t.to(DEV), target_vocab=target_vocab, in_place=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="draft", timestep=t, slot_mapping=slot_mapping.tolist(),
+                               d2t=d2t, drafted=tokens, history=t, probs=True, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=slot_mapping)
+
+
 @pytest.mark.parametrize("seed", [50, 51])
 def test_scalar_path_multistep(seed):
 

@@ -247,3 +247,31 @@ def test_extreme_divisors_and_penalties():
     expected = oracle.singular(logits, state, scope="target", logprobs=False)
     tokens = selection.tokens[:, 0].cpu()
     assert [int(t) for t in tokens] == [e.token for e in expected]
+
+
+def test_merge_paths_at_128_tiles():
+    """V = 131072 at block 1024: 128 candidate lists of which the row merge samples 4 entries
+    each. Rows whose top-128 crowds into a few lists have those lists merged whole; rows with
+    more crowded lists than the bound, or all-equal rows, take the radix merge. Every path must
+    give the oracle's tokens and logprobs."""
+
+    from helpers import merge_path_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import to_device
+
+    rows, vocab, block = 20, 131072, 1024
+    logits = merge_path_logits(rows, vocab, block, seed=61)
+    host = SamplingBuffers.random(size=rows, timesteps=1, vocab_size=vocab, device="cpu", seed=62,
+                                  max_top_logprobs=8)
+    buffers = to_device(host, DEV)
+    print(f"merge paths at 128 tiles: rows={rows}", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=8,
+                                                block_size=block, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=8)
+    check_singular(selection, expected, logprobs=True)

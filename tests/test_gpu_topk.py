@@ -133,3 +133,36 @@ def test_one_workgroup_per_row_strategy(vocab, k, dtype):
     ev, ei = oracle_topk(logits, k)
     assert torch.equal(indices.cpu(), ei)
     assert torch.equal(values.cpu().float(), ev.float())
+
+
+@pytest.mark.parametrize("k", [32, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_merge_paths_at_128_tiles(k, dtype):
+    """V = 131072 at block 1024: 128 sorted lists of k candidates, of which the merge samples 4
+    each. Rows whose top-k crowds into a few lists (merged whole), into more than 16 lists or ties
+    everywhere (radix merge), and plain rows (sampled merge) must all be exact."""
+
+    from bench import spiked_logits
+
+    rows, vocab, block = 10, 131072, 1024
+    g = torch.Generator().manual_seed(k)
+    logits = spiked_logits(rows, vocab, seed=900 + k, dtype=torch.float32)
+
+    for r in range(rows):
+
+        kind = r % 5
+
+        if kind == 3:
+
+            logits[r] = torch.randint(-2, 2, (vocab,), generator=g).float()
+            continue
+
+        hot, per = {1: (3, k // 2), 2: (24, k // 4), 4: (12, k // 4)}.get(kind, (0, 0))
+
+        for t in torch.randperm(vocab // block, generator=g)[:hot].tolist():
+
+            cols = t * block + torch.randperm(block, generator=g)[:per]
+            logits[r, cols] = 40.0 + torch.rand(per, generator=g) * 8.0
+
+    print(f"top-k merge paths at 128 tiles: k={k} {dtype}", flush=True)
+    check(logits.to(dtype), k, block)

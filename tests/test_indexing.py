@@ -202,3 +202,245 @@ def test_masked_survivors_are_the_keys_above_the_threshold(E):
             continue
 
         assert sorted(run) == expected
+
+
+REFILL_LISTS = 16
+
+
+def tile_lists(values, block):
+    """Sorted candidate lists of the tile stage: per tile its top-128 (key, column) by (key desc,
+    column asc), padded with absent entries (key 0)."""
+
+    lists = []
+
+    for t0 in range(0, len(values), block):
+
+        entries = sorted(((int(k), t0 + j) for j, k in enumerate(values[t0:t0 + block])),
+                         key=lambda e: (-e[0], e[1]))[:SS_K]
+        lists.append(entries + [(0, -1)] * (SS_K - len(entries)))
+
+    return lists
+
+
+def row_merge(lists):
+    """merge_row + merge_refill over the lists, restated step for step: returns the (key, column)
+    top-128 and the path taken ("sampled", "refill" or "radix")."""
+
+    tiles = len(lists)
+    kp = merge_prefix(tiles)
+    slot = lambda s: (s // kp, s % kp)  # noqa: E731
+
+    def comp(key, g):
+
+        return (key << 16) | (0xffff - g) if key else 0
+
+    f = sorted((comp(lists[t][p][0], t * kp + p) for t in range(tiles) for p in range(kp)), reverse=True)
+    f = (f + [0] * SS_K)[:SS_K]
+    last = f[-1]
+    llast = slot(0xffff - (last & 0xffff))[0] if last else tiles
+    beats = 0
+
+    if kp < SS_K:
+
+        for t in range(tiles):
+
+            kn = lists[t][kp][0]
+            beats += bool(kn and (kn > last >> 16 or (kn == last >> 16 and t < llast)))
+
+    if beats == 0:
+
+        return [(c >> 16, lists[slot(0xffff - (c & 0xffff))[0]][slot(0xffff - (c & 0xffff))[1]][1] if c else -1)
+                for c in f], "sampled"
+
+    if beats > REFILL_LISTS or kp == 0:
+
+        everything = sorted((e for lst in lists for e in lst if e[0]), key=lambda e: (-e[0], e[1]))[:SS_K]
+        return everything + [(0, -1)] * (SS_K - len(everything)), "radix"
+
+    def to_entry(c):
+
+        if not c:
+
+            return 0
+
+        t, p = slot(0xffff - (c & 0xffff))
+        return (c & 0xffff0000) | (0xffff - (t * SS_K + p))
+
+    f = [to_entry(c) for c in f]
+
+    for t0 in range(0, tiles, WAVE):
+
+        cn = [comp(lists[t][kp][0], t * SS_K + kp) if t < tiles else 0 for t in range(t0, t0 + WAVE)]
+        m = [lane for lane in range(WAVE) if cn[lane] > f[-1]]
+
+        while m:
+
+            lst = t0 + m[0]
+            r = [comp(lists[lst][kp + 127 - e][0], lst * SS_K + kp + 127 - e) if e >= kp else 0
+                 for e in range(SS_K)]
+            merged = [max(a, b) for a, b in zip(f, r)]
+            # the elementwise maximum must be bitonic (one descent, then one ascent at most)
+            turns = sum(1 for i in range(1, SS_K - 1) if merged[i] < merged[i - 1] and merged[i] < merged[i + 1])
+            assert turns <= 1
+            f = sorted(merged, reverse=True)
+            m = [lane for lane in m[1:] if cn[lane] > f[-1]]
+
+    def column(c):
+
+        if not c:
+
+            return -1
+
+        g = 0xffff - (c & 0xffff)
+        return lists[g >> 7][g & 127][1]
+
+    return [(c >> 16, column(c)) for c in f], "refill"
+
+
+def refill_cases():
+
+    rng = np.random.default_rng(7)
+    block = 256  # small tiles keep the emulation fast; only the list structure matters
+
+    for tiles in (2, 5, 32, 64, 100, 128, 256, 300, 512):
+
+        v = tiles * block - (17 if tiles % 2 else 0)   # odd tile counts end in a partial tile
+        yield f"random-{tiles}", rng.integers(0x7000, 0x9000, v)
+        yield f"ties-{tiles}", rng.integers(0x8000, 0x8004, v)
+        yield f"equal-{tiles}", np.full(v, 0x8100)
+        spiked = rng.integers(0x7000, 0x8000, v)
+        full = tiles - (1 if v % block else 0)
+        hot = rng.choice(full, size=min(full, rng.integers(1, 24)), replace=False)
+        for t in hot:
+
+            spiked[t * block + rng.choice(block, 60, replace=False)] = rng.integers(0x9000, 0x9100, 60)
+
+        yield f"spiked-{tiles}", spiked
+
+
+@pytest.mark.parametrize("name,values", list(refill_cases()), ids=lambda x: x if isinstance(x, str) else "")
+def test_row_merge_refill_is_exact(name, values):
+    """The sampled merge, its exactness check and the refill give the exact top-128 by (value
+    desc, column asc) on every path; the all-equal and spiked rows reach the refill and the radix
+    bound."""
+
+    lists = tile_lists(values, 256)
+    got, path = row_merge(lists)
+    exact = sorted(((int(k), j) for j, k in enumerate(values)), key=lambda e: (-e[0], e[1]))[:SS_K]
+    exact += [(0, -1)] * (SS_K - len(exact))
+    assert got == exact, (name, path)
+
+
+def test_row_merge_refill_paths_are_reached():
+
+    paths = {row_merge(tile_lists(values, 256))[1] for _, values in refill_cases()}
+    assert paths == {"sampled", "refill", "radix"}
+
+
+TOPK_REFILL_LISTS = 16
+
+
+def topk_merge(values, block, k):
+    """topk_merge_kernel restated step for step: the tiles' sorted top-k lists, the sampled merge
+    (kp entries per list), the exactness check against the k-th merged composite, the whole-list
+    refill with its element pairing, and the radix fallback. Returns ((key, column) top-k, path)."""
+
+    tiles = -(-len(values) // block)
+    lists = [sorted(((int(values[c]), c) for c in range(t * block, min(len(values), (t + 1) * block))),
+                    key=lambda e: (-e[0], e[1]))[:k] for t in range(tiles)]
+    comp = lambda e: (e[0] << 32) | (0xffffffff - e[1])  # noqa: E731
+    ncand = tiles * k
+    kp = k if ncand <= 512 else (1 << ((512 // tiles).bit_length() - 1)) if tiles <= 512 else 0
+    exact = sorted((e for lst in lists for e in lst), key=lambda e: (-e[0], e[1]))[:k]
+
+    if kp == 0:
+
+        return exact, "radix"
+
+    f = sorted((comp(lists[s // kp][s % kp]) for s in range(512) if s // kp < tiles), reverse=True)
+    f = (f + [0] * SS_K)[:SS_K]
+    beats = sum(1 for t in range(tiles) if kp < k and comp(lists[t][kp]) > f[k - 1]) if kp < k else 0
+
+    if beats > TOPK_REFILL_LISTS:
+
+        return exact, "radix"
+
+    for t0 in range(0, tiles if beats else 0, WAVE):
+
+        nx = [comp(lists[t][kp]) if t < tiles else 0 for t in range(t0, t0 + WAVE)]
+        m = [lane for lane in range(WAVE) if nx[lane] > f[k - 1]]
+
+        while m:
+
+            lst = lists[t0 + m[0]]
+            r = [comp(lst[kp + 127 - e]) if e >= SS_K - k + kp else 0 for e in range(SS_K)]
+            assert all(kp <= kp + 127 - e < k for e in range(SS_K - k + kp, SS_K))
+            f = sorted((max(a, b) for a, b in zip(f, r)), reverse=True)
+            m = [lane for lane in m[1:] if nx[lane] > f[k - 1]]
+
+    got = [(c >> 32, 0xffffffff - (c & 0xffffffff)) for c in f[:k]]
+
+    return got, ("refill" if beats else "sampled") if got == exact else "WRONG"
+
+
+def topk_cases():
+
+    rng = np.random.default_rng(11)
+
+    for k, block, tiles in [(32, 256, 32), (32, 256, 16), (128, 256, 32), (128, 256, 5), (64, 256, 100),
+                            (8, 256, 300), (128, 256, 512)]:
+
+        v = tiles * block - 9
+        yield k, f"random-{k}-{tiles}", rng.integers(0, 2 ** 31, v), block
+        yield k, f"ties-{k}-{tiles}", rng.integers(1000, 1003, v), block
+        spiked = rng.integers(0, 2 ** 30, v)
+        for t in rng.choice(tiles - 1, size=min(tiles - 1, 6), replace=False):
+
+            spiked[t * block + rng.choice(block, k, replace=False)] = rng.integers(2 ** 31, 2 ** 32, k)
+
+        yield k, f"spiked-{k}-{tiles}", spiked, block
+
+
+@pytest.mark.parametrize("k,name,values,block", list(topk_cases()),
+                         ids=lambda x: x if isinstance(x, str) else "")
+def test_topk_merge_is_exact(k, name, values, block):
+
+    got, path = topk_merge(values, block, k)
+    assert path != "WRONG", name
+
+
+def test_topk_merge_paths_are_reached():
+
+    paths = {topk_merge(values, block, k)[1] for k, _, values, block in topk_cases()}
+    assert paths == {"sampled", "refill", "radix"}
+
+
+@pytest.mark.parametrize("E", [4, 8, 16, 32, 128])
+def test_topk_block_bound_shares(E):
+    """topk_block_kernel's lower bound: wave w's share of k is ceil(k * n_w / V) for its n_w
+    valid columns (chunk c gives it columns c * 1024 + 256 w .. + 255). The shares sum to at least
+    k, a wave has a share iff it has columns, and a full block gives every wave k / 4."""
+
+    block = 256 * E
+
+    for k in (1, 2, 8, 32, 64, 128):
+
+        for V in sorted({1, 2, 17, 255, 256, 257, 300, 1023, 1024, 1025, block // 2, block - 1, block} - {0}):
+
+            if V > block:
+
+                continue
+
+            nw = [sum(min(max(V - (c * 1024 + 256 * w), 0), 256) for c in range(E // 4)) for w in range(4)]
+            need = [(k * n + V - 1) // V if n else 0 for n in nw]
+            assert sum(nw) == V
+            assert sum(need) >= k
+            assert all((n > 0) == (s > 0) for n, s in zip(nw, need))
+
+            if V == block:
+
+                assert need == [-(-k // 4)] * 4
+
+    # the config-0 last tile at block 1024 (256 valid columns, all in wave 0) keeps a bound
+    nw = [min(max(256 - 256 * w, 0), 256) for w in range(4)]
+    assert [(32 * n + 255) // 256 if n else 0 for n in nw] == [32, 0, 0, 0]

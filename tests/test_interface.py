@@ -135,9 +135,14 @@ def test_dispatch_table_for_gfx950():
     table = DispatchSummary.load(k=MAX_K, arch="gfx950")
 
     assert table is not None
-    assert table.vocab.get(size=128256).block_n == 4096
-    assert table.vocab.get(size=32000).block_n == 2048
-    assert table.vocab.get(size=151936).block_n == 4096
+    # a vocabulary bucket's block_n is its smallest width (the scratchpad is sized for it); a
+    # launch takes the width of the bucket of its row count
+    assert table.vocab.get(size=128256).block_n == 1024
+    assert table.vocab.get(size=32000).block_n == 1024
+    assert table.vocab.get(size=151936).block_n == 2048
+    assert table.vocab.get(size=128256).batch.get(size=64).best.block_n == 4096     # config 1
+    assert table.vocab.get(size=32000).batch.get(size=256).best.block_n == 8192     # config 4
+    assert table.vocab.get(size=128256).batch.get(size=2048).best.block_n == 8192
 
 
 @pytest.mark.parametrize("k, block, message", [
@@ -157,9 +162,11 @@ def test_tiling_buffers():
     tiling, values, indices = TwoStageTiling.factory(vocab_size=128256, batch_size=8, lookahead=3,
                                                      arch="gfx950", device="cpu")
 
-    assert tiling.block_n == 4096
-    assert tiling.vocabulary.blocks == 32
-    assert tiling.scratchpad.shape == (8 * 4, 32 * MAX_K)
+    # sized for the bucket's smallest width (1024: 126 tiles); 32 rows launch at 4096
+    assert tiling.block_n == 1024
+    assert tiling.vocabulary.blocks == 126
+    assert tiling.scratchpad.shape == (8 * 4, 126 * MAX_K)
+    assert tiling.tuning(32)[2] == 4096
     assert tiling.scratchpad.dtype == torch.uint32
     assert values.shape == indices.shape == (32, MAX_K)
 
@@ -222,21 +229,47 @@ def test_fused_multistep_layout_errors():
 
 
 def test_autotune_ranks_widths_and_round_trips(tmp_path):
-    """The table the autotune harness writes ranks each bucket's widths by the measured time,
-    skips widths that leave a single tile, and reads back through DispatchSummary."""
+    """The table the autotune harness writes holds, per bucket, the width with the smallest worst
+    slowdown over the call kinds (never one that leaves a single tile; a kind that has no call of
+    the bucket's size is left out), and reads back through DispatchSummary."""
 
     from sonic_sampler.interface.autotune import autotune
     from sonic_sampler.interface.dispatch import DispatchSummary
 
     best = {8192: 1024, 131072: 4096}
-    fake = lambda v, b, w: abs(w - (8192 if b >= 256 else best[v])) + 1.0  # noqa: E731
-    summary = autotune([8192, 131072], [1, 64, 512], measure=fake, arch="gfx950")
+    seen = []
+
+    def measure(kind, v, b, w):
+
+        seen.append((kind, v, b, w))
+
+        if kind == "multistep" and b < 2:
+
+            return None
+
+        return abs(w - (8192 if b >= 256 else best[v])) + 1.0
+
+    summary = autotune([8192, 131072], [1, 64, 512], measure=measure, kinds=("singular", "multistep", "topk"),
+                       arch="gfx950")
     path = tmp_path / "gfx950_k128.toml"
     summary.save(path)
     back = DispatchSummary.read(path)
 
-    small = back.vocab.get(8192)
-    assert [c.block_n for c in small.batch.get(1).config] == [1024, 2048, 4096]   # 8192 leaves one tile
+    assert sorted(w for kind, v, b, w in seen if (kind, v, b) == ("topk", 8192, 1)) == [1024, 2048, 4096]
+    assert {kind for kind, *_ in seen} == {"singular", "multistep", "topk"}
+    assert [(c.priority, c.block_n) for c in back.vocab.get(8192).batch.get(1).config] == [(0, 1024)]
     assert back.vocab.get(131072).batch.get(64).best.block_n == 4096
     assert back.vocab.get(131072).batch.get(300).best.block_n == 8192
-    assert [c.priority for c in back.vocab.get(131072).batch.get(1).config] == [0, 1, 2, 3]
+    assert back.vocab.get(131072).block_n == 4096   # the scratchpad is sized for the smallest width
+
+    # a wider width within the tolerance of the best score wins
+    times = {1024: 10.0, 2048: 10.1, 4096: 11.0, 8192: 12.0}
+    near = autotune([32768], [1], measure=lambda kind, v, b, w: times[w])
+    assert near.vocab.get(32768).batch.get(1).best.block_n == 2048
+
+    # the worst slowdown over the kinds decides: 4096 is 5% behind on one kind, 1024 2x on another
+    split = {"singular": {1024: 10.0, 2048: 11.0, 4096: 10.5, 8192: 13.0},
+             "multistep": {1024: 20.0, 2048: 12.0, 4096: 10.0, 8192: 10.2},
+             "topk": {1024: 9.0, 2048: 9.5, 4096: 9.2, 8192: 9.9}}
+    mixed = autotune([32768], [8], measure=lambda kind, v, b, w: split[kind][w], kinds=split)
+    assert mixed.vocab.get(32768).batch.get(8).best.block_n == 4096

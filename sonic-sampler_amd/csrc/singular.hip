@@ -50,14 +50,21 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 // Tile stage: grid (tiles, rows). With d2t and a grammar mask, `stage_words` > 0 stages the
 // row's grammar words in workgroup memory (dynamic shared memory) before the prologue, so that the
 // per-element lookups through d2t read LDS: as scattered global gathers (one cache line per
-// element) they are bounded by the vector cache's line rate, not by HBM.
+// element) they are bounded by the vector cache's line rate, not by HBM. Such launches number
+// their workgroups XCD by XCD (xcd_grouped), so that a row's tiles share one L2.
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles,
                                                                   int stage_words) {
     __shared__ TileSmem<E> sm;
     extern __shared__ __align__(16) uint32_t grammar_words[];
-    const int row = blockIdx.y;
-    const int tile = blockIdx.x;
+    int row = blockIdx.y, tile = blockIdx.x;
+    if (MODE != MODE_DIRECT && stage_words > 0) {
+        // the tiles of a row stage the same grammar row: run them on one XCD, whose L2 then
+        // fetches it once
+        const int v = xcd_grouped((int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y));
+        row = v / tiles;
+        tile = v - row * tiles;
+    }
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
     const int slot = a.slot_mapping ? a.slot_mapping[row] : row;

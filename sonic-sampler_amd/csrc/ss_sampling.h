@@ -100,6 +100,17 @@ __host__ __device__ inline ListMap make_list_map(int per, int shard, int block_n
     return m;
 }
 
+// Renumbers workgroup L of a launch of N so that each XCD runs a contiguous range of the new
+// numbers: the dispatcher hands consecutive workgroups to the device's 8 XCDs in turn (L % 8), and
+// workgroup L becomes number local + the start of XCD L % 8's range, the first N % 8 XCDs taking
+// one number more. A bijection on [0, N) for any N; workgroups that share data (the tiles of one
+// row) then share an L2.
+__device__ __forceinline__ int xcd_grouped(int L, int N) {
+    const int q = N >> 3, r = N & 7;
+    const int x = L & 7, local = L >> 3;
+    return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+}
+
 __device__ __forceinline__ int tile_col(int j) {  // column offset of element j inside a tile
     return (j >> 2) * (SS_BLOCK * 4) + (int)threadIdx.x * 4 + (j & 3);
 }

@@ -444,3 +444,31 @@ def test_topk_block_bound_shares(E):
     # the config-0 last tile at block 1024 (256 valid columns, all in wave 0) keeps a bound
     nw = [min(max(256 - 256 * w, 0), 256) for w in range(4)]
     assert [(32 * n + 255) // 256 if n else 0 for n in nw] == [32, 0, 0, 0]
+
+
+def xcd_grouped(L, N):
+    """ss_sampling.h xcd_grouped, restated."""
+
+    q, r = N >> 3, N & 7
+    x, local = L & 7, L >> 3
+    return x * (q + 1) + local if x < r else r * (q + 1) + (x - r) * q + local
+
+
+def test_xcd_grouped_is_a_bijection_with_contiguous_xcd_ranges():
+
+    for N in list(range(1, 300)) + [1024, 1025, 2047, 4096, 65535]:
+
+        v = [xcd_grouped(L, N) for L in range(N)]
+        assert sorted(v) == list(range(N)), N
+
+        for x in range(8):
+
+            mine = sorted(v[L] for L in range(x, N, 8))
+            assert mine == list(range(mine[0], mine[0] + len(mine))) if mine else True
+
+    # config 4: 256 rows of 4 tiles; the 4 tiles of every row land on one XCD
+    tiles = 4
+    for L in range(1024):
+
+        row = xcd_grouped(L, 1024) // tiles
+        assert all(xcd_grouped(M, 1024) // tiles != row or M % 8 == L % 8 for M in range(L % 8, 1024, 1))

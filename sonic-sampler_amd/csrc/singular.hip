@@ -234,7 +234,7 @@ struct RowwiseSmem {
         TileSmem<E> tile;
         SampleSmem sample;
     };
-    uint32_t lists[ROWWISE_MAX_TILES * SS_K];
+    alignas(16) uint32_t lists[ROWWISE_MAX_TILES * SS_K];
 };
 
 // One-launch form, grid rows: one workgroup per row streams the row tile by tile (the next tile's

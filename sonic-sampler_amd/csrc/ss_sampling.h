@@ -845,20 +845,21 @@ template <int E>
 __device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const Keys<E> &keys,
                                                           uint32_t T) {
     static_assert(E / 2 <= 16, "one mask bit per element");
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint32_t *run = sm.run[wave];
     uint32_t *spill = sm.keys[wave];
-    const u16x2 tt = __builtin_bit_cast(u16x2, T | (T << 16));
-    const u16x2 one = {1, 1};
+    const uint32_t tt = T | (T << 16);
     uint32_t mask = 0;
 #pragma unroll
     for (int i = 0; i < E / 2; ++i) {
-        // max(key - T, 0) is nonzero exactly when key > T; its minimum with 1 is that bit
-        const u16x2 d = __builtin_elementwise_min(
-            __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, keys.p[i]), tt), one);
-        mask |= __builtin_bit_cast(uint32_t, d) << i;
+        // max(key - T, 0) is nonzero exactly when key > T; its minimum with 1 is that bit. Written
+        // as the two packed 16-bit instructions: as C the compiler turns them into a compare and
+        // a select per half and a permute (seven instructions a pair instead of two).
+        uint32_t d;
+        asm("v_pk_sub_u16 %0, %1, %2 clamp\n\tv_pk_min_u16 %0, %0, %3" : "=&v"(d)
+            : "v"(keys.p[i]), "v"(tt), "v"(0x00010001u));
+        mask |= d << i;
         spill[i * 64 + lane] = keys.p[i];
     }
     const uint32_t n = (uint32_t)__popc(mask);
@@ -888,8 +889,8 @@ __device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const
 // 32 keys >= t,
 // so the wave holds at least 32 keys >= t; with lo the smallest of the four wave bounds, the tile
 // holds at least 128 keys >= lo. Every wave then collects its survivors (keys >= lo: about 160 of
-// a 4096-wide tile of unstructured logits, 30-50 per wave) in its own LDS region and sorts them
-// (wave_survivors); a two-level merge tree keeps the top-128 of the four sorted runs.
+// a 4096-wide tile of unstructured logits, 30-50 per wave) in its own LDS region and sorts them;
+// a two-level merge tree keeps the top-128 of the four sorted runs.
 //
 // When a wave has more than 128 survivors (long runs of equal keys such as the -inf of
 // grammar-masked elements, or the tile's high values concentrated in one wave), the tile finds

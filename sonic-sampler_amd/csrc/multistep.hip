@@ -4,8 +4,9 @@
 //   tile stage    grid (tiles, rows): prologue over one tile of one row -> tile argmax / top-128;
 //   row stage     grid rows: merge -> truncation -> fp32 log_softmax, written to values /
 //                 indices [row, 128] (greedy rows: the argmax in indices[row, 0]);
-//   request stage grid B (one wavefront each): greedy or stochastic chain verification, residual
-//                 resampling, logprobs, top-Z, decode-count update.
+//   request stage grid B (one wavefront each): greedy chain verification, or the stochastic
+//                 chain from the rows' verification records (acceptance, residual / bonus
+//                 samples, computed by the row stage); logprobs, top-Z, decode-count update.
 // Semantics follow the reference's PyTorch path (core/naive.py:497-646 `verification`,
 // :694-708 `multistep`), applied per request so that slots and variable lookahead compose.
 #include "ss_launch.h"
@@ -123,12 +124,17 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
 }
 
 // Row stage: grid rows; merge -> truncation -> fp32 log_softmax into values / indices [row, 128]
-// (greedy rows: the argmax in indices[row, 0]).
+// (greedy rows: the argmax in indices[row, 0]). A stochastic row also does its own part of the
+// chain verification (core/naive.py:580-620), which depends on no other row: whether its drafted
+// token is accepted, that token's logprob, and the token it emits if the chain stops here (the
+// residual sample at a rejection, the bonus sample on the last row) with its logprob. It writes
+// them as one 16-byte record at the start of its scratch row, whose candidates it has consumed:
+// {accepted, stop token, logprob if accepted (fp32 bits), stop token's logprob (fp32 bits)}.
 __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_args a, int tiles) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
     touch_kernargs<sizeof(ss_multistep_args)>();
-    const uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
     const int pivot = request_pivot(a);
     const ListMap lm = make_list_map(tiles, 0, a.block_n);
     RowSamples smp;
@@ -151,19 +157,99 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
         }
         return;
     }
+    // The drafted token of this step and its uniform, read while the candidates merge, as vector
+    // loads: a scalar load shares its wait counter with workgroup memory, so the merge's first
+    // wait for its own LDS traffic would also wait for these.
+    const bool last = step == rq.n - 1;
+    int d = 0;
+    float ud = 0.0f;
+    if (!last) {
+        const __amdgpu_buffer_rsrc_t dr = row_buffer(a.drafted_tokens + row, 4);
+        const __amdgpu_buffer_rsrc_t ur = row_buffer(a.uniform + (int64_t)slot * a.stride_uniform + step, 2);
+        d = (int)__builtin_amdgcn_raw_buffer_load_b32(dr, 0, 0, 0);
+        ud = bf2f((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(ur, 0, 0, 0));
+    }
     float v0 = 0.f, v1 = 0.f;
     int i0 = 0, i1 = 0;
     merge_row(sm, scr, smp, tiles, lm, a.vocab_size, v0, v1, i0, i1);
-    if (threadIdx.x >= 64) return;
-    truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
-             __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
-    float m, x0, x1;
-    const float logs = logf(exp_parts(v0, v1, m, x0, x1));
-    const int e0 = 2 * threadIdx.x;
-    vrow[e0] = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
-    vrow[e0 + 1] = (v1 - m) - logs;
-    irow[e0] = i0;
-    irow[e0 + 1] = i1;
+    // Waves 1 and 2 draw the 128 candidates' noise and gather their draft probabilities (one
+    // candidate per lane) while wave 0 truncates and tests the drafted token.
+    const int wave = (int)threadIdx.x >> 6;
+    const int lane = lane_id();
+    const int e0 = 2 * lane;
+    const bool svgd = (ind & IND_SVGD) || !a.draft_probabilities;
+    const uint16_t *qrow = svgd ? nullptr
+                                : a.draft_probabilities + (int64_t)slot * a.probs_stride_slot +
+                                      (int64_t)step * a.probs_stride_step;
+    if (wave == 0) {
+        sm.tok[e0] = i0;
+        sm.tok[e0 + 1] = i1;
+    }
+    __syncthreads();
+    if (wave == 1 || wave == 2) {
+        const int e = (wave - 1) * 64 + lane;
+        const int t = sm.tok[e];
+        sm.noise[e] = a.philox.enabled
+                          ? philox_gumbel(a.philox.seed, a.philox.offset, slot, step, t)
+                          : bf2f(a.gumbel[(int64_t)slot * a.gumbel_stride_slot + (int64_t)step * a.gumbel_stride_step + t]);
+        sm.qcand[e] = qrow && !last ? bf2f(qrow[t]) : 0.0f;
+    }
+    int accepted = 1;
+    float l0 = 0.f, l1 = 0.f, lacc = 0.0f;
+    if (wave == 0) {
+        const bool in_vocab = d >= 0 && d < a.vocab_size;
+        const uint16_t qd16 = qrow && !last ? qrow[in_vocab ? d : 0] : (uint16_t)0;
+        truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
+                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
+        float m, x0, x1;
+        const float logs = logf(exp_parts(v0, v1, m, x0, x1));
+        l0 = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
+        l1 = (v1 - m) - logs;
+        vrow[e0] = l0;
+        vrow[e0 + 1] = l1;
+        irow[e0] = i0;
+        irow[e0 + 1] = i1;
+        // acceptance of the drafted token: p at its first sorted position (0 when absent; its
+        // logprob then is the value at position 0, the argmax of an all-false match row),
+        // bf16(u * q) <= p (core/naive.py:580-599)
+        if (!last) {
+            const uint64_t m0 = __ballot(i0 == d), m1 = __ballot(i1 == d);
+            const int p0 = m0 ? 2 * (__ffsll((unsigned long long)m0) - 1) : 1 << 20;
+            const int p1 = m1 ? 2 * (__ffsll((unsigned long long)m1) - 1) + 1 : 1 << 20;
+            const int pos = min(p0, p1) < SS_K ? min(p0, p1) : -1;
+            const int at = pos >= 0 ? pos : 0;
+            lacc = lane_f32((at & 1) ? l1 : l0, at >> 1);
+            const float pk = pos >= 0 ? expf(lacc) : 0.0f;
+            const float qd = svgd ? 1.0f : in_vocab ? bf2f(qd16) : 0.0f;
+            accepted = rbf(ud * qd) <= pk ? 1 : 0;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    if (accepted && !last) {
+        // an accepted draft never ends the chain: no stop token
+        if (lane == 0) *(int4 *)scr = make_int4(1, 0, __float_as_int(lacc), 0);
+        return;
+    }
+    // the token emitted if the chain stops at this row: the residual max(p - q, 0) at a rejection
+    // (q a point mass on the draft under 0x800), p itself on the last row
+    const float pe0 = expf(l0), pe1 = expf(l1);
+    float r0, r1;
+    if (last) {
+        r0 = pe0;
+        r1 = pe1;
+    } else if (svgd) {
+        r0 = i0 == d ? 0.0f : pe0;
+        r1 = i1 == d ? 0.0f : pe1;
+    } else {
+        r0 = fmaxf(pe0 - sm.qcand[e0], 0.0f);
+        r1 = fmaxf(pe1 - sm.qcand[e0 + 1], 0.0f);
+    }
+    const float w0 = sm.noise[e0], w1 = sm.noise[e0 + 1];
+    const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
+    const int token = lane_i32((sel & 1) ? i1 : i0, sel >> 1);
+    const float lsel = lane_f32((sel & 1) ? l1 : l0, sel >> 1);
+    if (lane == 0) *(int4 *)scr = make_int4(accepted, token, __float_as_int(lacc), __float_as_int(lsel));
 }
 
 // Request stage: grid B, one wavefront per request.
@@ -213,124 +299,48 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
         }
         token = idxs[(int64_t)j * SS_K];
     } else {
-        // Draft positions VCH at a time: every load of a chunk is issued before any result is
-        // used (rows at and past n - 1 read row n - 2 and are ignored), so a chunk costs two
-        // rounds of loads instead of two per position: first the candidate rows (the lane's two
-        // candidate tokens and values of each row), then the drafted token's value and draft
-        // probability. The top logprobs and a rejected row's candidates then need no further
-        // loads; only the residual's draft probabilities at the rejected row's candidates are
-        // gathered once that row is known (gathering them for every row of a chunk costs more
-        // scattered reads than the round trip it saves).
+        // The rows' records (multistep_rows_kernel), one lane per row, in one round with the top
+        // logprobs of the first VCH rows; the chain stops at the first rejected draft, else at
+        // the bonus row n - 1 (core/naive.py:600-620).
         constexpr int VCH = 8;
-        const uint16_t *u = a.uniform + (int64_t)slot * a.stride_uniform;
         const bool want_top = want_lp && (ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0;
         const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
-        // top logprobs of row r from its candidate pairs
-        auto write_top = [&](int r, int2 tok, float2 val) {
-            const int64_t o = (int64_t)(rq.margin + r) * a.stride_top;
-            if (e0 < lim) {
-                a.top_values[o + e0] = (uint16_t)f2bf(val.x);
-                a.top_tokens[o + e0] = tok.x;
-            }
-            if (e1 < lim) {
-                a.top_values[o + e1] = (uint16_t)f2bf(val.y);
-                a.top_tokens[o + e1] = tok.y;
-            }
-        };
-        int2 cj = make_int2(0, 0);          // row j's candidate tokens (lane pair)
-        float2 lj = make_float2(0.f, 0.f);  // their log-softmax values
-        bool rejected = false;
-        for (int base = 0; base < n - 1 && !rejected; base += VCH) {
-            int d[VCH], pos[VCH];
-            int2 w[VCH];
-            float2 vv[VCH];
-            float uk[VCH];
+        int4 rec = make_int4(1, 0, 0, 0);
+        if (lane < n) rec = *(const int4 *)(a.scratch + (int64_t)(rq.margin + lane) * a.stride_scratch);
+        int2 w[VCH];
+        float2 vv[VCH];
+        if (want_top) {
 #pragma unroll
             for (int k = 0; k < VCH; ++k) {
-                const int r = min(base + k, n - 2);
-                d[k] = drafted[r];
-                uk[k] = bf2f(u[r]);
+                const int r = min(k, n - 1);
                 w[k] = *(const int2 *)(idxs + (int64_t)r * SS_K + e0);
                 vv[k] = *(const float2 *)(vals + (int64_t)r * SS_K + e0);
             }
-            float v[VCH], qd[VCH];
-#pragma unroll
-            for (int k = 0; k < VCH; ++k) {
-                const int r = min(base + k, n - 2);
-                // first sorted position whose token is d[k] (core/naive.py:580-584), or -1
-                const uint64_t m0 = __ballot(w[k].x == d[k]), m1 = __ballot(w[k].y == d[k]);
-                const int p0 = m0 ? 2 * (__ffsll((unsigned long long)m0) - 1) : 1 << 20;
-                const int p1 = m1 ? 2 * (__ffsll((unsigned long long)m1) - 1) + 1 : 1 << 20;
-                pos[k] = min(p0, p1) < SS_K ? min(p0, p1) : -1;
-                v[k] = vals[(int64_t)r * SS_K + (pos[k] >= 0 ? pos[k] : 0)];
-                const bool in_vocab = d[k] >= 0 && d[k] < a.vocab_size;
-                qd[k] = svgd ? 1.0f
-                             : bf2f(q[(int64_t)r * a.probs_stride_step + (in_vocab ? d[k] : 0)]);
-                qd[k] = in_vocab || svgd ? qd[k] : 0.0f;
-            }
-            int rej = -1;
-#pragma unroll
-            for (int k = 0; k < VCH; ++k) {
-                const float pk = pos[k] >= 0 ? expf(v[k]) : 0.0f;
-                // bf16(u * q) <= p  (core/naive.py:594-599)
-                if (rej < 0 && base + k < n - 1 && !(rbf(uk[k] * qd[k]) <= pk)) rej = k;
-            }
-            // logprobs of the accepted positions: the value at the drafted token's position, or
-            // at position 0 when the token is not among the candidates (argmax of an all-false
-            // match row, core/naive.py:580-584); top logprobs of rows up to the rejected one
-#pragma unroll
-            for (int k = 0; k < VCH; ++k) {
-                if (base + k >= n - 1 || (rej >= 0 && k > rej)) break;
-                if (want_lp && lane == 0 && k != rej) a.logprobs[rq.margin + base + k] = (uint16_t)f2bf(v[k]);
-                if (want_top) write_top(base + k, w[k], vv[k]);
-                if (k == rej) {
-                    cj = w[k];
-                    lj = vv[k];
+        }
+        const uint64_t rej = __ballot(lane < n - 1 && rec.x == 0);
+        j = rej ? __ffsll((unsigned long long)rej) - 1 : n - 1;
+        token = lane_i32(rec.y, j);
+        if (want_lp && lane <= j)
+            a.logprobs[rq.margin + lane] = (uint16_t)f2bf(__int_as_float(lane < j ? rec.z : rec.w));
+        if (want_top) {
+            // top logprobs of the rows up to j, from their candidate pairs
+            auto write_top = [&](int r, int2 tok, float2 val) {
+                const int64_t o = (int64_t)(rq.margin + r) * a.stride_top;
+                if (e0 < lim) {
+                    a.top_values[o + e0] = (uint16_t)f2bf(val.x);
+                    a.top_tokens[o + e0] = tok.x;
                 }
-            }
-            if (rej >= 0) {
-                j = base + rej;
-                rejected = true;
-            }
+                if (e1 < lim) {
+                    a.top_values[o + e1] = (uint16_t)f2bf(val.y);
+                    a.top_tokens[o + e1] = tok.y;
+                }
+            };
+#pragma unroll
+            for (int k = 0; k < VCH; ++k)
+                if (k <= j) write_top(k, w[k], vv[k]);
+            for (int r = VCH; r <= j; ++r)
+                write_top(r, *(const int2 *)(idxs + (int64_t)r * SS_K + e0), *(const float2 *)(vals + (int64_t)r * SS_K + e0));
         }
-        if (!rejected) {
-            // every draft accepted: the bonus row n - 1
-            cj = *(const int2 *)(idxs + (int64_t)j * SS_K + e0);
-            lj = *(const float2 *)(vals + (int64_t)j * SS_K + e0);
-            if (want_top) write_top(j, cj, lj);
-        }
-        const int c0 = cj.x, c1 = cj.y;
-        const float p0 = expf(lj.x), p1 = expf(lj.y);
-        float r0, r1;
-        if (j == n - 1) {
-            r0 = p0;
-            r1 = p1;
-        } else if (svgd) {
-            // q is a point mass on the draft: the residual zeroes the drafted candidate.
-            const int dj = drafted[j];
-            r0 = c0 == dj ? 0.0f : p0;
-            r1 = c1 == dj ? 0.0f : p1;
-        } else {
-            const uint16_t *qr = q + (int64_t)j * a.probs_stride_step;
-            r0 = fmaxf(p0 - bf2f(qr[c0]), 0.0f);
-            r1 = fmaxf(p1 - bf2f(qr[c1]), 0.0f);
-        }
-        float w0, w1;
-        if (a.philox.enabled) {
-            w0 = philox_gumbel(a.philox.seed, a.philox.offset, slot, j, c0);
-            w1 = philox_gumbel(a.philox.seed, a.philox.offset, slot, j, c1);
-        } else {
-            const uint16_t *g = a.gumbel + (int64_t)slot * a.gumbel_stride_slot +
-                                (int64_t)j * a.gumbel_stride_step;
-            w0 = bf2f(g[c0]);
-            w1 = bf2f(g[c1]);
-        }
-        const int sel = wave_argmax_first(logf(r0) - w0, logf(r1) - w1);
-        token = lane_i32((sel & 1) ? c1 : c0, sel >> 1);
-        // row j's logprob: the selected candidate's value (positions before j were written
-        // during verification)
-        const float lsel = lane_f32((sel & 1) ? lj.y : lj.x, sel >> 1);
-        if (want_lp && lane == 0) a.logprobs[rq.margin + j] = (uint16_t)f2bf(lsel);
     }
     if (greedy && a.return_logprobs && a.logprobs) {
         if (lane <= j) a.logprobs[rq.margin + lane] = 0;

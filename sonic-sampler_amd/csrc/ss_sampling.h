@@ -33,6 +33,7 @@ struct SampleSmem {
     uint32_t red[SS_WAVES];
     int32_t tok[SS_K];         // selection: the candidates' tokens (columns, then remapped)
     float noise[SS_K];         // selection: their Gumbel noise
+    float qcand[SS_K];         // verification: their draft probabilities
 };
 
 // Workgroup memory of the tile kernels (E keys per thread).

@@ -55,8 +55,11 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles,
                                                                   int stage_words) {
-    __shared__ TileSmem<E> sm;
-    extern __shared__ __align__(16) uint32_t grammar_words[];
+    // the tile stage's memory and, overlaying its runs and keys, a staged grammar row (dynamic
+    // shared memory of tile_smem_bytes)
+    extern __shared__ __align__(16) uint32_t tile_smem[];
+    TileSmem<E> &sm = *reinterpret_cast<TileSmem<E> *>(tile_smem);
+    uint32_t *grammar_words = tile_smem + TILE_OVERLAY / 4;
     int row = blockIdx.y, tile = blockIdx.x;
     if (MODE != MODE_DIRECT && stage_words > 0) {
         // the tiles of a row stage the same grammar row: run them on one XCD, whose L2 then
@@ -310,6 +313,15 @@ static size_t staged_grammar_bytes(const ss_singular_args *a) {
     return staged_grammar_words(a) ? (size_t)(stage_quads(vt) + 1) * 16 : 0;
 }
 
+// Dynamic shared memory of singular_tiles_kernel<E>: its TileSmem, or a staged grammar row from
+// TILE_OVERLAY on where that is larger.
+template <int E>
+static size_t tile_smem_bytes(const ss_singular_args *a) {
+    const size_t g = staged_grammar_bytes(a);
+    const size_t t = sizeof(TileSmem<E>);
+    return g && TILE_OVERLAY + g > t ? TILE_OVERLAY + g : t;
+}
+
 template <int MODE>
 static int launch_rowwise(const ss_singular_args *a, int tiles) {
     const int stage = staged_grammar_words(a);
@@ -332,14 +344,13 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     const int stage = staged_grammar_words(a);
-    const size_t dyn = staged_grammar_bytes(a);
     const int stages = a->stages ? a->stages : (SS_STAGE_TILES | SS_STAGE_ROWS);
     if (stages & SS_STAGE_TILES) {
         switch (a->block_n) {
-            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, dyn, s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, tile_smem_bytes<4>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
             default: return SS_ERR_UNSUPPORTED;
         }
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;

@@ -36,19 +36,26 @@ struct SampleSmem {
     float qcand[SS_K];         // verification: their draft probabilities
 };
 
-// Workgroup memory of the tile kernels (E keys per thread).
+// Workgroup memory of the tile kernels (E keys per thread). The members from `run` on are written
+// only after the tile stage's first barrier, when every wave has finished its prologue, so a
+// grammar row staged for the prologue (stage_grammar) may overlay them (TILE_OVERLAY).
 template <int E>
 struct TileSmem {
     uint32_t scan[SS_WAVES * 8];  // workgroup scans of up to 8 values per thread
     uint32_t red[SS_WAVES];
     uint32_t cnt[SS_WAVES];       // survivors of each wave
+    int32_t hist[64];             // drafted tokens that extend the decode history
     uint32_t run[SS_WAVES][SS_K + 64];  // each wave's survivors, then its sorted run
     uint32_t run2[2][SS_K];       // merge tree: the top-128 of runs (0, 1) and (2, 3)
-    int32_t hist[64];             // drafted tokens that extend the decode history
     // each wave's packed keys, pair i of lane l at [i * 64 + l], read back by the survivors of
     // wave_survivors_masked
     uint32_t keys[SS_WAVES][E / 2 * 64];
 };
+
+// Byte offset in TileSmem where a staged grammar row may begin.
+constexpr int TILE_OVERLAY = (SS_WAVES * 8 + 2 * SS_WAVES + 64) * 4;
+static_assert(TILE_OVERLAY % 16 == 0, "16-byte grammar stores");
+static_assert(TILE_OVERLAY == __builtin_offsetof(TileSmem<16>, run), "overlay starts at the runs");
 
 // Request state of one logit row, uniform over the workgroup. Row pointers are already offset to
 // the request's slot (and timestep for the grammar).

@@ -784,6 +784,17 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             issue_planes<E>(rs, u, true, rs.shard + col0, pl);
             direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
         }
+    } else if constexpr (E == 32 && MODE == MODE_GATHER_VEC) {
+        // Two 4096-column halves, as above: the gathered columns and planes of all 32 elements
+        // at once would hold 156 VGPRs (three waves per SIMD).
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x2 lh[4] = {lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]};
+            Keys<16> kh;
+            gather_keys<16, true>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
+        }
     } else {
         gather_keys<E, MODE == MODE_GATHER_VEC>(rs, u, col0, V, hist, lw, keys);
     }

@@ -285,4 +285,24 @@ __device__ __forceinline__ void wave_sort64_desc(uint32_t &v) {
     v = a[0];
 }
 
+// Sorts 64 64-bit composites held by one wave (one per lane, element = lane) in descending order.
+__device__ __forceinline__ void wave_sort64_desc(uint64_t &v) {
+    uint64_t a[1] = {v};
+    bitonic_lane_steps<1, 2>(a);
+    bitonic_lane_steps<2, 4>(a);
+    bitonic_lane_steps<4, 8>(a);
+    bitonic_lane_steps<8, 16>(a);
+    bitonic_lane_steps<16, 32>(a);
+    bitonic_lane_steps<32, 64>(a);
+    v = a[0];
+}
+
+// Sorts a bitonic sequence of 64 composites held by one wave (one per lane) in descending order:
+// the final merge of the network.
+__device__ __forceinline__ void wave_bitonic64_desc(uint64_t &v) {
+    uint64_t a[1] = {v};
+    bitonic_lane_steps<32, 64>(a);
+    v = a[0];
+}
+
 }  // namespace ss

@@ -68,7 +68,79 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
     // fit in 512 slots, else the largest power of two <= 512 / tiles (0 above 512 tiles).
     const int kp = ncand <= 2 * SS_BLOCK ? k
                    : tiles <= 2 * SS_BLOCK ? 1 << (31 - __builtin_clz((unsigned)(2 * SS_BLOCK / tiles))) : 0;
-    if (kp > 0) {
+    // k <= 64: 256 samples, one per thread, and the network one element per lane (the same
+    // exactness check and list refill as below against the k-th of the top-64)
+    const int kp64 = ncand <= SS_BLOCK ? k
+                     : tiles <= SS_BLOCK ? 1 << (31 - __builtin_clz((unsigned)(SS_BLOCK / tiles))) : 0;
+    if (k <= 64 && kp64 > 0) {
+        const int lane = lane_id(), wave = (int)threadIdx.x >> 6;
+        const int lk = __builtin_ctz((unsigned)k), lkp = __builtin_ctz((unsigned)kp64);
+        auto composite = [&](int p) {
+            const Cand cd = scr[p];
+            const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
+            return ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
+        };
+        const int s = (int)threadIdx.x;
+        const int list = s >> lkp;
+        uint64_t c = list < tiles ? composite(list * k + (s & (kp64 - 1))) : 0ull;
+        wave_sort64_desc(c);
+        sm.runs[wave][lane] = c;
+        __syncthreads();
+        if (wave < 2) {
+            uint64_t x = max_u64(sm.runs[2 * wave][lane], sm.runs[2 * wave + 1][63 - lane]);
+            wave_bitonic64_desc(x);
+            sm.runs[2 * wave][lane] = x;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint64_t f = max_u64(sm.runs[0][lane], sm.runs[2][63 - lane]);
+            wave_bitonic64_desc(f);
+            auto kth = [&]() {
+                return ((uint64_t)__builtin_amdgcn_readlane((int)(f >> 32), k - 1) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)f, k - 1);
+            };
+            int beats = 0;
+            if (kp64 < k) {
+                const uint64_t last = kth();
+                for (int t0 = 0; t0 < tiles; t0 += 64) {
+                    const int t = t0 + lane;
+                    beats += __popcll(__ballot(t < tiles && composite(t * k + kp64) > last));
+                }
+            }
+            if (beats > TOPK_REFILL_LISTS) {
+                if (lane == 0) sm.flag = 1;
+            } else {
+                for (int t0 = 0; beats > 0 && t0 < tiles; t0 += 64) {
+                    const int t = t0 + lane;
+                    const uint64_t nx = t < tiles ? composite(t * k + kp64) : 0ull;
+                    uint64_t m = __ballot(nx > kth());
+                    while (m) {
+                        const int l = t0 + (int)__builtin_ctzll(m);
+                        // lane pairs with entry kp + 63 - lane of list l (kp .. k - 1 exist)
+                        const uint64_t r = lane >= 64 - k + kp64 ? composite(l * k + kp64 + 63 - lane) : 0ull;
+                        f = max_u64(f, r);
+                        wave_bitonic64_desc(f);
+                        m &= m - 1;
+                        m &= __ballot(nx > kth());
+                    }
+                }
+                if (lane < k) {
+                    const uint32_t key = (uint32_t)(f >> 32);
+                    const int col = (int)(0xffffffffu - (uint32_t)f);
+                    const int64_t o = (int64_t)row * k + lane;
+                    if (F32) {
+                        ((float *)a.values)[o] = __uint_as_float(unkey32(key));
+                    } else {
+                        ((uint16_t *)a.values)[o] = (uint16_t)unkey16(key);
+                    }
+                    a.indices[o] = col < V ? col : V - 1;
+                }
+                if (lane == 0) sm.flag = 0;
+            }
+        }
+        __syncthreads();
+        if (!sm.flag) return;
+    } else if (kp > 0) {
         // Up to 512 samples, two per thread, as composites (key << 32) | (~column): their
         // descending order is (value desc, column asc). Every wave sorts its 128, and two rounds
         // of bitonic merges keep the top-128 of the four runs (the elementwise maximum of a run
@@ -341,8 +413,28 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
     }
     if (lane == 0) sm.red[wave] = cnt;
     __syncthreads();
-    const bool overflow = max(max(sm.red[0], sm.red[1]), max(sm.red[2], sm.red[3])) > (uint32_t)SS_K ||
-                          V < k || no_bound;
+    const uint32_t most = max(max(sm.red[0], sm.red[1]), max(sm.red[2], sm.red[3]));
+    const bool overflow = most > (uint32_t)SS_K || V < k || no_bound;
+    if (!overflow && k <= 64 && most <= 64) {
+        // k <= 64 and at most 64 survivors per wave: the same network one element per lane
+        uint64_t c = lane < (int)cnt ? run[lane] : 0ull;
+        wave_sort64_desc(c);
+        run[lane] = c;
+        __syncthreads();
+        if (wave < 2) {
+            // top-64 of runs 2w and 2w+1 (the second reversed: a bitonic sequence)
+            uint64_t x = max_u64(sm.runs[2 * wave][lane], sm.runs[2 * wave + 1][63 - lane]);
+            wave_bitonic64_desc(x);
+            sm.runs[2 * wave][lane] = x;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint64_t f = max_u64(sm.runs[0][lane], sm.runs[2][63 - lane]);
+            wave_bitonic64_desc(f);
+            if (lane < k) emit(lane, (uint32_t)(f >> 32), (int)(0xffffffffu - (uint32_t)f));
+        }
+        return;
+    }
     if (!overflow) {
         uint64_t c0 = 2 * lane < (int)cnt ? run[2 * lane] : 0ull;
         uint64_t c1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0ull;

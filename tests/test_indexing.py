@@ -350,15 +350,22 @@ def topk_merge(values, block, k):
                     key=lambda e: (-e[0], e[1]))[:k] for t in range(tiles)]
     comp = lambda e: (e[0] << 32) | (0xffffffff - e[1])  # noqa: E731
     ncand = tiles * k
-    kp = k if ncand <= 512 else (1 << ((512 // tiles).bit_length() - 1)) if tiles <= 512 else 0
+    # k <= 64: 256 samples and a 64-wide top list; else 512 samples and 128
+    slots, width = (256, 64) if k <= 64 else (512, SS_K)
+    kp = k if ncand <= slots else (1 << ((slots // tiles).bit_length() - 1)) if tiles <= slots else 0
+    if k <= 64 and kp == 0:
+
+        slots, width = 512, SS_K
+        kp = (1 << ((512 // tiles).bit_length() - 1)) if tiles <= 512 else 0
+
     exact = sorted((e for lst in lists for e in lst), key=lambda e: (-e[0], e[1]))[:k]
 
     if kp == 0:
 
         return exact, "radix"
 
-    f = sorted((comp(lists[s // kp][s % kp]) for s in range(512) if s // kp < tiles), reverse=True)
-    f = (f + [0] * SS_K)[:SS_K]
+    f = sorted((comp(lists[s // kp][s % kp]) for s in range(slots) if s // kp < tiles), reverse=True)
+    f = (f + [0] * width)[:width]
     beats = sum(1 for t in range(tiles) if kp < k and comp(lists[t][kp]) > f[k - 1]) if kp < k else 0
 
     if beats > TOPK_REFILL_LISTS:
@@ -373,8 +380,8 @@ def topk_merge(values, block, k):
         while m:
 
             lst = lists[t0 + m[0]]
-            r = [comp(lst[kp + 127 - e]) if e >= SS_K - k + kp else 0 for e in range(SS_K)]
-            assert all(kp <= kp + 127 - e < k for e in range(SS_K - k + kp, SS_K))
+            r = [comp(lst[kp + width - 1 - e]) if e >= width - k + kp else 0 for e in range(width)]
+            assert all(kp <= kp + width - 1 - e < k for e in range(width - k + kp, width))
             f = sorted((max(a, b) for a, b in zip(f, r)), reverse=True)
             m = [lane for lane in m[1:] if nx[lane] > f[k - 1]]
 

@@ -366,6 +366,7 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
         case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
         case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
         case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 16384: launch_timed((multistep_tiles_kernel<64, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
@@ -391,7 +392,7 @@ extern "C" int ss_fused_multistep(const ss_multistep_args *a) {
         return SS_ERR_INVALID_ARGUMENT;
     if (a->lookahead < 0 || a->lookahead > 63) return SS_ERR_INVALID_ARGUMENT;
     if (!a->cu_seqlens && a->rows != a->batch * (a->lookahead + 1)) return SS_ERR_INVALID_ARGUMENT;
-    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192 && a->block_n != 16384)
         return SS_ERR_UNSUPPORTED;
     if (a->rows > 65535) return SS_ERR_UNSUPPORTED;  // rows are the tile grid's y dimension
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;

@@ -351,6 +351,7 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
             case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
             case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
             case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 16384: launch_timed((singular_tiles_kernel<64, MODE>), grid, block, tile_smem_bytes<64>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
             default: return SS_ERR_UNSUPPORTED;
         }
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
@@ -379,7 +380,7 @@ extern "C" int ss_fused_singular(const ss_singular_args *a) {
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows < 0 || a->vocab_size <= 0 || a->stride_logits < a->vocab_size)
         return SS_ERR_INVALID_ARGUMENT;
-    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192 && a->block_n != 16384)
         return SS_ERR_UNSUPPORTED;
     if (a->rows > 65535) return SS_ERR_UNSUPPORTED;  // rows are the tile grid's y dimension
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;
@@ -449,7 +450,7 @@ static uint32_t *static_scratch() {
 extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
     using namespace ss;
     if (!a || a->vocab_size <= 0 || a->rows < 0) return SS_ERR_INVALID_ARGUMENT;
-    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192 && a->block_n != 16384)
         return SS_ERR_UNSUPPORTED;
     const int64_t tiles = ((int64_t)a->vocab_size + a->block_n - 1) / a->block_n;
     const int64_t world = a->world_size > 1 ? a->world_size : 1;

@@ -41,7 +41,7 @@ struct SampleSmem {
 // grammar row staged for the prologue (stage_grammar) may overlay them (TILE_OVERLAY).
 template <int E>
 struct TileSmem {
-    uint32_t scan[SS_WAVES * 8];  // workgroup scans of up to 8 values per thread
+    uint32_t scan[SS_WAVES * 16];  // workgroup scans of up to 16 values per thread
     uint32_t red[SS_WAVES];
     uint32_t cnt[SS_WAVES];       // survivors of each wave
     int32_t hist[64];             // drafted tokens that extend the decode history
@@ -53,7 +53,7 @@ struct TileSmem {
 };
 
 // Byte offset in TileSmem where a staged grammar row may begin.
-constexpr int TILE_OVERLAY = (SS_WAVES * 8 + 2 * SS_WAVES + 64) * 4;
+constexpr int TILE_OVERLAY = (SS_WAVES * 16 + 2 * SS_WAVES + 64) * 4;
 static_assert(TILE_OVERLAY % 16 == 0, "16-byte grammar stores");
 static_assert(TILE_OVERLAY == __builtin_offsetof(TileSmem<16>, run), "overlay starts at the runs");
 
@@ -763,15 +763,23 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     if constexpr (MODE == MODE_DIRECT) {
         if (!(u.g || u.rep || u.mult || u.bias)) {
             plain_keys<E>(rs, u, col0, V, lw, keys);
-        } else if constexpr (E == 32) {
-            // The processor chain in two 4096-column halves: element j of the second half is
-            // element j + 16 of the tile (4 chunks of 1024 columns further). Its per-element
-            // state for all 32 elements at once would set the kernel's register allocation, and so
-            // its occupancy, for every row (144 VGPRs, three waves per SIMD, against 90 for the
-            // plain rows alone).
+        } else if constexpr (E >= 32) {
+            // The processor chain in 4096-column passes: element j of pass h is element j + 16 h
+            // of the tile (4 h chunks of 1024 columns further). Its per-element state for all E
+            // elements at once would set the kernel's register allocation, and so its occupancy,
+            // for every row (144 VGPRs at E = 32, three waves per SIMD, against 90 for the plain
+            // rows alone).
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const u32x2 lh[4] = {lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]};
+            for (int h = 0; h < E / 16; ++h) {
+                // at E = 64 a pass reloads its logits with its planes (in the same round of loads):
+                // the preloaded ones would stay live through every pass
+                u32x2 lh[4];
+                if constexpr (E >= 64) {
+                    load_logits_vec<16>(rs.logits, col0 + 4 * 4 * SS_BLOCK * h, V, lh);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) lh[c] = lw[4 * h + c];
+                }
                 Planes<16> pl;
                 issue_planes<16>(rs, u, true, rs.shard + col0 + 4 * 4 * SS_BLOCK * h, pl);
                 Keys<16> kh;
@@ -784,14 +792,20 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
             issue_planes<E>(rs, u, true, rs.shard + col0, pl);
             direct_keys<E>(rs, u, col0, V, hist, lw, pl, keys);
         }
-    } else if constexpr (E == 32 && MODE == MODE_GATHER_VEC) {
-        // Two 4096-column halves, as above: the gathered columns and planes of all 32 elements
-        // at once would hold 156 VGPRs (three waves per SIMD).
+    } else if constexpr ((E >= 32 && MODE == MODE_GATHER_VEC) || E >= 64) {
+        // 4096-column passes, as above: the gathered columns and planes of all 32 elements at
+        // once would hold 156 VGPRs (three waves per SIMD).
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u32x2 lh[4] = {lw[4 * h], lw[4 * h + 1], lw[4 * h + 2], lw[4 * h + 3]};
+        for (int h = 0; h < E / 16; ++h) {
+            u32x2 lh[4];
+            if constexpr (MODE != MODE_SCALAR && E >= 64) {
+                load_logits_vec<16>(rs.logits, col0 + 4 * 4 * SS_BLOCK * h, V, lh);
+            } else if constexpr (MODE != MODE_SCALAR) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) lh[c] = lw[4 * h + c];
+            }
             Keys<16> kh;
-            gather_keys<16, true>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
+            gather_keys<16, MODE == MODE_GATHER_VEC>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
 #pragma unroll
             for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
         }
@@ -816,26 +830,46 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// One wave's part of the tile selection: its elements with key > T (or, with EXACT, those key == T
-// elements whose bit is set in tie_keep) go to the wave's own LDS region as composites (key << 16) | (0xffff - column), placed
-// by ballot and mbcnt, and the wave sorts them there in descending order (zero padded to 128).
-// Returns the wave's survivor count; above 128 the region holds only the first 128, unsorted.
-template <int E, bool EXACT>
-__device__ __forceinline__ uint32_t wave_survivors(TileSmem<E> &sm, const Keys<E> &keys, uint32_t T,
-                                                   uint32_t tie_keep) {
+// A wave's keys as wave_survivors_masked spilled them to workgroup memory (pair i of lane l at
+// TileSmem::keys[wave][i * 64 + l]), read through a volatile pointer: every use is a fresh LDS
+// read, so the rare exact cut keeps no copy of the keys in registers and does not set the tile
+// kernels' register allocation (at E = 32 it would hold 92 VGPRs instead of 57).
+struct SpilledKeys {
+    const volatile uint32_t *p;
+    __device__ __forceinline__ uint32_t pair(int i) const { return p[i * 64]; }
+    // count of this lane's keys k with pred(k)
+    template <int E, class Pred>
+    __device__ __forceinline__ uint32_t count(Pred pred) const {
+        uint32_t n = 0;
+#pragma unroll 4
+        for (int i = 0; i < E / 2; ++i) {
+            const uint32_t w = pair(i);
+            n += (pred(w & 0xffffu) ? 1u : 0u) + (pred(w >> 16) ? 1u : 0u);
+        }
+        return n;
+    }
+};
+
+// One wave's part of the exact cut: its elements with key > T, and those key == T elements whose
+// bit is set in tie_keep, go to the wave's own LDS region as composites (key << 16) |
+// (0xffff - column), placed by ballot and mbcnt, and the wave sorts them there in descending order
+// (zero padded to 128). The tie rule keeps every wave within 128.
+template <int E>
+__device__ __forceinline__ void wave_survivors_exact(TileSmem<E> &sm, const SpilledKeys &sk, uint32_t T,
+                                                     uint64_t tie_keep) {
     const int lane = lane_id();
     uint32_t *run = sm.run[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
     const uint32_t cb = 0xffffu - 4u * threadIdx.x;  // 0xffff - column of the lane's element 0
-    // Wave-uniform count, saturated at SS_K + 1 so that a count above SS_K still reads as an
-    // overflow. Writes happen only while cnt <= SS_K: positions then stay below SS_K + 64, inside
-    // the run (an overflowed run is rewritten by the exact pass).
-    uint32_t cnt = 0;
-#pragma unroll
+    uint32_t cnt = 0;  // wave-uniform
+#pragma unroll 2
     for (int j = 0; j < E; ++j) {
-        const bool p = EXACT ? keys.gt(j, T) | (((tie_keep >> j) & 1u) != 0u) : keys.gt(j, T);
+        const uint32_t w = sk.pair(j >> 1);
+        const uint32_t key = (j & 1) ? w >> 16 : w & 0xffffu;
+        const bool p = key > T || ((tie_keep >> j) & 1ull) != 0ull;
         const uint64_t m = __ballot(p);
         uint32_t *at = run + cnt;  // uniform
-        if (p && cnt <= (uint32_t)SS_K) at[mbcnt64(m)] = keys.composite(j, cb);
+        if (p && cnt <= (uint32_t)SS_K)
+            at[mbcnt64(m)] = ((key << 16) | cb) - (uint32_t)((j >> 2) * (SS_BLOCK * 4) + (j & 3));
         cnt = min(cnt + (uint32_t)__popcll(m), (uint32_t)SS_K + 1u);
     }
     if (cnt <= 64) {
@@ -843,18 +877,17 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem<E> &sm, const Keys<E
         wave_sort64_desc(v);
         run[lane] = v;
         run[64 + lane] = 0u;
-    } else if (cnt <= (uint32_t)SS_K) {
+    } else {
         uint32_t a0 = 2 * lane < (int)cnt ? run[2 * lane] : 0u;
         uint32_t a1 = 2 * lane + 1 < (int)cnt ? run[2 * lane + 1] : 0u;
         wave_bitonic128_desc<2>(a0, a1);
         run[2 * lane] = a0;
         run[2 * lane + 1] = a1;
     }
-    return cnt;
 }
 
-// The survivors (key > T) of one wave, as wave_survivors<E, false> leaves them, without a ballot
-// per element position. Every lane builds a bitmask of its surviving elements with packed 16-bit
+// The survivors (key > T) of one wave, unsorted, in the wave's run, without a ballot per element
+// position. Every lane builds a bitmask of its surviving elements with packed 16-bit
 // operations (bit i: element 2i, bit 16 + i: element 2i + 1), an exclusive scan of the lanes'
 // counts gives each lane its first position in the run, and the lane writes its survivors one
 // set bit at a time (a lane holds a few), reading each survivor's key back from its keys stored
@@ -863,13 +896,15 @@ __device__ __forceinline__ uint32_t wave_survivors(TileSmem<E> &sm, const Keys<E
 template <int E>
 __device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const Keys<E> &keys,
                                                           uint32_t T) {
-    static_assert(E / 2 <= 16, "one mask bit per element");
+    constexpr int NM = (E / 2 + 15) / 16;  // 32-bit masks of 16 key pairs each
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint32_t *run = sm.run[wave];
     uint32_t *spill = sm.keys[wave];
     const uint32_t tt = T | (T << 16);
-    uint32_t mask = 0;
+    uint32_t mask[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) mask[m] = 0;
 #pragma unroll
     for (int i = 0; i < E / 2; ++i) {
         // max(key - T, 0) is nonzero exactly when key > T; its minimum with 1 is that bit. Written
@@ -878,23 +913,29 @@ __device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const
         uint32_t d;
         asm("v_pk_sub_u16 %0, %1, %2 clamp\n\tv_pk_min_u16 %0, %0, %3" : "=&v"(d)
             : "v"(keys.p[i]), "v"(tt), "v"(0x00010001u));
-        mask |= d << i;
+        mask[i >> 4] |= d << (i & 15);
         spill[i * 64 + lane] = keys.p[i];
     }
-    const uint32_t n = (uint32_t)__popc(mask);
+    uint32_t n = 0;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) n += (uint32_t)__popc(mask[m]);
     const uint32_t inc = wave_inclusive_sum(n);
     const uint32_t total = lane_u32(inc, 63);
     if (total > (uint32_t)SS_K) return total;
     uint32_t pos = inc - n;
     const uint32_t cb = 0xffffu - 4u * threadIdx.x;  // 0xffff - column of the lane's element 0
-    while (mask) {
-        const uint32_t b = (uint32_t)__builtin_ctz(mask);
-        mask &= mask - 1u;
-        const uint32_t i = b & 15u, hi = b >> 4;
-        const uint32_t key = (spill[i * 64 + lane] >> (hi << 4)) & 0xffffu;
-        const uint32_t j = 2u * i + hi;  // element index; its column offset in the tile
-        const uint32_t off = (j >> 2) * (SS_BLOCK * 4) + (j & 3u);
-        run[pos++] = ((key << 16) | cb) - off;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        uint32_t mk = mask[m];
+        while (mk) {
+            const uint32_t b = (uint32_t)__builtin_ctz(mk);
+            mk &= mk - 1u;
+            const uint32_t i = 16u * (uint32_t)m + (b & 15u), hi = b >> 4;
+            const uint32_t key = (spill[i * 64 + lane] >> (hi << 4)) & 0xffffu;
+            const uint32_t j = 2u * i + hi;  // element index; its column offset in the tile
+            const uint32_t off = (j >> 2) * (SS_BLOCK * 4) + (j & 3u);
+            run[pos++] = ((key << 16) | cb) - off;
+        }
     }
     return total;
 }
@@ -981,15 +1022,12 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
     if (lane == 0) sm.cnt[wave] = cnt;
     __syncthreads();
     if (max(max(sm.cnt[0], sm.cnt[1]), max(sm.cnt[2], sm.cnt[3])) > (uint32_t)SS_K) {
-        // Exact cut. T is the 128th key: usually the bound itself (ties at lo, e.g. the -inf of
-        // grammar-masked elements), which one pair of counts confirms; otherwise bisection.
-        uint32_t gt = 0, ge = 0;
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            gt += keys.gt(j, lo);
-            ge += keys.ge(j, lo);
-        }
-        const uint32_t above_lo = block_count(gt, sm.red), from_lo = block_count(ge, sm.red);
+        // Exact cut, from the spilled keys. T is the 128th key: usually the bound itself (ties at
+        // lo, e.g. the -inf of grammar-masked elements), which one pair of counts confirms;
+        // otherwise bisection.
+        const SpilledKeys sk{sm.keys[wave] + lane};
+        const uint32_t above_lo = block_count(sk.count<E>([&](uint32_t k) { return k > lo; }), sm.red);
+        const uint32_t from_lo = block_count(sk.count<E>([&](uint32_t k) { return k >= lo; }), sm.red);
         uint32_t above;  // keys > T
         if (lo != 0 && above_lo < (uint32_t)SS_K && from_lo >= (uint32_t)SS_K) {
             T = lo;
@@ -999,43 +1037,35 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
 #pragma unroll 1
             for (int b = 15; b >= 0; --b) {
                 const uint32_t c = t | (1u << b);
-                uint32_t k = 0;
-#pragma unroll
-                for (int j = 0; j < E; ++j) k += keys.ge(j, c);
-                if (block_count(k, sm.red) >= (uint32_t)SS_K) t = c;
+                if (block_count(sk.count<E>([&](uint32_t k) { return k >= c; }), sm.red) >= (uint32_t)SS_K) t = c;
             }
             T = t;
-            uint32_t k = 0;
-#pragma unroll
-            for (int j = 0; j < E; ++j) k += keys.gt(j, T);
-            above = block_count(k, sm.red);
+            above = block_count(sk.count<E>([&](uint32_t k) { return k > T; }), sm.red);
         }
         // The first `need` keys equal to T in column order (chunk, thread, element) are kept: their
-        // ranks come from one workgroup scan of the per-chunk tie counts.
+        // ranks come from one workgroup scan of the tie counts per chunk, chunk after chunk (a
+        // runtime loop over the spilled keys, so that the counts of all chunks are never live
+        // together: as registers they would set the kernel's allocation).
         const uint32_t need = (uint32_t)SS_K - above;
-        constexpr int NCH = E / 4;
-        uint32_t eq[NCH], tot[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            eq[c] = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) eq[c] += keys.eq(4 * c + i, T);
-        }
-        block_exclusive_scan<NCH>(eq, tot, sm.scan);
-        uint32_t tie_keep = 0, before = 0;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            uint32_t r = before + eq[c];  // rank of this thread's first tie in chunk c
+        uint64_t tie_keep = 0;
+        uint32_t before = 0;
+#pragma unroll 1
+        for (int c = 0; c < E / 4; ++c) {
+            const uint32_t w0 = sk.pair(2 * c), w1 = sk.pair(2 * c + 1);
+            const uint32_t k4[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
+            uint32_t eq[1] = {(uint32_t)(k4[0] == T) + (k4[1] == T) + (k4[2] == T) + (k4[3] == T)}, tot[1];
+            block_exclusive_scan<1>(eq, tot, sm.scan);
+            uint32_t r = before + eq[0];  // rank of this thread's first tie in chunk c
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (keys.eq(4 * c + i, T)) {
-                    tie_keep |= (r < need ? 1u : 0u) << (4 * c + i);
+                if (k4[i] == T) {
+                    tie_keep |= (r < need ? 1ull : 0ull) << (4 * c + i);
                     ++r;
                 }
             }
-            before += tot[c];
+            before += tot[0];
         }
-        wave_survivors<E, true>(sm, keys, T, tie_keep);
+        wave_survivors_exact<E>(sm, sk, T, tie_keep);
         __syncthreads();
     }
     if (wave < 2) {

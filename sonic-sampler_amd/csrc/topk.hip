@@ -512,6 +512,7 @@ static int launch_topk_tiles(const ss_topk_args *a, int tiles, dim3 grid, dim3 b
         case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8, true>), grid, block, 0, s, *a, tiles); break;
         case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16, true>), grid, block, 0, s, *a, tiles); break;
         case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32, true>), grid, block, 0, s, *a, tiles); break;
+        case 16384: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 64, true>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     return SS_OK;
@@ -537,7 +538,7 @@ extern "C" int ss_topk(const ss_topk_args *a) {
         return SS_ERR_INVALID_ARGUMENT;
     if (a->rows < 0 || a->vocab_size <= 0) return SS_ERR_INVALID_ARGUMENT;
     if (a->k < 1 || a->k > SS_MAX_K || (a->k & (a->k - 1)) != 0) return SS_ERR_INVALID_ARGUMENT;
-    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192)
+    if (a->block_n != 1024 && a->block_n != 2048 && a->block_n != 4096 && a->block_n != 8192 && a->block_n != 16384)
         return SS_ERR_UNSUPPORTED;
     if (a->dtype != SS_DTYPE_BF16 && a->dtype != SS_DTYPE_F32) return SS_ERR_UNSUPPORTED;
     const int tiles = (a->vocab_size + a->block_n - 1) / a->block_n;

@@ -49,7 +49,7 @@ from sonic_sampler.ops.base import MAX_K
 
 VOCAB_BUCKETS = (8192, 32768, 131072, 262144)
 BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
-WIDTHS = (1024, 2048, 4096, 8192)
+WIDTHS = (1024, 2048, 4096, 8192, 16384)
 TOLERANCE = 0.02
 
 KINDS = ("singular", "drafting", "multistep")

@@ -32,7 +32,7 @@ I32 = torch.int32
 U32 = torch.uint32
 
 # Tile widths the gfx950 kernels are compiled for.
-SUPPORTED_BLOCK_N = (1024, 2048, 4096, 8192)
+SUPPORTED_BLOCK_N = (1024, 2048, 4096, 8192, 16384)
 
 
 def cdiv(a: int, b: int) -> int:

@@ -131,8 +131,9 @@ def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
                    slot_mapping=slot_mapping)
 
 
-@pytest.mark.parametrize("seed", [44, 45])
-def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed):
+@pytest.mark.parametrize("seed,draft_vocab,target_vocab,block", [(44, 6144, 8197, 2048), (45, 6144, 8197, 2048),
+                                                                (46, 40000, 131075, 16384)])
+def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed, draft_vocab, target_vocab, block):
     """Drafting through d2t into a 8197-token target vocabulary (its last grammar word holds 5
     tokens) with every processor on: the tile kernel stages each row's 257 grammar words in
     workgroup memory, clears the bits past the vocabulary and reads a zero quad for clamped
@@ -143,7 +144,6 @@ def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed):
     from sonic_sampler.interface import UnshardedFusedSingular
 
     slots, rows, gamma, t = 10, 8, 3, 1
-    draft_vocab, target_vocab = 6144, 8197
     g = torch.Generator().manual_seed(seed)
     host = random_host(slots, gamma + 1, target_vocab, seed, indicator=EVERY_PROCESSOR)
     host.grammar.view(torch.int32)[::2] = -1
@@ -157,7 +157,7 @@ def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed):
     print(f"staged grammar V_t={target_vocab} seed={seed}", flush=True)
 
     sampler = UnshardedFusedSingular.initialize(vocab_size=draft_vocab, batch_size=rows, lookahead=gamma,
-                                                block_size=2048, max_top_logprobs=5, device=DEV)
+                                                block_size=block, max_top_logprobs=5, device=DEV)
     probs = torch.zeros(slots, target_vocab, dtype=torch.bfloat16, device=DEV)
     selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=tokens.to(DEV),
                                  probabilities=probs, slot_mapping=slot_mapping.to(DEV),
@@ -223,6 +223,21 @@ def test_8192_tiles_autoregressive_every_processor(vocab):
     assert autoregressive_case(logits, host, 8192) >= rows - 1
 
 
+@pytest.mark.parametrize("vocab,indicator", [(65536, EVERY_PROCESSOR), (57344 + 4100, EVERY_PROCESSOR),
+                                             (131072, None), (40000, 0x400)])
+def test_16384_tiles_autoregressive(vocab, indicator):
+    """16384-column tiles (64 elements per thread): the processor chain in four 4096-column passes,
+    survivor masks over 32 key pairs, the exact cut's tie scan in two groups; partial last tiles."""
+
+    from bench import spiked_logits
+
+    rows = 12
+    print(f"16384 tiles, autoregressive: V={vocab} indicator={indicator}", flush=True)
+    host = random_host(rows, 1, vocab, vocab % 91, indicator)
+    logits = spiked_logits(rows, vocab, seed=vocab + 5).to(DEV)
+    assert autoregressive_case(logits, host, 16384) >= rows - 1
+
+
 @pytest.mark.parametrize("vocab", SPLIT_VOCABS)
 def test_8192_tiles_drafting_history(vocab):
     """Drafting without d2t: the first t drafted columns extend the decode history."""
@@ -255,8 +270,8 @@ def test_8192_tiles_drafting_history(vocab):
     check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=slot_mapping)
 
 
-@pytest.mark.parametrize("vocab", SPLIT_VOCABS)
-def test_8192_tiles_multistep_every_processor(vocab):
+@pytest.mark.parametrize("vocab,block", [(v, 8192) for v in SPLIT_VOCABS] + [(65536, 16384), (40004, 16384)])
+def test_8192_tiles_multistep_every_processor(vocab, block):
 
     from bench import MultistepWorkload, spiked_logits
 
@@ -273,8 +288,8 @@ def test_8192_tiles_multistep_every_processor(vocab):
     work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
                              cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
                              max_top_logprobs=4, probabilities=probabilities)
-    print(f"8192 tiles, multistep: V={vocab}", flush=True)
-    verification, buffers, _ = run_verifier(work, update_counts=True, block_size=8192,
+    print(f"{block} tiles, multistep: V={vocab}", flush=True)
+    verification, buffers, _ = run_verifier(work, update_counts=True, block_size=block,
                                             slot_mapping=slot_mapping.to(DEV))
 
     state = oracle.State.from_buffers(host)

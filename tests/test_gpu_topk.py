@@ -52,7 +52,8 @@ def test_ties_and_k(k, dtype):
     check(logits, k, block_size=1024)
 
 
-@pytest.mark.parametrize("vocab,block", [(128256, None), (151936, None), (262144, None), (5000, 1024), (40003, 2048)])
+@pytest.mark.parametrize("vocab,block", [(128256, None), (151936, None), (262144, None), (5000, 1024), (40003, 2048),
+                                         (131072, 16384), (40004, 16384)])
 def test_bf16_shapes(vocab, block):
 
     from bench import spiked_logits

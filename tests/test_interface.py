@@ -264,12 +264,13 @@ def test_autotune_ranks_widths_and_round_trips(tmp_path):
 
     # a wider width within the tolerance of the best score wins
     times = {1024: 10.0, 2048: 10.1, 4096: 11.0, 8192: 12.0}
-    near = autotune([32768], [1], measure=lambda kind, v, b, w: times[w])
+    near = autotune([32768], [1], widths=times, measure=lambda kind, v, b, w: times[w])
     assert near.vocab.get(32768).batch.get(1).best.block_n == 2048
 
     # the worst slowdown over the kinds decides: 4096 is 5% behind on one kind, 1024 2x on another
     split = {"singular": {1024: 10.0, 2048: 11.0, 4096: 10.5, 8192: 13.0},
              "multistep": {1024: 20.0, 2048: 12.0, 4096: 10.0, 8192: 10.2},
              "topk": {1024: 9.0, 2048: 9.5, 4096: 9.2, 8192: 9.9}}
-    mixed = autotune([32768], [8], measure=lambda kind, v, b, w: split[kind][w], kinds=split)
+    mixed = autotune([32768], [8], widths=split["singular"], measure=lambda kind, v, b, w: split[kind][w],
+                     kinds=split)
     assert mixed.vocab.get(32768).batch.get(8).best.block_n == 4096

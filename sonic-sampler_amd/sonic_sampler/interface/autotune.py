@@ -1,24 +1,31 @@
-"""Measures a dispatch table for this GPU. For every (vocabulary, batch) bucket, each call kind
-that the table serves (``KINDS``: the fused single step with every processor on and logprobs, the
-drafting step through d2t into an 8x wider target vocabulary under a grammar mask, timed in the
-buckets of draft vocabularies (at most ``DRAFT_VOCAB_MAX`` columns), and the multistep
-verification at lookahead 3; ``"topk"``, the bounded top-128, on request) is timed at each
-compiled tile width. A width's score is its worst slowdown over the kinds (time / the
-kind's fastest time), and the bucket gets the widest width whose score is within ``TOLERANCE`` of
-the best (run-to-run noise is about that size, and a wider tile means a smaller scratchpad). The
-standalone top-k reads the same table, as in the reference; at k = 128 its tile kernel prefers
-wider tiles than the fused calls, so scoring it by default would slow the fused path it shares
-buckets with.
+"""Measures the dispatch tables for this GPU. For every (vocabulary, batch) bucket, each call kind
+(``KINDS``) is timed at each compiled tile width:
 
-The table has the schema of the reference's generated tables (``resources/dispatch/
+- ``singular``: the fused single step with every processor on and logprobs;
+- ``drafting``: the drafting step through d2t into an 8x wider target vocabulary under a grammar
+  mask, timed in the buckets of draft vocabularies (at most ``DRAFT_VOCAB_MAX`` columns);
+- ``multistep``: the verification at lookahead 3 with a typical verification state (temperature,
+  top-k, top-p, top logprobs; ``VERIFY_INDICATOR``);
+- ``topk``: the bounded top-128.
+
+Each kind gets a table of its own (``--out`` names the shared one, which the ``singular`` kind
+scores; the others are written beside it as ``<stem>_<kind>.toml``): the kinds' best widths differ
+(the verification, bound by per-element instructions at two bytes per element, prefers wider tiles
+than the decode step, which reads four planes per element), so one table scored over all of them
+would slow each. Within a table a width's score is its worst slowdown over the kinds it serves
+(time / that kind's fastest time), and the bucket gets the widest width whose score is within
+``TOLERANCE`` of the best (run-to-run noise is about that size, and a wider tile means a smaller
+scratchpad). ``--from-log`` scores the times of an earlier run's log again instead of measuring.
+
+The tables have the schema of the reference's generated tables (``resources/dispatch/
 sm100_k128.toml``, read by ``interface/dispatch.py``), whose priorities rank one configuration per
 selection strategy; the gfx950 kernels have a single exact selection, so each bucket holds one
 configuration (priority 0) and the measured times go to the log. ``TwoStageTiling`` sizes its
-scratchpad for the smallest width of the vocabulary bucket and launches each call at the width of
-the bucket of its row count.
+scratchpad for the smallest width of the vocabulary bucket (over the kinds that share it) and
+launches each call at the width of the bucket of its row count.
 
     python -m sonic_sampler.interface.autotune --out gfx950_k128.toml [--vocab 8192,32768 --batch 1,64]
-    [--kinds singular,multistep,topk]
+    [--kinds singular,multistep] [--from-log autotune.log]
 
 Tile strategies and warp counts are recorded with fixed values: the gfx950 kernels have one exact
 selection and 256-thread workgroups, so the tile width is the only tuned parameter.
@@ -52,10 +59,11 @@ BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 512)
 WIDTHS = (1024, 2048, 4096, 8192, 16384)
 TOLERANCE = 0.02
 
-KINDS = ("singular", "drafting", "multistep")
-ALL_KINDS = ("singular", "drafting", "multistep", "topk")
+KINDS = ("singular", "drafting", "multistep", "topk")
+SHARED = "singular"  # the kind the shared table serves
 LOOKAHEAD = 3
 DRAFT_VOCAB_MAX = 32768
+VERIFY_INDICATOR = 0x5A0  # temperature, top-k, top-p, top logprobs
 
 Measure = Callable[[str, int, int, int], float]
 
@@ -132,6 +140,8 @@ def measure_kind(kind: str, vocab: int, batch: int, block_n: int, *, device="cud
 
             return None
 
+        from sonic_sampler.core.flags import Flags, Indicator
+
         n = min(LOOKAHEAD + 1, batch)
         requests = batch // n
         rows = requests * n
@@ -139,7 +149,16 @@ def measure_kind(kind: str, vocab: int, batch: int, block_n: int, *, device="cud
                                                       block_size=block_n, max_top_logprobs=5, device=device)
         view = logits[:rows].view(requests, n, vocab)
         tokens = drafted[:rows].view(requests, n)
-        return _time(lambda: verifier(view, tokens, buffers, logprobs=True, philox_seed=1), steps, warmup)
+        flags = buffers.flags
+        buffers.flags = Flags.from_values(flags.layout.rows, LOOKAHEAD + 1, Indicator(VERIFY_INDICATOR),
+                                          Indicator(VERIFY_INDICATOR), device=device)
+        try:
+
+            return _time(lambda: verifier(view, tokens, buffers, logprobs=True, philox_seed=1), steps, warmup)
+
+        finally:
+
+            buffers.flags = flags
 
     if kind == "topk":
 
@@ -190,7 +209,8 @@ def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[i
              k: int = MAX_K, arch: Optional[str] = None, log=None) -> DispatchSummary:
     """The dispatch table measured by `measure(kind, vocab, batch, block_n) -> microseconds or
     None` (by default `measure_kind` on the current GPU). Widths that leave fewer than two tiles
-    are skipped."""
+    are skipped, and so are buckets where no kind has a call (lookups there take the nearest
+    bucket, or the shared table)."""
 
     measure = measure or measure_kind
     arch = arch or resolve_arch(None)
@@ -222,6 +242,10 @@ def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[i
 
                 lines.append(f"{kind} " + " ".join(f"{w}:{times[w]:.2f}" for w in usable))
 
+            if not lines:
+
+                continue
+
             low = min(score.values())
             pick = max(w for w in usable if score[w] <= low * (1 + TOLERANCE))
 
@@ -232,7 +256,9 @@ def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[i
             config = RuntimeConfig(priority=0, block_n=pick, strategy="radix", first_warps=4, second_warps=4)
             batches.append(BatchBucket(size=b, config=[config]))
 
-        vocab.append(VocabBucket(size=v, batch=batches))
+        if batches:
+
+            vocab.append(VocabBucket(size=v, batch=batches))
 
     stamp = datetime.datetime.now(datetime.timezone.utc).isoformat()
 
@@ -240,24 +266,82 @@ def autotune(vocab_sizes: Iterable[int] = VOCAB_BUCKETS, batch_sizes: Iterable[i
                            k=k, vocab=vocab)
 
 
+def table_path(out: str, kind: str) -> str:
+    """Where the table of `kind` goes when the shared table goes to `out`."""
+
+    if kind == SHARED:
+
+        return out
+
+    stem, dot, ext = out.rpartition(".")
+
+    return f"{stem}_{kind}.{ext}" if dot else f"{out}_{kind}"
+
+
+def parse_log(lines: Iterable[str]) -> Dict[tuple, float]:
+    """Times of a run's log: {(kind, vocab, batch, block_n): microseconds}, from lines
+    ``vocab V batch B: pick | kind w:t w:t ... | kind ...``."""
+
+    times = {}
+
+    for line in lines:
+
+        if not line.startswith("vocab ") or "|" not in line:
+
+            continue
+
+        head, *parts = line.strip().split(" | ")
+        words = head.split()
+        vocab, batch = int(words[1]), int(words[3].rstrip(":"))
+
+        for part in parts:
+
+            kind, *entries = part.split()
+
+            for entry in entries:
+
+                width, time = entry.split(":")
+                times[(kind, vocab, batch, int(width))] = float(time)
+
+    return times
+
+
 def main(argv=None) -> int:
 
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--out", required=True, help="path of the TOML table to write")
+    parser.add_argument("--out", required=True, help="path of the shared TOML table to write")
     parser.add_argument("--vocab", default=",".join(map(str, VOCAB_BUCKETS)))
     parser.add_argument("--batch", default=",".join(map(str, BATCH_BUCKETS)))
     parser.add_argument("--widths", default=",".join(map(str, WIDTHS)))
     parser.add_argument("--kinds", default=",".join(KINDS))
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--from-log", default=None, help="score the times of an earlier run's log")
     args = parser.parse_args(argv)
 
     ints = lambda text: [int(x) for x in text.split(",") if x]  # noqa: E731
-    summary = autotune(ints(args.vocab), ints(args.batch), ints(args.widths),
-                       measure=lambda *key: measure_kind(*key, steps=args.steps, warmup=args.warmup),
-                       kinds=[x for x in args.kinds.split(",") if x], log=lambda line: print(line, flush=True))
-    summary.save(args.out)
-    print(f"wrote {args.out}", flush=True)
+    kinds = [x for x in args.kinds.split(",") if x]
+
+    if args.from_log:
+
+        with open(args.from_log) as f:
+
+            logged = parse_log(f)
+
+        measure = lambda *key: logged.get(key)  # noqa: E731
+
+    else:
+
+        measure = functools.lru_cache(maxsize=None)(
+            lambda *key: measure_kind(*key, steps=args.steps, warmup=args.warmup))
+
+    for kind in kinds:
+
+        summary = autotune(ints(args.vocab), ints(args.batch), ints(args.widths), measure=measure, kinds=[kind],
+                           log=lambda line: print(line, flush=True))
+        path = table_path(args.out, kind)
+        summary.save(path)
+        print(f"wrote {path}", flush=True)
 
     return 0
 

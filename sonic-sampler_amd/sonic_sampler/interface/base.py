@@ -9,8 +9,8 @@ in-flight buffers: ``scratchpad [B * (gamma + 1), blocks * 128]`` uint32 and, fo
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-from typing import Optional, Tuple, Union
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Tuple, Union
 
 import torch
 
@@ -120,7 +120,10 @@ def resolve_dispatch(
     vocab_size: int,
     block_size: Optional[int],
     arch: Union[int, str, None],
+    kind: Optional[str] = None,
 ) -> Tuple[Optional[VocabBucket], int]:
+    """The vocabulary bucket of the table (of call kind `kind` where it has its own table with a
+    bucket for `vocab_size`) and its smallest width, or no bucket and `block_size`."""
 
     if k > MAX_K:
 
@@ -139,6 +142,12 @@ def resolve_dispatch(
         if (bucket := dispatch.vocab.get(size=vocab_size)) is None:
 
             raise ValueError("unable to match tuning configuration for given vocabulary size")
+
+        if kind is not None and (table := DispatchSummary.load(k=MAX_K, arch=arch, kind=kind)) is not None:
+
+            if (own := table.vocab.get(size=vocab_size)) is not None:
+
+                bucket = own
 
         return bucket, bucket.block_n
 
@@ -183,6 +192,9 @@ class TwoStageTiling:
     # Tuned dispatch, when resolved from a table.
     dispatch: Optional[VocabBucket]
 
+    # Tuned dispatch of further call kinds that share the buffers (`tuning(..., kind=)`).
+    kind_dispatch: Dict[str, VocabBucket] = field(default_factory=dict)
+
     @classmethod
     def resolve(
         cls,
@@ -192,9 +204,10 @@ class TwoStageTiling:
         block_size: Optional[int] = None,
         arch: Union[int, str, None] = None,
         ensure_multiblock: bool = True,
+        kind: Optional[str] = None,
     ):
 
-        dispatch, block_n = resolve_dispatch(k, vocab_size, block_size, arch)
+        dispatch, block_n = resolve_dispatch(k, vocab_size, block_size, arch, kind)
         vocabulary = Vocabulary.resolve(vocab_size, block_n)
 
         if ensure_multiblock and (blocks := vocabulary.blocks) <= 1:
@@ -222,16 +235,17 @@ class TwoStageTiling:
         unpacked_buffers: bool = True,
         values_dtype: torch.dtype = FP32,
         device=None,
+        kinds: Tuple[Optional[str], ...] = (None,),
     ):
+        """`kinds` names the call kinds that will use the buffers: the first one's table gives
+        `dispatch`, the others' go to `kind_dispatch`, and the scratchpad holds the lists of the
+        smallest width among them (None: the shared table)."""
 
-        dispatch, vocabulary, block_n = cls.resolve(
-            vocab_size=vocab_size,
-            k=k,
-            top_logprobs=top_logprobs,
-            block_size=block_size,
-            arch=arch,
-            ensure_multiblock=ensure_multiblock,
-        )
+        resolved = [cls.resolve(vocab_size=vocab_size, k=k, top_logprobs=top_logprobs, block_size=block_size,
+                                arch=arch, ensure_multiblock=ensure_multiblock, kind=kind) for kind in kinds]
+        dispatch = resolved[0][0]
+        _, vocabulary, block_n = min(resolved, key=lambda r: r[2])
+        extra = {kind: r[0] for kind, r in zip(kinds[1:], resolved[1:]) if kind is not None and r[0] is not None}
 
         target = default_device(device)
         total_rows = batch_size * (lookahead + 1)
@@ -253,6 +267,7 @@ class TwoStageTiling:
             vocabulary=vocabulary,
             scratchpad=scratchpad,
             dispatch=dispatch,
+            kind_dispatch=extra,
         )
 
         return instance, values, indices
@@ -262,14 +277,17 @@ class TwoStageTiling:
         size: int,
         strategy: Optional[TopKStrategy] = None,
         tuning: Optional[TwoStageWarpConfig] = None,
+        kind: Optional[str] = None,
     ):
-        """Warp config, strategy and block_n for a launch of `size` rows (reference ``:243-276``)."""
+        """Warp config, strategy and block_n for a launch of `size` rows (reference ``:243-276``),
+        from the table of call kind `kind` where the buffers were made for it."""
 
         block_size = self.block_n
         k_strategy = strategy
         config = tuning
+        dispatch = self.kind_dispatch.get(kind, self.dispatch) if kind is not None else self.dispatch
 
-        if config is None and self.dispatch and (bucket := self.dispatch.batch.get(size=size)):
+        if config is None and dispatch and (bucket := dispatch.batch.get(size=size)):
 
             if strategy and strategy.key in bucket.mapping:
 

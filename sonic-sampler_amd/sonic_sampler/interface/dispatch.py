@@ -3,7 +3,12 @@
 A table maps a vocabulary bucket to batch buckets, each holding a priority-ordered list of
 launch configurations, in the reference's TOML schema. The tables shipped here are for gfx950
 (``resources/dispatch/gfx950_k128.toml``). ``arch`` may be given as ``950`` or ``"gfx950"``; when
-it is omitted the current device's architecture is used. The warp counts and top-k strategy of
+it is omitted the current device's architecture is used. Call kinds whose best tile widths differ
+from the fused single step's have tables of their own beside it (``gfx950_k128_multistep.toml``,
+``gfx950_k128_drafting.toml``, ``gfx950_k128_topk.toml``): the verification without penalties is
+bound by per-element instructions and prefers wider tiles than the decode step, which reads four
+planes per element. A kind without a table, or without a bucket for a vocabulary, uses the shared
+table. The warp counts and top-k strategy of
 each entry are kept for schema compatibility; the gfx950 kernels use one 256-thread workgroup
 shape and one selection algorithm, so only ``block_n`` changes what runs.
 """
@@ -219,10 +224,13 @@ class DispatchSummary:
                                              else path.read_text()))
 
     @classmethod
-    def load(cls, k: int = MAX_K, arch: Union[int, str, None] = None,
-             inference: bool = True) -> Optional["DispatchSummary"]:
+    def load(cls, k: int = MAX_K, arch: Union[int, str, None] = None, inference: bool = True,
+             kind: Optional[str] = None) -> Optional["DispatchSummary"]:
+        """The shipped table ``{arch}_k{k}.toml``, or with `kind` the table of that call kind
+        (``{arch}_k{k}_{kind}.toml``), None where there is no such file."""
 
-        path = resources.files("sonic_sampler") / "resources/dispatch" / f"{resolve_arch(arch)}_k{k}.toml"
+        name = f"{resolve_arch(arch)}_k{k}" + (f"_{kind}" if kind else "")
+        path = resources.files("sonic_sampler") / "resources/dispatch" / f"{name}.toml"
 
         if path.is_file():
 

@@ -58,6 +58,7 @@ class UnshardedFusedMultistep(TwoStageTiling):
             ensure_multiblock=True,
             unpacked_buffers=True,
             device=device,
+            kinds=("multistep",),
         )
 
         return cls(

@@ -68,6 +68,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             ensure_multiblock=True,
             unpacked_buffers=False,
             device=device,
+            kinds=(None, "drafting"),
         )
 
         return cls(
@@ -78,6 +79,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             vocabulary=factory.vocabulary,
             scratchpad=factory.scratchpad,
             dispatch=factory.dispatch,
+            kind_dispatch=factory.kind_dispatch,
         )
 
     def autoregressive(
@@ -164,7 +166,7 @@ class UnshardedFusedSingular(TwoStageTiling):
 
         penalties = buffers.repetition
         counts = penalties.counts
-        config, k_strategy, block_n = self.tuning(logits.size(0), strategy, tuning)
+        config, k_strategy, block_n = self.tuning(logits.size(0), strategy, tuning, kind="drafting")
 
         output_tokens, drafted_tokens = resolve_tokens(tokens, timestep, in_place)
 

@@ -75,6 +75,7 @@ class UnshardedBoundedTopK(TwoStageTiling):
             unpacked_buffers=True,
             values_dtype=BF16,
             device=device,
+            kinds=("topk",),
         )
 
         instance = cls(

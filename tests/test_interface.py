@@ -137,12 +137,41 @@ def test_dispatch_table_for_gfx950():
     assert table is not None
     # a vocabulary bucket's block_n is its smallest width (the scratchpad is sized for it); a
     # launch takes the width of the bucket of its row count
-    assert table.vocab.get(size=128256).block_n == 1024
+    assert table.vocab.get(size=128256).block_n == 2048
     assert table.vocab.get(size=32000).block_n == 1024
-    assert table.vocab.get(size=151936).block_n == 2048
     assert table.vocab.get(size=128256).batch.get(size=64).best.block_n == 4096     # config 1
-    assert table.vocab.get(size=32000).batch.get(size=256).best.block_n == 8192     # config 4
     assert table.vocab.get(size=128256).batch.get(size=2048).best.block_n == 8192
+
+
+def test_call_kind_tables_for_gfx950():
+    """The verification and the drafting step read tables of their own; a kind without a bucket
+    for the vocabulary (drafting is measured for draft vocabularies only) takes the shared one."""
+
+    multistep = DispatchSummary.load(k=MAX_K, arch="gfx950", kind="multistep")
+    drafting = DispatchSummary.load(k=MAX_K, arch="gfx950", kind="drafting")
+
+    assert DispatchSummary.load(k=MAX_K, arch="gfx950", kind="absent") is None
+    assert multistep.vocab.get(size=128256).batch.get(size=294).best.block_n == 16384   # config 3
+    assert multistep.vocab.get(size=151936).batch.get(size=640).best.block_n == 16384   # config 2
+    assert drafting.vocab.get(size=32000).batch.get(size=256).best.block_n == 8192      # config 4
+    assert drafting.vocab.get(size=128256) is None
+    topk = DispatchSummary.load(k=MAX_K, arch="gfx950", kind="topk")
+    assert topk.vocab.get(size=32000).batch.get(size=8).best.block_n == 1024             # config 0
+
+    shared, _ = resolve_dispatch(MAX_K, 128256, None, "gfx950")
+    own, _ = resolve_dispatch(MAX_K, 128256, None, "gfx950", kind="multistep")
+    fallback, _ = resolve_dispatch(MAX_K, 128256, None, "gfx950", kind="drafting")
+    assert own.batch.get(size=294).best.block_n == 16384
+    assert fallback.batch.get(size=294).best.block_n == shared.batch.get(size=294).best.block_n == 8192
+
+    # buffers shared by the decode and drafting steps hold the lists of the smaller width of the two
+    tiling, _, _ = TwoStageTiling.factory(vocab_size=32000, batch_size=256, arch="gfx950", device="cpu",
+                                          kinds=(None, "drafting"))
+    assert tiling.block_n == min(tiling.dispatch.block_n, tiling.kind_dispatch["drafting"].block_n) == 1024
+    assert tiling.scratchpad.shape == (256, 32 * MAX_K)
+    assert tiling.tuning(256)[2] == 4096
+    assert tiling.tuning(256, kind="drafting")[2] == 8192
+    assert tiling.tuning(256, kind="topk")[2] == 4096   # no table of that kind was resolved
 
 
 @pytest.mark.parametrize("k, block, message", [
@@ -162,10 +191,10 @@ def test_tiling_buffers():
     tiling, values, indices = TwoStageTiling.factory(vocab_size=128256, batch_size=8, lookahead=3,
                                                      arch="gfx950", device="cpu")
 
-    # sized for the bucket's smallest width (1024: 126 tiles); 32 rows launch at 4096
-    assert tiling.block_n == 1024
-    assert tiling.vocabulary.blocks == 126
-    assert tiling.scratchpad.shape == (8 * 4, 126 * MAX_K)
+    # sized for the bucket's smallest width (2048: 63 tiles); 32 rows launch at 4096
+    assert tiling.block_n == 2048
+    assert tiling.vocabulary.blocks == 63
+    assert tiling.scratchpad.shape == (8 * 4, 63 * MAX_K)
     assert tiling.tuning(32)[2] == 4096
     assert tiling.scratchpad.dtype == torch.uint32
     assert values.shape == indices.shape == (32, MAX_K)
@@ -274,3 +303,38 @@ def test_autotune_ranks_widths_and_round_trips(tmp_path):
     mixed = autotune([32768], [8], widths=split["singular"], measure=lambda kind, v, b, w: split[kind][w],
                      kinds=split)
     assert mixed.vocab.get(32768).batch.get(8).best.block_n == 4096
+
+
+def test_autotune_writes_a_table_per_kind_from_a_log(tmp_path):
+    """`--from-log` scores an earlier run's times again: one table per kind, the shared one for
+    the decode step, buckets where a kind has no call left out."""
+
+    from sonic_sampler.interface.autotune import main, parse_log, table_path
+    from sonic_sampler.interface.dispatch import DispatchSummary
+
+    log = tmp_path / "autotune.log"
+    log.write_text("\n".join([
+        "noise from the runtime",
+        "vocab 32768 batch 1: 2048 | singular 1024:10.00 2048:10.10 4096:11.00 8192:12.00",
+        "vocab 32768 batch 8: 8192 | singular 1024:10.00 2048:11.00 4096:10.50 8192:13.00 | "
+        "multistep 1024:20.00 2048:12.00 4096:10.00 8192:10.10",
+    ]) + "\n")
+
+    times = parse_log(log.read_text().splitlines())
+    assert times[("multistep", 32768, 8, 8192)] == 10.1
+    assert ("multistep", 32768, 1, 1024) not in times
+
+    out = str(tmp_path / "gfx950_k128.toml")
+    assert table_path(out, "singular") == out
+    assert table_path(out, "multistep") == str(tmp_path / "gfx950_k128_multistep.toml")
+
+    assert main(["--out", out, "--vocab", "32768", "--batch", "1,8", "--widths", "1024,2048,4096,8192",
+                 "--kinds", "singular,multistep", "--from-log", str(log)]) == 0
+    shared = DispatchSummary.read(out)
+    multistep = DispatchSummary.read(table_path(out, "multistep"))
+
+    assert [b.size for b in shared.vocab.get(32768).batch] == [1, 8]
+    assert shared.vocab.get(32768).batch.get(1).best.block_n == 2048
+    assert shared.vocab.get(32768).batch.get(8).best.block_n == 1024
+    assert [b.size for b in multistep.vocab.get(32768).batch] == [8]     # no one-row verification
+    assert multistep.vocab.get(32768).batch.get(8).best.block_n == 8192

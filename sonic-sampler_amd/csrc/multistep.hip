@@ -181,11 +181,6 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     const uint16_t *qrow = svgd ? nullptr
                                 : a.draft_probabilities + (int64_t)slot * a.probs_stride_slot +
                                       (int64_t)step * a.probs_stride_step;
-    if (wave == 0) {
-        sm.tok[e0] = i0;
-        sm.tok[e0 + 1] = i1;
-    }
-    __syncthreads();
     if (wave == 1 || wave == 2) {
         const int e = (wave - 1) * 64 + lane;
         const int t = sm.tok[e];

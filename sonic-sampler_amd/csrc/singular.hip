@@ -115,8 +115,9 @@ __device__ __forceinline__ void singular_greedy(const ss_singular_args &a, const
 }
 
 // Selection of a non-greedy row from its sorted top-128 (wave 0 holds element e = 2 * lane + i
-// as (v_i, idx_i)): truncation, d2t remap, Gumbel-max over bf16(v - w), count update, logprobs,
-// top-Z logprobs and the probability scatter. All threads call.
+// as (v_i, idx_i), sm.tok[e] = idx_e as merge_row leaves them): truncation, d2t remap, Gumbel-max
+// over bf16(v - w), count update, logprobs, top-Z logprobs and the probability scatter. All
+// threads call.
 __device__ __forceinline__ void singular_select(const ss_singular_args &a, SampleSmem &sm, int row,
                                                 int slot, uint32_t prm, float v0, float v1, int i0,
                                                 int i1) {
@@ -126,11 +127,6 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
     const int wave = (int)threadIdx.x >> 6;
     const int lane = lane_id();
     const int e0 = 2 * lane, e1 = e0 + 1;
-    if (wave == 0) {
-        sm.tok[e0] = i0;
-        sm.tok[e1] = i1;
-    }
-    __syncthreads();
     if (wave == 1 || wave == 2) {
         const int e = (wave - 1) * 64 + lane;
         int t = sm.tok[e];
@@ -148,7 +144,7 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
     i0 = sm.tok[e0];
     i1 = sm.tok[e1];
     const float w0 = sm.noise[e0], w1 = sm.noise[e1];
-    const int sel = wave_argmax_first(rbf(v0 - w0), rbf(v1 - w1));
+    const int sel = wave_argmax_first_bf16(rbf(v0 - w0), rbf(v1 - w1));
     const int token = lane_i32((sel & 1) ? i1 : i0, sel >> 1);
 
     if (lane == 0 && a.update_counts && a.decode_counts) {

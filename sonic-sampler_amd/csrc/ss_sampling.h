@@ -1296,7 +1296,8 @@ __device__ __forceinline__ void merge_refill(const uint32_t *scr, const RowSampl
 
 // Row merge over the tiles' sorted candidate lists, from the samples of load_samples. All threads
 // call; on return wave 0 holds the row's top-128 sorted by (value desc, column asc), element
-// e = 2 * lane + i as (v_i, idx_i).
+// e = 2 * lane + i as (v_i, idx_i), and sm.tok[e] holds idx_e, visible to every wave (the return
+// follows a barrier).
 //
 // Only the first kp = min(128, 512 / tiles) entries of every list are merged: 512 sample slots,
 // slot s = list * kp + position, as composites (key << 16) | (0xffff - s), whose order is the
@@ -1369,22 +1370,31 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
                 beats += __popcll(__ballot(nx != 0u && (kn > klast || (kn == klast && t < llast))));
             }
         }
-        if (lane == 0) sm.flag = beats > SS_REFILL_LISTS || (beats > 0 && kp == 0) ? 1 : 0;
-    }
-    if (beats > 0 && beats <= SS_REFILL_LISTS && kp > 0) {
-        // wave 0 only (beats is 0 in the other waves)
-        merge_refill(scr, smp, tiles, lm, V, f0, f1, v0, v1, i0, i1);
+        // exact (refilled when few lists are short), or the radix merge by every wave after the
+        // barrier; one barrier publishes both the decision and the exact result's columns
+        const bool radix = beats > SS_REFILL_LISTS || (beats > 0 && kp == 0);
+        if (lane == 0) sm.flag = radix ? 1 : 0;
+        if (!radix) {
+            if (beats > 0) {
+                merge_refill(scr, smp, tiles, lm, V, f0, f1, v0, v1, i0, i1);
+            } else {
+                v0 = bf2f(unkey16(f0 >> 16));
+                v1 = bf2f(unkey16(f1 >> 16));
+                i0 = f0 ? sm.col[0xffffu - (f0 & 0xffffu)] : V - 1;
+                i1 = f1 ? sm.col[0xffffu - (f1 & 0xffffu)] : V - 1;
+            }
+            sm.tok[2 * lane] = i0;
+            sm.tok[2 * lane + 1] = i1;
+        }
     }
     __syncthreads();
     if (sm.flag) {
         merge_row_radix(sm, scr, tiles, lm, V, v0, v1, i0, i1);
-        return;
-    }
-    if (wave == 0 && beats == 0) {
-        v0 = bf2f(unkey16(f0 >> 16));
-        v1 = bf2f(unkey16(f1 >> 16));
-        i0 = f0 ? sm.col[0xffffu - (f0 & 0xffffu)] : V - 1;
-        i1 = f1 ? sm.col[0xffffu - (f1 & 0xffffu)] : V - 1;
+        if (wave == 0) {
+            sm.tok[2 * lane] = i0;
+            sm.tok[2 * lane + 1] = i1;
+        }
+        __syncthreads();
     }
 }
 
@@ -1429,6 +1439,16 @@ __device__ __forceinline__ void truncate(uint32_t ind, int32_t topk, float topp,
         if (s0 < lower) v0 = -INFINITY;
         if (s1 < lower) v1 = -INFINITY;
     }
+}
+
+// wave_argmax_first for bfloat16 values z (the low 16 bits of each float are zero): distinct
+// values differ in the upper half of their order keys, so that half and the position make one
+// 32-bit word and the reduction runs on single words.
+__device__ __forceinline__ int wave_argmax_first_bf16(float z0, float z1) {
+    const int e0 = 2 * lane_id();
+    const uint32_t a = (key32(__float_as_uint(z0)) & 0xffff0000u) | (uint32_t)(127 - e0);
+    const uint32_t b = (key32(__float_as_uint(z1)) & 0xffff0000u) | (uint32_t)(126 - e0);
+    return 127 - (int)(wave_max_u32(a > b ? a : b) & 0xffffu);
 }
 
 // First element (lowest sorted position) holding the maximum of z over the wave's 128 elements.

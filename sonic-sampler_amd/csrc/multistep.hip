@@ -194,12 +194,12 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
     if (wave == 0) {
         const bool in_vocab = d >= 0 && d < a.vocab_size;
         const uint16_t qd16 = qrow && !last ? qrow[in_vocab ? d : 0] : (uint16_t)0;
+        SoftmaxParts sp;
         truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
-                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
-        float m, x0, x1;
-        const float logs = logf(exp_parts(v0, v1, m, x0, x1));
-        l0 = (v0 - m) - logs;  // log_softmax in fp32, as the reference's softmax()
-        l1 = (v1 - m) - logs;
+                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1, sp);
+        const float logs = logf(softmax_sum(sp, v0, v1));
+        l0 = (v0 - sp.m) - logs;  // log_softmax in fp32, as the reference's softmax()
+        l1 = (v1 - sp.m) - logs;
         vrow[e0] = l0;
         vrow[e0 + 1] = l1;
         irow[e0] = i0;

@@ -123,7 +123,7 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
                                                 int i1) {
     const uint32_t ind = lane_u32(prm, RP_IND);
     // Waves 1 and 2 remap the 128 candidates' columns and draw their noise (one candidate per
-    // lane) while wave 0 applies the truncation.
+    // lane) while wave 0 applies the truncation and the log-softmax.
     const int wave = (int)threadIdx.x >> 6;
     const int lane = lane_id();
     const int e0 = 2 * lane, e1 = e0 + 1;
@@ -136,9 +136,29 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
                           : bf2f(a.gumbel[(int64_t)slot * a.stride_gumbel + t]);
         sm.tok[e] = t;
     }
-    if (wave == 0)
+    // wave 0: the truncation, then the log-softmax of the truncated values (independent of the
+    // noise, so it runs before the barrier, while waves 1 and 2 draw the noise)
+    const bool want_lp = a.return_logprobs && a.logprobs;
+    const bool want_probs = a.return_probabilities && a.probabilities;
+    float o0 = 0.0f, o1 = 0.0f;  // the logprob of each element as the reference computes it
+    if (wave == 0) {
+        SoftmaxParts sp;
         truncate(ind, (int32_t)lane_u32(prm, RP_TOPK), __uint_as_float(lane_u32(prm, RP_TOPP)),
-                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1);
+                 __uint_as_float(lane_u32(prm, RP_MINP)), v0, v1, sp);
+        if (want_lp || want_probs) {
+            const float logs = logf(softmax_sum(sp, v0, v1));
+            if (want_probs) {
+                // log_softmax in fp32: (v - max) - log(sum)
+                o0 = (v0 - sp.m) - logs;
+                o1 = (v1 - sp.m) - logs;
+            } else {
+                // v - logsumexp(v), logsumexp = max + log(sum(exp(v - max)))
+                const float lse = sp.m + logs;
+                o0 = v0 - lse;
+                o1 = v1 - lse;
+            }
+        }
+    }
     __syncthreads();
     if (wave != 0) return;
     i0 = sm.tok[e0];
@@ -151,42 +171,25 @@ __device__ __forceinline__ void singular_select(const ss_singular_args &a, Sampl
         int32_t *d = a.decode_counts + (int64_t)slot * a.stride_decode + token;
         if (a.is_prefill) atomicExch(d, 1); else atomicAdd(d, 1);
     }
-
-    const bool want_lp = a.return_logprobs && a.logprobs;
-    const bool want_probs = a.return_probabilities && a.probabilities;
-    if (want_lp || want_probs) {
-        float m, x0, x1;
-        const float s = exp_parts(v0, v1, m, x0, x1);
-        const float logs = logf(s);
-        float o0, o1;  // the logprob of each element as the reference computes it
-        if (want_probs) {
-            // log_softmax in fp32: (v - max) - log(sum)
-            o0 = (v0 - m) - logs;
-            o1 = (v1 - m) - logs;
-            uint16_t *p = a.probabilities + (int64_t)slot * a.stride_probabilities;
-            p[i0] = (uint16_t)f2bf(expf(o0));
-            p[i1] = (uint16_t)f2bf(expf(o1));
-        } else {
-            // v - logsumexp(v), logsumexp = max + log(sum(exp(v - max)))
-            const float lse = m + logs;
-            o0 = v0 - lse;
-            o1 = v1 - lse;
-        }
-        if (want_lp) {
-            const float osel = lane_f32((sel & 1) ? o1 : o0, sel >> 1);
-            if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
-            if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
-                const int top_lim = (int)lane_u32(prm, RP_TOPZ);
-                const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
-                const int64_t o = (int64_t)row * a.stride_top;
-                if (e0 < lim) {
-                    a.top_values[o + e0] = (uint16_t)f2bf(o0);
-                    a.top_tokens[o + e0] = i0;
-                }
-                if (e1 < lim) {
-                    a.top_values[o + e1] = (uint16_t)f2bf(o1);
-                    a.top_tokens[o + e1] = i1;
-                }
+    if (want_probs) {
+        uint16_t *p = a.probabilities + (int64_t)slot * a.stride_probabilities;
+        p[i0] = (uint16_t)f2bf(expf(o0));
+        p[i1] = (uint16_t)f2bf(expf(o1));
+    }
+    if (want_lp) {
+        const float osel = lane_f32((sel & 1) ? o1 : o0, sel >> 1);
+        if (lane == 0) a.logprobs[(int64_t)row * a.stride_logprobs] = (uint16_t)f2bf(osel);
+        if ((ind & IND_TOPLOGPROBS) && a.top_values && a.max_top_logprobs > 0) {
+            const int top_lim = (int)lane_u32(prm, RP_TOPZ);
+            const int lim = top_lim < a.max_top_logprobs ? top_lim : a.max_top_logprobs;
+            const int64_t o = (int64_t)row * a.stride_top;
+            if (e0 < lim) {
+                a.top_values[o + e0] = (uint16_t)f2bf(o0);
+                a.top_tokens[o + e0] = i0;
+            }
+            if (e1 < lim) {
+                a.top_values[o + e1] = (uint16_t)f2bf(o1);
+                a.top_tokens[o + e1] = i1;
             }
         }
     }

@@ -1398,46 +1398,65 @@ __device__ __forceinline__ void merge_row(SampleSmem &sm, const uint32_t *scr,
     }
 }
 
-// exp(v - m) for both elements of the lane and the wave-wide sum. m is element 0 (the maximum).
-__device__ __forceinline__ float exp_parts(float v0, float v1, float &m, float &x0, float &x1) {
-    m = lane_f32(v0, 0);
-    x0 = expf(v0 - m);
-    x1 = expf(v1 - m);
-    return wave_sum_f32(x0 + x1);
+// exp(v - m) of the lane's two elements of the sorted top-128 (wave 0), m = v[0] (the maximum),
+// kept across the truncation stages and the log-softmax that follows them. A stage that removes
+// an element (v = -inf) sets its part to exp(-inf - m), the value recomputing it would give, so
+// every later sum reads exactly the parts it would recompute; they are recomputed when v[0] is no
+// longer m (position 0 removed by an out-of-range parameter, or NaN).
+struct SoftmaxParts {
+    float m = 0.0f, x0 = 0.0f, x1 = 0.0f;
+    bool valid = false;
+};
+
+// Sum of exp(v - v[0]) over the wave's 128 elements, with `sp` holding m = v[0] and the parts.
+__device__ __forceinline__ float softmax_sum(SoftmaxParts &sp, float v0, float v1) {
+    const float m = lane_f32(v0, 0);
+    if (!sp.valid || !(m == sp.m)) {
+        sp.m = m;
+        sp.x0 = expf(v0 - m);
+        sp.x1 = expf(v1 - m);
+        sp.valid = true;
+    }
+    return wave_sum_f32(sp.x0 + sp.x1);
+}
+
+// Removes the lane's elements whose flag is set: v = -inf, part exp(-inf - m).
+__device__ __forceinline__ void softmax_remove(SoftmaxParts &sp, bool r0, bool r1, float &v0, float &v1) {
+    if (r0) v0 = -INFINITY;
+    if (r1) v1 = -INFINITY;
+    if (sp.valid) {
+        const float z = expf(-INFINITY - sp.m);
+        if (r0) sp.x0 = z;
+        if (r1) sp.x1 = z;
+    }
 }
 
 // top-k -> top-p -> min-p on the sorted top-128 (wave 0), each on the values left by the
 // previous one, as in reference core/naive.py:270-328 (applied in that order by
-// `thread_first(values, self.top_k, self.top_p, self.min_p)`, core/naive.py:338).
+// `thread_first(values, self.top_k, self.top_p, self.min_p)`, core/naive.py:338). `sp` leaves
+// with the softmax parts of the last stage that took them.
 __device__ __forceinline__ void truncate(uint32_t ind, int32_t topk, float topp, float minp,
-                                         float &v0, float &v1) {
+                                         float &v0, float &v1, SoftmaxParts &sp) {
     const int e0 = 2 * lane_id(), e1 = e0 + 1;
-    if (ind & IND_TOPK) {
-        if (e0 >= topk) v0 = -INFINITY;
-        if (e1 >= topk) v1 = -INFINITY;
-    }
+    if (ind & IND_TOPK) softmax_remove(sp, e0 >= topk, e1 >= topk, v0, v1);
     if (ind & IND_TOPP) {
         // softmax in fp32 (x * (1 / sum)), cumulative sum accumulated in fp64 and compared in
         // fp32 against p; position 0 is always kept.
-        float m, x0, x1;
-        const float s = exp_parts(v0, v1, m, x0, x1);
+        const float s = softmax_sum(sp, v0, v1);
         const float inv = 1.0f / s;
-        const float p0 = x0 * inv, p1 = x1 * inv;
+        const float p0 = sp.x0 * inv, p1 = sp.x1 * inv;
         const double inc = wave_inclusive_sum_f64((double)p0 + (double)p1);
         const double exc = shift_up1_f64(inc);  // 0 in lane 0
         const double c0 = exc + (double)p0, c1 = c0 + (double)p1;
-        if (e0 > 0 && (float)c0 > topp) v0 = -INFINITY;
-        if ((float)c1 > topp) v1 = -INFINITY;
+        softmax_remove(sp, e0 > 0 && (float)c0 > topp, (float)c1 > topp, v0, v1);
     }
     if (ind & IND_MINP) {
         // bf16 softmax, masked where the rounded probability is below bf16(min_p * p_max).
-        float m, x0, x1;
-        const float s = exp_parts(v0, v1, m, x0, x1);
+        const float s = softmax_sum(sp, v0, v1);
         const float inv = 1.0f / s;
-        const float s0 = rbf(x0 * inv), s1 = rbf(x1 * inv);
+        const float s0 = rbf(sp.x0 * inv), s1 = rbf(sp.x1 * inv);
         const float lower = rbf(minp * lane_f32(s0, 0));
-        if (s0 < lower) v0 = -INFINITY;
-        if (s1 < lower) v1 = -INFINITY;
+        softmax_remove(sp, s0 < lower, s1 < lower, v0, v1);
     }
 }
 

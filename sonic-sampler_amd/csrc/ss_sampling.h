@@ -755,6 +755,29 @@ enum { MODE_DIRECT = 0, MODE_GATHER_VEC = 1, MODE_SCALAR = 2 };
 
 // Streams one tile of one row through the processor chain and returns the keys (0 = absent).
 // `lw` holds the tile's logits from load_logits_vec unless MODE is MODE_SCALAR.
+// Gather pass H of a tile (elements j + 16 H, 4 H chunks of 1024 columns further) and the passes
+// after it. H is a template parameter so that the keys each pass writes keep constant indices: a
+// loop over the passes that the compiler leaves rolled (at E = 64 the body is too large to unroll)
+// would index the key array at run time and place it in scratch memory.
+template <int E, int MODE, int H>
+__device__ __forceinline__ void gather_pass(const RowState &rs, const Uses &u, int col0, int V,
+                                            const int32_t *hist, const u32x2 (&lw)[E / 4], Keys<E> &keys) {
+    if constexpr (H < E / 16) {
+        u32x2 lh[4];
+        if constexpr (MODE != MODE_SCALAR && E >= 64) {
+            load_logits_vec<16>(rs.logits, col0 + 4 * 4 * SS_BLOCK * H, V, lh);
+        } else if constexpr (MODE != MODE_SCALAR) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) lh[c] = lw[4 * H + c];
+        }
+        Keys<16> kh;
+        gather_keys<16, MODE == MODE_GATHER_VEC>(rs, u, col0 + 4 * 4 * SS_BLOCK * H, V, hist, lh, kh);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) keys.p[8 * H + i] = kh.p[i];
+        gather_pass<E, MODE, H + 1>(rs, u, col0, V, hist, lw, keys);
+    }
+}
+
 template <int E, int MODE>
 __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
                                               const int32_t *hist, const u32x2 (&lw)[E / 4],
@@ -795,19 +818,23 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
     } else if constexpr ((E >= 32 && MODE == MODE_GATHER_VEC) || E >= 64) {
         // 4096-column passes, as above: the gathered columns and planes of all 32 elements at
         // once would hold 156 VGPRs (three waves per SIMD).
+        if constexpr (E >= 64) {
+            gather_pass<E, MODE, 0>(rs, u, col0, V, hist, lw, keys);
+        } else {
+            // two passes, which the compiler unrolls (and schedules in fewer registers than the
+            // recursive form: 96 VGPRs against 102 at E = 32)
 #pragma unroll
-        for (int h = 0; h < E / 16; ++h) {
-            u32x2 lh[4];
-            if constexpr (MODE != MODE_SCALAR && E >= 64) {
-                load_logits_vec<16>(rs.logits, col0 + 4 * 4 * SS_BLOCK * h, V, lh);
-            } else if constexpr (MODE != MODE_SCALAR) {
+            for (int h = 0; h < E / 16; ++h) {
+                u32x2 lh[4];
+                if constexpr (MODE != MODE_SCALAR) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) lh[c] = lw[4 * h + c];
+                    for (int c = 0; c < 4; ++c) lh[c] = lw[4 * h + c];
+                }
+                Keys<16> kh;
+                gather_keys<16, MODE == MODE_GATHER_VEC>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
             }
-            Keys<16> kh;
-            gather_keys<16, MODE == MODE_GATHER_VEC>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
         }
     } else {
         gather_keys<E, MODE == MODE_GATHER_VEC>(rs, u, col0, V, hist, lw, keys);

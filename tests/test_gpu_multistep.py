@@ -151,3 +151,64 @@ def test_merge_paths_at_128_tiles():
         for i, idx in enumerate(e.row_indices):
 
             assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i)
+
+
+@pytest.mark.parametrize("block", [4096, 16384])
+def test_temperature_rows_at_the_cut(block):
+    """Temperature-only rows whose scaled keys tie where the tile stage cuts its top-128:
+    temperatures with inexact reciprocals (neighbouring logits share a scaled key, so the cut goes
+    by column), tiny logits under a large temperature (scaled keys collide in long runs), rows of
+    equal logits and rows of a few distinct values (the exact cut). The last tile is partial. The
+    per-row top-128 ids must match the oracle exactly."""
+
+    from bench import MultistepWorkload, spiked_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, ScopedIndicators
+
+    batch, gamma, vocab = 6, 3, 65432
+    n = gamma + 1
+    rows = batch * n
+    g = torch.Generator().manual_seed(71)
+    bf = lambda v: float(torch.tensor(v).to(torch.bfloat16))  # noqa: E731
+    temperature = [bf(t) for t in (3.0, 1.7, 50.0, 0.3, 7.0, 1.3)]
+    scoped = ScopedIndicators.from_params(
+        size=batch, timesteps=n, multiplicative=[1.0] * batch, frequency=[0.0] * batch,
+        presence=[0.0] * batch, biases=[{} for _ in range(batch)], temperature=temperature,
+        top_k=[128] * batch, top_p=[1.0] * batch, min_p=[0.0] * batch, top_logprobs=[4] * batch,
+    )
+    host = SamplingBuffers.default(size=batch, timesteps=n, vocab_size=vocab, device="cpu", noise=False)
+    host.flags = Flags.from_scoped(scoped, device="cpu")
+    host.weights.gumbel.target.exponential_(1.0, generator=g).log_()
+    host.temperature.copy_(torch.tensor(temperature).to(torch.bfloat16))
+    logits = spiked_logits(rows, vocab, seed=72).float()
+
+    for r in range(rows):
+
+        kind = r % 4
+
+        if kind == 1:
+            logits[r] = torch.randn(vocab, generator=g) * 1e-37
+        elif kind == 2:
+            logits[r] = 0.75
+        elif kind == 3:
+            logits[r] = torch.randint(-3, 4, (vocab,), generator=g).float() * 0.3
+
+    logits = logits.to(torch.bfloat16)
+    drafted = torch.randint(1, vocab, (rows,), generator=g, dtype=torch.int32)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, rows + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=None)
+    print(f"temperature rows at the cut: block={block}", flush=True)
+    verification, _, verifier = run_verifier(work, block_size=block)
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, logprobs=True, max_top_logprobs=4)
+    check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
+
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i, temperature[b])

@@ -1,5 +1,6 @@
 // Bounded top-k over [rows, vocab] logits (replaces K2 ops/topk/bitpack.py:99-158 followed by K3
-// ops/topk/unpack.py:312-377 of the reference), as two back-to-back launches.
+// ops/topk/unpack.py:312-377 of the reference), as two back-to-back launches, or one launch of a
+// 1024-thread workgroup per row (topk_wide_kernel) for many rows of at most 32768 columns.
 //
 // Tile stage, grid rows * tiles: each workgroup turns block_n logits into order-preserving keys
 // and writes its exact top-k (ties to the lowest column) to the scratch row in column order.
@@ -287,9 +288,9 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
 // ---------------------------------------------------------------------------------------------
 // Block selection: one workgroup holds a block of SS_BLOCK * E columns (E values per thread,
 // element j of thread t at column (j / 4) * 1024 + 4 t + j % 4 of the block, loaded as 16-byte fp32
-// / 8-byte bf16 chunks) and selects its top-k. TILED: the block is tile blockIdx.x % tiles of row
+// / 8-byte bf16 chunks) and selects its top-k: the block is tile blockIdx.x % tiles of row
 // blockIdx.x / tiles and its top-k goes to the scratch row as packed candidates for the merge
-// kernel; otherwise the block is the whole row (one launch) and the top-k is the output.
+// kernel.
 //
 // Lower bound: every wave sorts its 64 lane maxima; at least need_w of its lanes hold a value >= the
 // need_w-th largest of them, with need_w the wave's share of k (k / 4 in a full block, in
@@ -300,8 +301,6 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
 // of bitonic merges keep the top-128 of the four runs, and the first k are written. A wave with more
 // than 128 survivors (long runs of equal values) sends the row to the exact radix selection.
 // ---------------------------------------------------------------------------------------------
-constexpr int TOPK_ROW_E = 128;  // whole rows of at most SS_BLOCK * 128 = 32768 columns
-
 struct TopkRowSmem {
     SelectSmem sel;                 // exact fallback
     uint64_t runs[SS_WAVES][SS_K];  // each wave's survivors, then its sorted run
@@ -315,13 +314,13 @@ __device__ __forceinline__ uint32_t float_key(float v) {
     return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 
-template <bool F32, bool VEC, int E, bool TILED>
+template <bool F32, bool VEC, int E>
 __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, int tiles) {
     __shared__ TopkRowSmem sm;
-    const int row = TILED ? (int)blockIdx.x / tiles : (int)blockIdx.x;
-    const int tile = TILED ? (int)blockIdx.x - row * tiles : 0;
+    const int row = (int)blockIdx.x / tiles;
+    const int tile = (int)blockIdx.x - row * tiles;
     const int col0 = tile * a.block_n;  // first column of the block
-    const int V = TILED ? min(a.block_n, a.vocab_size - col0) : a.vocab_size;  // columns of the block
+    const int V = min(a.block_n, a.vocab_size - col0);  // columns of the block
     const int k = a.k;
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -329,21 +328,13 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
     const int64_t bytes = (int64_t)V * (F32 ? 4 : 2);
     const char *base = (const char *)a.logits + ((int64_t)row * a.stride_logits + col0) * (F32 ? 4 : 2);
     const __amdgpu_buffer_rsrc_t rb = row_buffer(base, bytes);
-    // the block's top-k: packed candidates of the merge kernel (tiled) or the row's output
+    // the block's top-k: packed candidates of the merge kernel
     auto emit = [&](int e, uint32_t key, int col) {
-        if (TILED) {
-            using Tr = TopkTraits<F32>;
-            typename Tr::Cand *scr = (typename Tr::Cand *)a.scratch + (int64_t)row * a.stride_scratch;
-            // absent elements (key 0) keep key 0 in the 16-bit packing too
-            const uint32_t pk = F32 ? key : key ? key16(__float_as_uint(__uint_as_float(unkey32(key))) >> 16) : 0u;
-            scr[tile * k + e] = Tr::pack(pk, col);
-        } else {
-            const float val = __uint_as_float(unkey32(key));
-            const int64_t o = (int64_t)row * k + e;
-            if (F32) ((float *)a.values)[o] = val;
-            else ((uint16_t *)a.values)[o] = (uint16_t)(__float_as_uint(val) >> 16);
-            a.indices[o] = col < V ? col : V - 1;
-        }
+        using Tr = TopkTraits<F32>;
+        typename Tr::Cand *scr = (typename Tr::Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+        // absent elements (key 0) keep key 0 in the 16-bit packing too
+        const uint32_t pk = F32 ? key : key ? key16(__float_as_uint(__uint_as_float(unkey32(key))) >> 16) : 0u;
+        scr[tile * k + e] = Tr::pack(pk, col);
     };
 
     // ---- the row, every load issued before any is used; columns past V read -inf -----------------
@@ -465,7 +456,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
         return;
     }
 
-    // ---- exact selection over the whole row (ties at the k-th value kept in column order) ---------
+    // ---- exact selection over the whole block (ties at the k-th value kept in column order) -------
     auto keys_of = [&](int, uint32_t(&out)[E]) {
 #pragma unroll
         for (int j = 0; j < E; ++j) out[j] = col_of(j) < V ? float_key(v[j]) : 0u;
@@ -490,6 +481,236 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, in
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Whole rows of at most 32768 columns in one workgroup of 1024 threads: one launch and no scratch
+// round trip. 32 values per thread, element j of thread t at column (j / 4) * 4096 + 4 t + j % 4,
+// loaded as 16-byte fp32 / 8-byte bf16 chunks. The lower bound of topk_block_kernel over 16 waves
+// (each wave's share of k from its sorted lane maxima, the smallest of the 16 bounds), the
+// survivors of every wave gathered into one list and sorted by wave 0 (waves 0 and 1 for more than
+// 128). Rows whose survivors overflow the list (long runs of equal values) take an exact selection
+// over the registers: the k-th largest key by bisection on workgroup counts, the ties at it kept
+// in column order by workgroup scans, chunk by chunk.
+// ---------------------------------------------------------------------------------------------
+constexpr int TOPK_WIDE_THREADS = 1024;
+constexpr int TOPK_WIDE_WAVES = TOPK_WIDE_THREADS / 64;
+constexpr int TOPK_WIDE_E = 32;                          // 32768 columns
+constexpr int TOPK_WIDE_CHUNK = 4 * TOPK_WIDE_THREADS;   // columns of one 4-element chunk
+constexpr int TOPK_WIDE_LIST = 2 * SS_K;
+
+struct TopkWideSmem {
+    uint64_t runs[TOPK_WIDE_WAVES][SS_K];  // each wave's survivors
+    uint64_t list[TOPK_WIDE_LIST];         // the row's survivors, or its exact selection
+    uint32_t red[TOPK_WIDE_WAVES];
+};
+
+// Workgroup sum of one count per thread (all threads call).
+__device__ __forceinline__ uint32_t wide_sum(uint32_t n, uint32_t *red) {
+    n = wave_sum(n);
+    if (lane_id() == 0) red[threadIdx.x >> 6] = n;
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WIDE_WAVES; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// Exclusive scan of one count per thread in thread order, and the total (all threads call).
+__device__ __forceinline__ uint32_t wide_exclusive_scan(uint32_t n, uint32_t *red, uint32_t &total) {
+    const int wave = (int)threadIdx.x >> 6;
+    const uint32_t inc = wave_inclusive_sum(n);
+    if (lane_id() == 63) red[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, t = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WIDE_WAVES; ++w) {
+        const uint32_t r = red[w];
+        before += w < wave ? r : 0u;
+        t += r;
+    }
+    __syncthreads();
+    total = t;
+    return before + inc - n;
+}
+
+template <bool F32, bool VEC>
+__global__ __launch_bounds__(TOPK_WIDE_THREADS) void topk_wide_kernel(ss_topk_args a) {
+    __shared__ TopkWideSmem sm;
+    constexpr int E = TOPK_WIDE_E;
+    const int row = (int)blockIdx.x;
+    const int V = a.vocab_size;
+    const int k = a.k;
+    const int lane = lane_id();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane4 = 4 * (int)threadIdx.x;
+    const char *base = (const char *)a.logits + (int64_t)row * a.stride_logits * (F32 ? 4 : 2);
+    const __amdgpu_buffer_rsrc_t rb = row_buffer(base, (int64_t)V * (F32 ? 4 : 2));
+    auto emit = [&](int e, uint64_t c) {
+        const float val = __uint_as_float(unkey32((uint32_t)(c >> 32)));
+        const int col = (int)(0xffffffffu - (uint32_t)c);
+        const int64_t o = (int64_t)row * k + e;
+        if (F32) ((float *)a.values)[o] = val;
+        else ((uint16_t *)a.values)[o] = (uint16_t)(__float_as_uint(val) >> 16);
+        a.indices[o] = col < V ? col : V - 1;
+    };
+
+    float v[E];
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        const int col = c * TOPK_WIDE_CHUNK + lane4;
+        uint32_t w[4];
+        if (VEC) {
+            if (F32) {
+                const i32x4 q = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, col * 4, 0, NT));
+                w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+            } else {
+                const u32x2 q = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rb, col * 2, 0, NT));
+                w[0] = q.x << 16; w[1] = q.x & 0xffff0000u; w[2] = q.y << 16; w[3] = q.y & 0xffff0000u;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w[i] = F32 ? __builtin_amdgcn_raw_buffer_load_b32(rb, (col + i) * 4, 0, NT)
+                           : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb, (col + i) * 2, 0, NT) << 16;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * c + i] = col + i < V ? __uint_as_float(w[i]) : -INFINITY;
+    }
+    auto col_of = [&](int j) { return (j >> 2) * TOPK_WIDE_CHUNK + lane4 + (j & 3); };
+    auto composite = [&](int j) {
+        return ((uint64_t)float_key(v[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)col_of(j));
+    };
+
+    // ---- lower bound: the wave's share of k from its sorted lane maxima -------------------------
+    float m = v[0];
+#pragma unroll
+    for (int j = 1; j < E; ++j) m = fmaxf(m, v[j]);
+    uint32_t mk = float_key(m);
+    wave_sort64_desc(mk);
+    int nw = 0;  // columns of the row this wave holds (256 of every chunk)
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) nw += min(max(V - (c * TOPK_WIDE_CHUNK + 256 * wave), 0), 256);
+    const int need = nw ? (k * nw + V - 1) / V : 0;
+    if (need == 0 && lane == 0) sm.red[wave] = 0xffffffffu;
+    if (need > 64 && lane == 0) sm.red[wave] = 0u;
+    if (need > 0 && need <= 64 && lane == need - 1) sm.red[wave] = mk;
+    __syncthreads();
+    uint32_t lo = 0xffffffffu;
+#pragma unroll
+    for (int w = 0; w < TOPK_WIDE_WAVES; ++w) lo = min(lo, sm.red[w]);
+    const bool no_bound = lo == 0u;
+    const float lo_f = __uint_as_float((lo & 0x80000000u) ? (lo & 0x7fffffffu) : ~lo);
+    __syncthreads();
+
+    // ---- survivors per wave, then one list -----------------------------------------------------
+    uint64_t *run = sm.runs[wave];
+    uint32_t cnt = 0;  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const bool p = v[j] >= lo_f;
+        const uint64_t msk = __ballot(p);
+        if (msk) {
+            const uint32_t pos = cnt + mbcnt64(msk);
+            if (p && pos < (uint32_t)SS_K) run[pos] = composite(j);
+            cnt += (uint32_t)__popcll(msk);
+        }
+    }
+    if (lane == 0) sm.red[wave] = cnt;
+    __syncthreads();
+    uint32_t off = 0, total = 0, most = 0;
+#pragma unroll
+    for (int w = 0; w < TOPK_WIDE_WAVES; ++w) {
+        const uint32_t c = sm.red[w];
+        off += w < wave ? c : 0u;
+        total += c;
+        most = max(most, c);
+    }
+    const bool overflow = most > (uint32_t)SS_K || total > (uint32_t)TOPK_WIDE_LIST || no_bound;
+    if (!overflow) {
+        for (uint32_t i = (uint32_t)lane; i < cnt; i += 64) sm.list[off + i] = run[i];
+        __syncthreads();
+        if (total <= 64) {
+            if (wave == 0) {
+                uint64_t c = lane < (int)total ? sm.list[lane] : 0ull;
+                wave_sort64_desc(c);
+                if (lane < k) emit(lane, c);
+            }
+            return;
+        }
+        // up to 256: waves 0 and 1 sort 128 each, wave 0 keeps the top-128 of the two runs
+        if (wave < 2) {
+            const int b0 = SS_K * wave;
+            uint64_t c0 = b0 + 2 * lane < (int)total ? sm.list[b0 + 2 * lane] : 0ull;
+            uint64_t c1 = b0 + 2 * lane + 1 < (int)total ? sm.list[b0 + 2 * lane + 1] : 0ull;
+            wave_sort128_desc(c0, c1);
+            sm.runs[wave][2 * lane] = c0;
+            sm.runs[wave][2 * lane + 1] = c1;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint64_t f0 = max_u64(sm.runs[0][2 * lane], sm.runs[1][127 - 2 * lane]);
+            uint64_t f1 = max_u64(sm.runs[0][2 * lane + 1], sm.runs[1][126 - 2 * lane]);
+            wave_bitonic128_desc<128>(f0, f1);
+            if (2 * lane < k) emit(2 * lane, f0);
+            if (2 * lane + 1 < k) emit(2 * lane + 1, f1);
+        }
+        return;
+    }
+
+    // ---- exact selection: the k-th largest key T, then every key > T and the first ties --------
+    uint32_t key[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) key[j] = col_of(j) < V ? float_key(v[j]) : 0u;
+    uint32_t T = 0;  // the largest t with at least k keys >= t
+#pragma unroll 1
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = T | (1u << b);
+        uint32_t n = 0;
+#pragma unroll
+        for (int j = 0; j < E; ++j) n += key[j] >= c ? 1u : 0u;
+        if (wide_sum(n, sm.red) >= (uint32_t)k) T = c;
+    }
+    uint32_t n_above = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) n_above += key[j] > T ? 1u : 0u;
+    const uint32_t margin = (uint32_t)k - wide_sum(n_above, sm.red);  // ties kept
+    uint32_t base_g = 0, base_q = 0;
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        uint32_t g = 0, q = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g += key[4 * c + i] > T ? 1u : 0u;
+            q += key[4 * c + i] == T ? 1u : 0u;
+        }
+        uint32_t tot;
+        const uint32_t ex = wide_exclusive_scan(g | (q << 16), sm.red, tot);
+        g = base_g + (ex & 0xffffu);
+        q = base_q + (ex >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * c + i;
+            if (key[j] > T) {
+                sm.list[g + (q < margin ? q : margin)] = composite(j);
+                ++g;
+            } else if (key[j] == T) {
+                if (q < margin) sm.list[g + q] = composite(j);
+                ++q;
+            }
+        }
+        base_g += tot & 0xffffu;
+        base_q += tot >> 16;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t c0 = 2 * lane < k ? sm.list[2 * lane] : 0ull;
+        uint64_t c1 = 2 * lane + 1 < k ? sm.list[2 * lane + 1] : 0ull;
+        wave_sort128_desc(c0, c1);
+        if (2 * lane < k) emit(2 * lane, c0);
+        if (2 * lane + 1 < k) emit(2 * lane + 1, c1);
+    }
+}
+
 template <bool F32>
 static bool topk_vec(const ss_topk_args *a) {
     const int esz = F32 ? 4 : 2;
@@ -498,21 +719,21 @@ static bool topk_vec(const ss_topk_args *a) {
 
 template <bool F32>
 static int launch_topk_rows(const ss_topk_args *a) {
-    dim3 grid((unsigned)a->rows), block(SS_BLOCK);
+    dim3 grid((unsigned)a->rows), block(TOPK_WIDE_THREADS);
     hipStream_t s = (hipStream_t)a->stream;
-    if (topk_vec<F32>(a)) hipLaunchKernelGGL((topk_block_kernel<F32, true, TOPK_ROW_E, false>), grid, block, 0, s, *a, 1);
-    else hipLaunchKernelGGL((topk_block_kernel<F32, false, TOPK_ROW_E, false>), grid, block, 0, s, *a, 1);
+    if (topk_vec<F32>(a)) hipLaunchKernelGGL((topk_wide_kernel<F32, true>), grid, block, 0, s, *a);
+    else hipLaunchKernelGGL((topk_wide_kernel<F32, false>), grid, block, 0, s, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
 template <bool F32, bool VEC>
 static int launch_topk_tiles(const ss_topk_args *a, int tiles, dim3 grid, dim3 block, hipStream_t s) {
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 4, true>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8, true>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16, true>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32, true>), grid, block, 0, s, *a, tiles); break;
-        case 16384: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 64, true>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 4>), grid, block, 0, s, *a, tiles); break;
+        case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8>), grid, block, 0, s, *a, tiles); break;
+        case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16>), grid, block, 0, s, *a, tiles); break;
+        case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32>), grid, block, 0, s, *a, tiles); break;
+        case 16384: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 64>), grid, block, 0, s, *a, tiles); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     return SS_OK;
@@ -547,11 +768,18 @@ extern "C" int ss_topk(const ss_topk_args *a) {
     if (a->stride_logits < a->vocab_size) return SS_ERR_INVALID_ARGUMENT;
     if (a->rows == 0) return SS_OK;
     if (a->strategy < SS_STRATEGY_AUTO || a->strategy > SS_STRATEGY_ROWWISE) return SS_ERR_INVALID_ARGUMENT;
-    // One workgroup per row (one launch) serves rows of at most 32768 columns on request; AUTO
-    // takes the tile grid: one CU keeps too few cache lines in flight to stream a long row quickly
-    // (config 0, 8 rows of 128 KB: 12.7 us in one launch).
-    if (a->strategy == SS_STRATEGY_ROWWISE && a->vocab_size > SS_BLOCK * ss::TOPK_ROW_E) return SS_ERR_UNSUPPORTED;
-    if (a->strategy == SS_STRATEGY_ROWWISE)
+    // One 1024-thread workgroup per row (one launch) serves rows of at most 32768 columns on
+    // request. AUTO takes it where it measured faster than the tile grid at every width: at least
+    // 128 rows of more than 16384 columns and k <= 32 (256 rows of 32000 fp32 columns at k = 32:
+    // 12.1 us against 17.0; 1024 rows: 42.5 against 47.6). Fewer rows leave CUs idle while one CU
+    // streams each row (8 rows of 32000 fp32: 9.6 against 8.6 us), narrower rows leave most of a
+    // thread's 32 elements empty, and a larger k overflows the survivor list into the exact
+    // selection.
+    if (a->strategy == SS_STRATEGY_ROWWISE && a->vocab_size > ss::TOPK_WIDE_THREADS * ss::TOPK_WIDE_E) return SS_ERR_UNSUPPORTED;
+    const bool wide = a->strategy == SS_STRATEGY_ROWWISE ||
+                      (a->strategy == SS_STRATEGY_AUTO && a->rows >= 128 && a->k <= 32 && a->vocab_size > 16384 &&
+                       a->vocab_size <= ss::TOPK_WIDE_THREADS * ss::TOPK_WIDE_E);
+    if (wide)
         return a->dtype == SS_DTYPE_F32 ? ss::launch_topk_rows<true>(a) : ss::launch_topk_rows<false>(a);
     return a->dtype == SS_DTYPE_F32 ? ss::launch_topk<true>(a, tiles)
                                     : ss::launch_topk<false>(a, tiles);

@@ -107,8 +107,9 @@ def test_one_launch_rows_concentrated_values():
 @pytest.mark.parametrize("vocab,k,dtype", [(32000, 32, torch.float32), (30001, 128, torch.bfloat16),
                                            (8192, 8, torch.float32)])
 def test_one_workgroup_per_row_strategy(vocab, k, dtype):
-    """ss_topk with strategy ROWWISE (one launch, one workgroup per row), called through the
-    C-ABI: bit-exact against the oracle, including a heavily tied row that takes the exact path."""
+    """ss_topk with strategy ROWWISE (one launch, one 1024-thread workgroup per row), called
+    through the C-ABI: bit-exact against the oracle, including rows whose survivors need two sorting
+    waves, overflow the survivor list, or tie heavily (the exact selection)."""
 
     import ctypes
 
@@ -116,8 +117,14 @@ def test_one_workgroup_per_row_strategy(vocab, k, dtype):
     from sonic_sampler import _native
 
     rows = 8
+    g = torch.Generator().manual_seed(1)
     logits = spiked_logits(rows, vocab, seed=vocab, dtype=dtype)
-    logits[1] = torch.randint(-3, 4, (vocab,), generator=torch.Generator().manual_seed(1)).to(dtype)
+    logits[1] = torch.randint(-3, 4, (vocab,), generator=g).to(dtype)
+    # 200 and 600 raised values spread over every wave's columns: more survivors than one sorted
+    # wave holds (two waves sort them), and more than the survivor list holds (exact selection)
+    for r, n in ((2, 200), (3, 600)):
+        cols = torch.randperm(vocab, generator=g)[:n]
+        logits[r, cols] = (30.0 + 10.0 * torch.rand(n, generator=g)).to(dtype)
     x = logits.to(DEV)
     values = torch.empty(rows, k, dtype=dtype, device=DEV)
     indices = torch.empty(rows, k, dtype=torch.int32, device=DEV)
@@ -167,3 +174,23 @@ def test_merge_paths_at_128_tiles(k, dtype):
 
     print(f"top-k merge paths at 128 tiles: k={k} {dtype}", flush=True)
     check(logits.to(dtype), k, block)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_many_narrow_rows_take_one_launch(dtype):
+    """160 rows of 32000 columns at k = 32 through the interface: the library's automatic choice
+    is one 1024-thread workgroup per row; bit-exact against the oracle, with tied and crowded rows
+    among them."""
+
+    from bench import spiked_logits
+
+    rows, vocab, k = 160, 32000, 32
+    g = torch.Generator().manual_seed(11)
+    logits = spiked_logits(rows, vocab, seed=12, dtype=torch.float32)
+    logits[5] = torch.randint(-3, 4, (vocab,), generator=g).float()
+    logits[6] = 0.5
+    cols = torch.randperm(vocab, generator=g)[:300]
+    logits[7, cols] = 30.0 + 10.0 * torch.rand(300, generator=g)
+    logits = logits.to(dtype)
+    print(f"many narrow rows, one launch: {dtype}", flush=True)
+    check(logits, k, 1024)

@@ -132,13 +132,16 @@ def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
 
 
 @pytest.mark.parametrize("seed,draft_vocab,target_vocab,block", [(44, 6144, 8197, 2048), (45, 6144, 8197, 2048),
-                                                                (46, 40000, 131075, 16384)])
+                                                                (46, 40000, 131075, 16384),
+                                                                (47, 40000, 300007, 16384),
+                                                                (48, 40000, 300007, 8192)])
 def test_staged_grammar_target_vocabulary_not_a_multiple_of_32(seed, draft_vocab, target_vocab, block):
     """Drafting through d2t into a 8197-token target vocabulary (its last grammar word holds 5
     tokens) with every processor on: the tile kernel stages each row's 257 grammar words in
     workgroup memory, clears the bits past the vocabulary and reads a zero quad for clamped
     columns. Half the rows allow every token, including garbage bits past the vocabulary; d2t
-    reaches the last target ids."""
+    reaches the last target ids. A 300007-token target exceeds what the kernel stages (8192 words):
+    its gathers read the grammar words from global memory (in four passes at 16384 columns)."""
 
     from bench import spiked_logits, to_device
     from sonic_sampler.interface import UnshardedFusedSingular

@@ -511,35 +511,7 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
     torch.cuda.synchronize()
     tile_kernel_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
 
-    # hipGraph replays (one captured step per input set), back to back.
-    graphs = []
-
-    for i in range(sets):
-
-        g = torch.cuda.CUDAGraph()
-
-        with torch.cuda.graph(g):
-
-            step(i)
-
-        graphs.append(g)
-
-    for i in range(3 * sets):
-
-        graphs[i % sets].replay()
-
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _queue_behind_sleep(max(60.0, steps * 0.05))
-    start.record(stream)
-
-    for i in range(steps):
-
-        graphs[i % sets].replay()
-
-    end.record(stream)
-    torch.cuda.synchronize()
-    graph_us = start.elapsed_time(end) * 1e3 / steps
+    graph_us, graph_single_us = _time_graphs(step, steps, sets)
 
     algorithmic = c1_algorithmic_bytes(batch, vocab)
     tile_bytes = c1_tile_bytes(batch, vocab)
@@ -575,6 +547,7 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
             "median_event_pair_us": round(statistics.median(launch_us), 3),
             "tile_kernel_us": round(tile_kernel_us, 3),
             "graph_replay_us_per_step": round(graph_us, 3),
+            "graph_replay_single_step_us": round(graph_single_us, 3),
             "host_us_per_eager_call": round(statistics.median(enqueue) * 1e6, 1),
         },
         "roofline": {
@@ -619,6 +592,61 @@ def _time_back_to_back(step, steps: int) -> float:
     return start.elapsed_time(end) * 1e3 / steps
 
 
+def _time_graphs(step, steps: int, sets: int) -> tuple:
+    """Microseconds per step replayed from hipGraphs, back to back behind a GPU sleep: (a) one
+    graph holding the steps of every input set in turn, replayed steps // sets times, and (b) one
+    graph per step. A graph launch costs about 4 us of GPU time of its own, which (b) pays on every
+    step; an engine's graph holds its whole decode step (forward pass and sampling) and pays it
+    once per step whatever the sampler, so (a) is the sampler's share."""
+
+    stream = torch.cuda.current_stream()
+    whole = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(whole):
+
+        for i in range(sets):
+
+            step(i)
+
+    singles = []
+
+    for i in range(sets):
+
+        g = torch.cuda.CUDAGraph()
+
+        with torch.cuda.graph(g):
+
+            step(i)
+
+        singles.append(g)
+
+    def timed(replays, launch) -> float:
+
+        for i in range(3):
+
+            launch(i)
+
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _queue_behind_sleep(max(60.0, steps * 0.05))
+        start.record(stream)
+
+        for i in range(replays):
+
+            launch(i)
+
+        end.record(stream)
+        torch.cuda.synchronize()
+
+        return start.elapsed_time(end) * 1e3
+
+    rounds = max(1, steps // sets)
+    whole_us = timed(rounds, lambda i: whole.replay()) / (rounds * sets)
+    single_us = timed(steps, lambda i: singles[i % sets].replay()) / steps
+
+    return whole_us, single_us
+
+
 def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
     """Eager timing (launches queued back to back; per-step event pairs as a second figure) and
     hipGraph replay timing of `step(i)`."""
@@ -643,36 +671,11 @@ def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
     torch.cuda.synchronize()
     eager = [a.elapsed_time(b) * 1e3 for a, b in events]
     back_to_back = _time_back_to_back(step, steps)
-    graphs = []
-
-    for i in range(sets):
-
-        g = torch.cuda.CUDAGraph()
-
-        with torch.cuda.graph(g):
-
-            step(i)
-
-        graphs.append(g)
-
-    for i in range(3 * sets):
-
-        graphs[i % sets].replay()
-
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _queue_behind_sleep(max(60.0, steps * 0.05))
-    start.record(stream)
-
-    for i in range(steps):
-
-        graphs[i % sets].replay()
-
-    end.record(stream)
-    torch.cuda.synchronize()
+    graph_us, graph_single_us = _time_graphs(step, steps, sets)
 
     return {"eager_us": back_to_back, "event_pair_us": statistics.mean(eager),
-            "median_event_pair_us": statistics.median(eager), "graph_us": start.elapsed_time(end) * 1e3 / steps}
+            "median_event_pair_us": statistics.median(eager), "graph_us": graph_us,
+            "graph_single_us": graph_single_us}
 
 
 CONFIG_NAMES = {
@@ -826,6 +829,7 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
             "event_pair_us_per_step": round(t["event_pair_us"], 3),
             "median_event_pair_us": round(t["median_event_pair_us"], 3),
             "graph_replay_us_per_step": round(t["graph_us"], 3),
+            "graph_replay_single_step_us": round(t["graph_single_us"], 3),
         },
     }
 

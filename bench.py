@@ -680,7 +680,8 @@ def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
 
 CONFIG_NAMES = {
     0: "config 0: UnshardedBoundedTopK B=8 V=32000 fp32 k=32",
-    2: "config 2: UnshardedFusedMultistep greedy gamma=4 B=128 V=151936 bf16, logprobs",
+    2: "config 2: UnshardedFusedMultistep greedy gamma=4 B=128 V=151936 bf16, logprobs (all_greedy hint: "
+       "two launches)",
     3: "config 3: UnshardedFusedMultistep stochastic varlen gamma<=7 B=64 V=128256 bf16, draft "
        "probabilities, top-20 logprobs",
     4: "config 4: UnshardedFusedSingular.drafting t=3 of gamma=4, 256 of 512 slots, d2t 32000->262144, "
@@ -773,8 +774,10 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
 
             logits, tokens, buffers, probs, cu = staged[i % sets]
 
+            # config 2's requests are all greedy, which an engine running greedy verification
+            # knows: it says so, and the request stage takes the argmaxes itself
             return verifier(logits, tokens, buffers, probabilities=probs, logprobs=True, cu_seqlens=cu,
-                            philox_seed=None)
+                            philox_seed=None, all_greedy=config == 2)
 
         rows = works[0].logits.size(0)
         algorithmic = rows * works[0].vocab * 2

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SS_ABI_VERSION 2
+#define SS_ABI_VERSION 3
 
 /* Upper bound on top-k and the width of every candidate block (reference ops/base.py:24). */
 #define SS_MAX_K 128
@@ -249,6 +249,11 @@ typedef struct ss_multistep_args {
     /* timing: hipEvent_t pair recorded by the tile kernel's own dispatch (start, end), or NULL */
     void *tile_start;
     void *tile_end;
+    /* 1: the caller knows that every row's indicator has SS_GREEDY (for example from its host
+       copy of the indicators): the request stage takes each row's argmax from the tiles' maxima
+       itself and the row launch is skipped, one launch fewer. A row without SS_GREEDY is then
+       not served (its request's outputs are unspecified). 0: any mix of rows. */
+    int32_t all_greedy;
 } ss_multistep_args;
 
 int ss_fused_multistep(const ss_multistep_args *args);

@@ -281,7 +281,40 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args 
     const bool want_lp = a.return_logprobs && a.logprobs;
     int j = n - 1;
     int token;
-    if (greedy) {
+    if (greedy && a.all_greedy) {
+        // No row launch ran: row i's argmax comes from its tiles' maxima here (lane i holds it),
+        // and it is written where the row stage would have left it (indices[row, 0], values 0).
+        const int tiles = (a.vocab_size + a.block_n - 1) / a.block_n;
+        const ListMap lm = make_list_map(tiles, 0, a.block_n);
+        int argmax = 0;
+        if (n * tiles <= 64) {
+            // every (row, tile) maximum in one round of loads, lane r * tiles + t
+            const int r = lane / tiles, t = lane - r * tiles;
+            const uint32_t c = r < n ? a.scratch[(int64_t)(rq.margin + r) * a.stride_scratch + lm.greedy_entry(t)] : 0u;
+            const uint64_t c64 = ((uint64_t)(c >> 16) << 32) | ((uint64_t)(0xffffu - (uint32_t)t) << 16) |
+                                 (uint64_t)(c & 0xffffu);
+            for (int i = 0; i < n; ++i) {
+                const uint64_t best = wave_max_u64(r == i ? c64 : 0ull);
+                const int tile = (int)(0xffffu - (uint32_t)((best >> 16) & 0xffffu));
+                const int idx = lm.base(tile) + (int)(0xffffu - (uint32_t)(best & 0xffffu));
+                if (lane == i) argmax = idx < a.vocab_size ? idx : a.vocab_size - 1;
+            }
+        } else {
+            for (int i = 0; i < n; ++i) {
+                const uint32_t *srow = a.scratch + (int64_t)(rq.margin + i) * a.stride_scratch;
+                const uint32_t first = lane < tiles ? srow[lm.greedy_entry(lane)] : 0u;
+                const int idx = greedy_merge(srow, tiles, lm, a.vocab_size, first);
+                if (lane == i) argmax = idx;
+            }
+        }
+        if (lane < n) {
+            a.indices[(int64_t)(rq.margin + lane) * SS_K] = argmax;
+            a.values[(int64_t)(rq.margin + lane) * SS_K] = 0.0f;
+        }
+        const uint64_t m = __ballot(lane < n - 1 && argmax != drafted[lane < n - 1 ? lane : 0]);
+        j = m ? __ffsll((unsigned long long)m) - 1 : n - 1;
+        token = lane_i32(argmax, j);
+    } else if (greedy) {
         // lane i compares row i's argmax with drafted token i; all of them in one round of loads
         for (int base = 0; base < n - 1; base += 64) {
             const int i = base + lane;
@@ -365,8 +398,10 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
-    if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    if (!a->all_greedy) {
+        hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
+        if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
+    }
     hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }

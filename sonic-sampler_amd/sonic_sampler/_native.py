@@ -28,7 +28,7 @@ STAGE_TILES, STAGE_ROWS = 1, 2
 STATIC_SCRATCH_BYTES = 8 << 20   # SS_STATIC_SCRATCH_BYTES
 SS_DTYPE_BF16 = 0
 SS_DTYPE_F32 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class Philox(ctypes.Structure):
@@ -91,7 +91,7 @@ class MultistepArgs(ctypes.Structure):
         ("top_values", c_p), ("top_tokens", c_p), ("stride_top", c_i64),
         ("values", c_p), ("indices", c_p),
         ("scratch", c_p), ("stride_scratch", c_i64), ("stream", c_p),
-        ("tile_start", c_p), ("tile_end", c_p),
+        ("tile_start", c_p), ("tile_end", c_p), ("all_greedy", c_i32),
     ]
 
 

@@ -171,6 +171,7 @@ def fused_multistep(
     philox_seed: Optional[int] = None,
     philox_offset: int = 0,
     tile_events: Optional[Tuple[torch.cuda.Event, torch.cuda.Event]] = None,
+    all_greedy: bool = False,
 ) -> Verification:
 
     validate_count_update(update_counts, decode_counts)
@@ -287,6 +288,10 @@ def fused_multistep(
         stream=_native.stream_of(logits),
     )
     args.tile_start, args.tile_end = _native.event_pair(tile_events)
+    # The caller vouches that every row is greedy: each request's argmax is taken in the request
+    # stage and the row launch is skipped. A hint, never inferred here: a captured graph replays
+    # whatever was decided at capture while the indicators may change in place between replays.
+    args.all_greedy = int(bool(all_greedy))
 
     _native.check(_native.load().ss_fused_multistep(ctypes.byref(args)), "ss_fused_multistep")
 

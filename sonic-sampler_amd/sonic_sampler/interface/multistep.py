@@ -99,11 +99,14 @@ class UnshardedFusedMultistep(TwoStageTiling):
         philox_seed: Optional[int] = None,
         philox_offset: int = 0,
         tile_events=None,
+        all_greedy: bool = False,
     ) -> Verification:
         """Verifies the drafts in `tokens` against target `logits`.
 
         ``cu_seqlens`` (an addition) selects the variable-lookahead layout: ``logits`` is
         ``[sum_i (gamma_i + 1), V]`` and ``tokens`` the matching flat ``[sum_i (gamma_i + 1)]``.
+        ``all_greedy`` (an addition) tells the library that every row of `buffers.flags.target` is
+        greedy, which saves a launch; rows that are not greedy are then not served.
         """
 
         penalties = buffers.repetition
@@ -149,4 +152,5 @@ class UnshardedFusedMultistep(TwoStageTiling):
             philox_seed=philox_seed,
             philox_offset=philox_offset,
             tile_events=tile_events,
+            all_greedy=all_greedy,
         )

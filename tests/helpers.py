@@ -123,7 +123,7 @@ def check_multistep(verification, expected, cu_seqlens, *, logprobs: bool,
 
 
 def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, block_size=None,
-                 slot_mapping=None, buffers=None):
+                 slot_mapping=None, buffers=None, all_greedy=False):
 
     from bench import to_device
     from sonic_sampler.interface import UnshardedFusedMultistep
@@ -151,7 +151,7 @@ def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, bl
     probs = work.probabilities.to("cuda:0") if work.probabilities is not None else None
     verification = verifier(logits, tokens, buffers, probabilities=probs, update_counts=update_counts,
                             logprobs=logprobs, in_place=in_place, cu_seqlens=cu,
-                            slot_mapping=slot_mapping)
+                            slot_mapping=slot_mapping, all_greedy=all_greedy)
     torch.cuda.synchronize()
 
     return verification, buffers, verifier

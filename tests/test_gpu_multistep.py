@@ -212,3 +212,27 @@ def test_temperature_rows_at_the_cut(block):
         for i, idx in enumerate(e.row_indices):
 
             assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i, temperature[b])
+
+
+def test_config2_all_greedy_hint():
+    """Config 2 with the all_greedy hint (no row launch: the request stage takes every row's argmax
+    from the tiles' maxima) gives the oracle's verification and the same values / indices columns
+    as the call without it."""
+
+    from bench import c2_workload
+
+    work = c2_workload()
+    print("config 2 with the all_greedy hint", flush=True)
+    plain, _, verifier = run_verifier(work)
+    plain_indices = verifier.indices[:, 0].clone()
+    hinted, buffers, verifier2 = run_verifier(work, all_greedy=True, update_counts=True)
+
+    state = oracle.State.from_buffers(work.buffers)
+    expected = oracle.multistep(work.logits, state, work.drafted, work.cu_seqlens, logprobs=True)
+    check_multistep(hinted, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.0)
+    counts = oracle.apply_multistep_counts(state.decode, expected, None)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    assert torch.equal(hinted.tokens.cpu(), plain.tokens.cpu())
+    assert torch.equal(hinted.offsets.cpu(), plain.offsets.cpu())
+    assert torch.equal(verifier2.indices[:, 0].cpu(), plain_indices.cpu())
+    assert torch.all(verifier2.values[:, 0].cpu() == 0)

@@ -84,6 +84,9 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
         const int s = (int)threadIdx.x;
         const int list = s >> lkp;
         uint64_t c = list < tiles ? composite(list * k + (s & (kp64 - 1))) : 0ull;
+        // wave 0: the first unsampled entry of list t = lane, read with the samples so that the
+        // exactness check below waits for no further load
+        const uint64_t head = threadIdx.x < 64 && kp64 < k && lane < tiles ? composite(lane * k + kp64) : 0ull;
         wave_sort64_desc(c);
         sm.runs[wave][lane] = c;
         __syncthreads();
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
                 const uint64_t last = kth();
                 for (int t0 = 0; t0 < tiles; t0 += 64) {
                     const int t = t0 + lane;
-                    beats += __popcll(__ballot(t < tiles && composite(t * k + kp64) > last));
+                    beats += __popcll(__ballot(t < tiles && (t0 ? composite(t * k + kp64) : head) > last));
                 }
             }
             if (beats > TOPK_REFILL_LISTS) {
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
             } else {
                 for (int t0 = 0; beats > 0 && t0 < tiles; t0 += 64) {
                     const int t = t0 + lane;
-                    const uint64_t nx = t < tiles ? composite(t * k + kp64) : 0ull;
+                    const uint64_t nx = t < tiles ? (t0 ? composite(t * k + kp64) : head) : 0ull;
                     uint64_t m = __ballot(nx > kth());
                     while (m) {
                         const int l = t0 + (int)__builtin_ctzll(m);
@@ -160,6 +163,8 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
             const int list = s >> lkp;
             c[i] = list < tiles ? composite(list * k + (s & (kp - 1))) : 0ull;
         }
+        // wave 0: the first unsampled entry of list t = lane, read with the samples
+        const uint64_t head = threadIdx.x < 64 && kp < k && lane < tiles ? composite(lane * k + kp) : 0ull;
         wave_sort128_desc(c[0], c[1]);
         sm.runs[wave][2 * lane] = c[0];
         sm.runs[wave][2 * lane + 1] = c[1];
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
                 const uint64_t last = kth();
                 for (int t0 = 0; t0 < tiles; t0 += 64) {
                     const int t = t0 + lane;
-                    beats += __popcll(__ballot(t < tiles && composite(t * k + kp) > last));
+                    beats += __popcll(__ballot(t < tiles && (t0 ? composite(t * k + kp) : head) > last));
                 }
             }
             if (beats > TOPK_REFILL_LISTS) {
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, in
             } else {
                 for (int t0 = 0; beats > 0 && t0 < tiles; t0 += 64) {
                     const int t = t0 + lane;
-                    const uint64_t nx = t < tiles ? composite(t * k + kp) : 0ull;
+                    const uint64_t nx = t < tiles ? (t0 ? composite(t * k + kp) : head) : 0ull;
                     uint64_t m = __ballot(nx > kth());
                     while (m) {
                         const int l = t0 + (int)__builtin_ctzll(m);

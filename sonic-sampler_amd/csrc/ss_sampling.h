@@ -753,8 +753,6 @@ __device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int vt, u
 //   MODE_SCALAR      anything else: per-element loads throughout.
 enum { MODE_DIRECT = 0, MODE_GATHER_VEC = 1, MODE_SCALAR = 2 };
 
-// Streams one tile of one row through the processor chain and returns the keys (0 = absent).
-// `lw` holds the tile's logits from load_logits_vec unless MODE is MODE_SCALAR.
 // Gather pass H of a tile (elements j + 16 H, 4 H chunks of 1024 columns further) and the passes
 // after it. H is a template parameter so that the keys each pass writes keep constant indices: a
 // loop over the passes that the compiler leaves rolled (at E = 64 the body is too large to unroll)
@@ -778,6 +776,8 @@ __device__ __forceinline__ void gather_pass(const RowState &rs, const Uses &u, i
     }
 }
 
+// Streams one tile of one row through the processor chain and returns the keys (0 = absent).
+// `lw` holds the tile's logits from load_logits_vec unless MODE is MODE_SCALAR.
 template <int E, int MODE>
 __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
                                               const int32_t *hist, const u32x2 (&lw)[E / 4],

@@ -31,13 +31,15 @@ class TopTargets:
     logprobs: Tensor
 
     @classmethod
-    def empty_blocked(cls, batch_size: int, targets: int, timesteps: int = 1) -> Optional["TopTargets"]:
+    def empty_blocked(cls, batch_size: int, targets: int, timesteps: int = 1,
+                      device=None) -> Optional["TopTargets"]:
 
         if targets > 0:
 
             shape = (batch_size, timesteps, targets) if timesteps > 1 else (batch_size, targets)
 
-            return cls(tokens=torch.empty(shape, dtype=I32), logprobs=torch.empty(shape, dtype=BF16))
+            return cls(tokens=torch.empty(shape, dtype=I32, device=device),
+                       logprobs=torch.empty(shape, dtype=BF16, device=device))
 
         return None
 
@@ -64,11 +66,14 @@ class LogProbabilities:
     top_k: Optional[TopTargets] = None
 
     @classmethod
-    def empty_blocked(cls, batch_size: int, timesteps: int = 1, top_k: int = 0) -> "LogProbabilities":
+    def empty_blocked(cls, batch_size: int, timesteps: int = 1, top_k: int = 0,
+                      device=None) -> "LogProbabilities":
+        """`device` None: the current default device (the reference allocates under a device
+        context; an explicit device avoids entering one on every call)."""
 
-        selected = torch.empty(batch_size, timesteps, dtype=BF16)
+        selected = torch.empty(batch_size, timesteps, dtype=BF16, device=device)
 
-        return cls(selected=selected, top_k=TopTargets.empty_blocked(batch_size, top_k, timesteps))
+        return cls(selected=selected, top_k=TopTargets.empty_blocked(batch_size, top_k, timesteps, device=device))
 
     @classmethod
     def empty_varlen(cls, num_tokens: int, top_k: int = 0) -> "LogProbabilities":
@@ -103,9 +108,8 @@ class Selection:
 
         if logprobs:
 
-            with torch.device(tokens.device):
-
-                buffer = LogProbabilities.empty_blocked(batch_size=tokens.size(0), top_k=top_logprobs)
+            buffer = LogProbabilities.empty_blocked(batch_size=tokens.size(0), top_k=top_logprobs,
+                                                    device=tokens.device)
 
         return cls(tokens=tokens, probabilities=probabilities, logprobs=buffer)
 

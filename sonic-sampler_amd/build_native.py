@@ -31,6 +31,11 @@ HIPCC_FLAGS = [
     "-Wno-unused-variable",
     # no packed fp32 VALU instructions (v_pk_{add,mul,fma}_f32) anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # kernarg preload: the leading scalar arguments of a kernel (up to 16 dwords) arrive in SGPRs
+    # at wave launch, so its first loads need not wait for a kernarg-segment read. Each kernel
+    # takes the fields its first loads use as leading scalars ahead of the argument struct, which
+    # is passed by reference in the kernarg segment and is never preloaded.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -98,13 +98,15 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
 
 // Tile stage: grid (tiles, rows).
 template <int E, int MODE>
-__global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_args a, int tiles) {
+__global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(const uint16_t *p_logits, int64_t p_stride,
+                                                                   int p_block_n, int p_vocab, int tiles,
+                                                                   ss_multistep_args a) {
     __shared__ TileSmem<E> sm;
     const int row = blockIdx.y;
     const int tile = blockIdx.x;
     const int pivot = request_pivot(a);
     u32x2 lw[E / 4];
-    if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
+    if (MODE != MODE_SCALAR) load_logits_vec<E>(p_logits + (int64_t)row * p_stride, tile * p_block_n, p_vocab, lw);
     const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
@@ -130,13 +132,15 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(ss_multistep_
 // residual sample at a rejection, the bonus sample on the last row) with its logprob. It writes
 // them as one 16-byte record at the start of its scratch row, whose candidates it has consumed:
 // {accepted, stop token, logprob if accepted (fp32 bits), stop token's logprob (fp32 bits)}.
-__global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_args a, int tiles) {
+__global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(uint32_t *p_scratch, int64_t p_stride,
+                                                                  int p_block_n, int tiles,
+                                                                  ss_multistep_args a) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
     touch_kernargs<sizeof(ss_multistep_args)>();
-    uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch;
+    uint32_t *scr = p_scratch + (int64_t)row * p_stride;
     const int pivot = request_pivot(a);
-    const ListMap lm = make_list_map(tiles, 0, a.block_n);
+    const ListMap lm = make_list_map(tiles, 0, p_block_n);
     RowSamples smp;
     load_samples(scr, tiles, lm, smp);  // depends on the row only: issued early
     const Request rq = resolve_request(a, row, pivot);
@@ -248,21 +252,23 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(ss_multistep_a
 }
 
 // Request stage: grid B, one wavefront per request.
-__global__ __launch_bounds__(64) void multistep_verify_kernel(ss_multistep_args a) {
+__global__ __launch_bounds__(64) void multistep_verify_kernel(const int32_t *p_cu, const int32_t *p_slots,
+                                                             const uint16_t *p_ind, int p_lookahead,
+                                                             int p_rows, ss_multistep_args a) {
     const int b = blockIdx.x;
     Request rq;
-    if (a.cu_seqlens) {
+    if (p_cu) {
         rq.b = b;
-        rq.margin = a.cu_seqlens[b];
-        rq.n = a.cu_seqlens[b + 1] - rq.margin;
+        rq.margin = p_cu[b];
+        rq.n = p_cu[b + 1] - rq.margin;
     } else {
         rq.b = b;
-        rq.n = a.lookahead + 1;
+        rq.n = p_lookahead + 1;
         rq.margin = b * rq.n;
     }
-    if (rq.n < 1 || rq.n > a.lookahead + 1 || rq.margin < 0 || rq.margin + rq.n > a.rows) return;
-    const int slot = a.slot_mapping ? a.slot_mapping[rq.b] : rq.b;
-    const uint32_t ind = a.indicators[slot];
+    if (rq.n < 1 || rq.n > p_lookahead + 1 || rq.margin < 0 || rq.margin + rq.n > p_rows) return;
+    const int slot = p_slots ? p_slots[rq.b] : rq.b;
+    const uint32_t ind = p_ind[slot];
     const bool greedy = (ind & IND_GREEDY) != 0;
     const int top_lim = a.top_logprobs ? a.top_logprobs[slot] : a.max_top_logprobs;
 
@@ -390,19 +396,20 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
-        case 16384: launch_timed((multistep_tiles_kernel<64, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, *a, tiles); break;
+        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
+        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
+        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
+        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
+        case 16384: launch_timed((multistep_tiles_kernel<64, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     if (!a->all_greedy) {
-        hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, tiles);
+        hipLaunchKernelGGL(multistep_rows_kernel, dim3((unsigned)a->rows), block, 0, s, a->scratch, a->stride_scratch, a->block_n, tiles, *a);
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     }
-    hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, *a);
+    hipLaunchKernelGGL(multistep_verify_kernel, dim3((unsigned)a->batch), dim3(64), 0, s, a->cu_seqlens,
+                       a->slot_mapping, a->indicators, a->lookahead, a->rows, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 

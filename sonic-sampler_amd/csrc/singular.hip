@@ -53,8 +53,9 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 // element) they are bounded by the vector cache's line rate, not by HBM. Such launches number
 // their workgroups XCD by XCD (xcd_grouped), so that a row's tiles share one L2.
 template <int E, int MODE>
-__global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_args a, int tiles,
-                                                                  int stage_words) {
+__global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t *p_logits, int64_t p_stride,
+                                                                  int p_block_n, int p_vocab, int tiles,
+                                                                  int stage_words, ss_singular_args a) {
     // the tile stage's memory and, overlaying its runs and keys, a staged grammar row (dynamic
     // shared memory of tile_smem_bytes)
     extern __shared__ __align__(16) uint32_t tile_smem[];
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(ss_singular_ar
         tile = v - row * tiles;
     }
     u32x2 lw[E / 4];
-    if (MODE != MODE_SCALAR) load_logits_vec<E>(a.logits + (int64_t)row * a.stride_logits, tile * a.block_n, a.vocab_size, lw);
+    if (MODE != MODE_SCALAR) load_logits_vec<E>(p_logits + (int64_t)row * p_stride, tile * p_block_n, p_vocab, lw);
     const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
     const uint32_t ind = uniform_u16(a.indicators, slot);
     RowState rs = singular_row_state(a, row, slot, ind);
@@ -218,12 +219,16 @@ __device__ __forceinline__ void singular_row(const ss_singular_args &a, SampleSm
 
 // Row stage: grid rows; `lists` = world_size * tiles candidate lists per row, `V` the width of
 // the column space they index (all shards).
-__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(ss_singular_args a, int lists,
-                                                                ListMap lm, int V) {
+__global__ __launch_bounds__(SS_BLOCK) void singular_rows_kernel(const uint32_t *p_scratch, int64_t p_stride,
+                                                                int lists, uint32_t lm_magic, int lm_per,
+                                                                int lm_shard, int lm_block_n, int V,
+                                                                ss_singular_args a) {
     __shared__ SampleSmem sm;
     touch_kernargs<sizeof(ss_singular_args)>();
     const int row = blockIdx.x;
-    singular_row(a, sm, row, lists, lm, V, a.scratch + (int64_t)row * a.stride_scratch);
+    ListMap lm;
+    lm.magic = lm_magic; lm.per = lm_per; lm.shard = lm_shard; lm.block_n = lm_block_n;
+    singular_row(a, sm, row, lists, lm, V, p_scratch + (int64_t)row * p_stride);
 }
 
 // Workgroup memory of the one-launch form. The tile stage's and the row stage's memory share
@@ -346,11 +351,11 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     const int stages = a->stages ? a->stages : (SS_STAGE_TILES | SS_STAGE_ROWS);
     if (stages & SS_STAGE_TILES) {
         switch (a->block_n) {
-            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, tile_smem_bytes<4>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
-            case 16384: launch_timed((singular_tiles_kernel<64, MODE>), grid, block, tile_smem_bytes<64>(a), s, a->tile_start, a->tile_end, *a, tiles, stage); break;
+            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, tile_smem_bytes<4>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
+            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
+            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
+            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
+            case 16384: launch_timed((singular_tiles_kernel<64, MODE>), grid, block, tile_smem_bytes<64>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
             default: return SS_ERR_UNSUPPORTED;
         }
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
@@ -360,7 +365,7 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
         const int shard = world > 1 ? a->shard_size : 0;
         const ListMap lm = make_list_map(tiles, shard, a->block_n);
         const int V = world > 1 ? world * a->shard_size : a->vocab_size;
-        hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, *a, world * tiles, lm, V);
+        hipLaunchKernelGGL(singular_rows_kernel, dim3((unsigned)a->rows), block, 0, s, (const uint32_t *)a->scratch, a->stride_scratch, world * tiles, lm.magic, lm.per, lm.shard, lm.block_n, V, *a);
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
     }
     return SS_OK;

@@ -54,16 +54,17 @@ struct TopkTraits<true> {
 
 // Merge stage: grid rows.
 template <bool F32>
-__global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(ss_topk_args a, int tiles) {
+__global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, int64_t p_stride, int p_vocab,
+                                                              int p_k, int tiles, ss_topk_args a) {
     touch_kernargs<sizeof(ss_topk_args)>();
     using Tr = TopkTraits<F32>;
     using Cand = typename Tr::Cand;
     constexpr int CH = 4;
     __shared__ TopkSmem sm;
     const int row = blockIdx.x;
-    const int V = a.vocab_size;
-    const int k = a.k;
-    const Cand *scr = (const Cand *)a.scratch + (int64_t)row * a.stride_scratch;
+    const int V = p_vocab;
+    const int k = p_k;
+    const Cand *scr = (const Cand *)p_scratch + (int64_t)row * p_stride;
     const int ncand = tiles * k;
     // Samples: the first kp entries of every sorted list, kp = k when all tiles * k candidates
     // fit in 512 slots, else the largest power of two <= 512 / tiles (0 above 512 tiles).
@@ -320,18 +321,20 @@ __device__ __forceinline__ uint32_t float_key(float v) {
 }
 
 template <bool F32, bool VEC, int E>
-__global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(ss_topk_args a, int tiles) {
+__global__ __launch_bounds__(SS_BLOCK) void topk_block_kernel(const void *p_logits, int64_t p_stride,
+                                                              int p_block_n, int p_vocab, int p_k, int tiles,
+                                                              ss_topk_args a) {
     __shared__ TopkRowSmem sm;
     const int row = (int)blockIdx.x / tiles;
     const int tile = (int)blockIdx.x - row * tiles;
-    const int col0 = tile * a.block_n;  // first column of the block
-    const int V = min(a.block_n, a.vocab_size - col0);  // columns of the block
-    const int k = a.k;
+    const int col0 = tile * p_block_n;  // first column of the block
+    const int V = min(p_block_n, p_vocab - col0);  // columns of the block
+    const int k = p_k;
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane4 = 4 * (int)threadIdx.x;
     const int64_t bytes = (int64_t)V * (F32 ? 4 : 2);
-    const char *base = (const char *)a.logits + ((int64_t)row * a.stride_logits + col0) * (F32 ? 4 : 2);
+    const char *base = (const char *)p_logits + ((int64_t)row * p_stride + col0) * (F32 ? 4 : 2);
     const __amdgpu_buffer_rsrc_t rb = row_buffer(base, bytes);
     // the block's top-k: packed candidates of the merge kernel
     auto emit = [&](int e, uint32_t key, int col) {
@@ -539,16 +542,17 @@ __device__ __forceinline__ uint32_t wide_exclusive_scan(uint32_t n, uint32_t *re
 }
 
 template <bool F32, bool VEC>
-__global__ __launch_bounds__(TOPK_WIDE_THREADS) void topk_wide_kernel(ss_topk_args a) {
+__global__ __launch_bounds__(TOPK_WIDE_THREADS) void topk_wide_kernel(const void *p_logits, int64_t p_stride, int p_vocab,
+                                                                     int p_k, ss_topk_args a) {
     __shared__ TopkWideSmem sm;
     constexpr int E = TOPK_WIDE_E;
     const int row = (int)blockIdx.x;
-    const int V = a.vocab_size;
-    const int k = a.k;
+    const int V = p_vocab;
+    const int k = p_k;
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane4 = 4 * (int)threadIdx.x;
-    const char *base = (const char *)a.logits + (int64_t)row * a.stride_logits * (F32 ? 4 : 2);
+    const char *base = (const char *)p_logits + (int64_t)row * p_stride * (F32 ? 4 : 2);
     const __amdgpu_buffer_rsrc_t rb = row_buffer(base, (int64_t)V * (F32 ? 4 : 2));
     auto emit = [&](int e, uint64_t c) {
         const float val = __uint_as_float(unkey32((uint32_t)(c >> 32)));
@@ -726,19 +730,19 @@ template <bool F32>
 static int launch_topk_rows(const ss_topk_args *a) {
     dim3 grid((unsigned)a->rows), block(TOPK_WIDE_THREADS);
     hipStream_t s = (hipStream_t)a->stream;
-    if (topk_vec<F32>(a)) hipLaunchKernelGGL((topk_wide_kernel<F32, true>), grid, block, 0, s, *a);
-    else hipLaunchKernelGGL((topk_wide_kernel<F32, false>), grid, block, 0, s, *a);
+    if (topk_vec<F32>(a)) hipLaunchKernelGGL((topk_wide_kernel<F32, true>), grid, block, 0, s, a->logits, a->stride_logits, a->vocab_size, a->k, *a);
+    else hipLaunchKernelGGL((topk_wide_kernel<F32, false>), grid, block, 0, s, a->logits, a->stride_logits, a->vocab_size, a->k, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 
 template <bool F32, bool VEC>
 static int launch_topk_tiles(const ss_topk_args *a, int tiles, dim3 grid, dim3 block, hipStream_t s) {
     switch (a->block_n) {
-        case 1024: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 4>), grid, block, 0, s, *a, tiles); break;
-        case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8>), grid, block, 0, s, *a, tiles); break;
-        case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16>), grid, block, 0, s, *a, tiles); break;
-        case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32>), grid, block, 0, s, *a, tiles); break;
-        case 16384: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 64>), grid, block, 0, s, *a, tiles); break;
+        case 1024: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 4>), grid, block, 0, s, a->logits, a->stride_logits, a->block_n, a->vocab_size, a->k, tiles, *a); break;
+        case 2048: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 8>), grid, block, 0, s, a->logits, a->stride_logits, a->block_n, a->vocab_size, a->k, tiles, *a); break;
+        case 4096: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 16>), grid, block, 0, s, a->logits, a->stride_logits, a->block_n, a->vocab_size, a->k, tiles, *a); break;
+        case 8192: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 32>), grid, block, 0, s, a->logits, a->stride_logits, a->block_n, a->vocab_size, a->k, tiles, *a); break;
+        case 16384: hipLaunchKernelGGL((topk_block_kernel<F32, VEC, 64>), grid, block, 0, s, a->logits, a->stride_logits, a->block_n, a->vocab_size, a->k, tiles, *a); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     return SS_OK;
@@ -753,7 +757,7 @@ static int launch_topk(const ss_topk_args *a, int tiles) {
                                     : launch_topk_tiles<F32, false>(a, tiles, grid, block, s);
     if (st != SS_OK) return st;
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, *a, tiles);
+    hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, a->scratch, a->stride_scratch, a->vocab_size, a->k, tiles, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 

@@ -646,18 +646,22 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
         // a masked element becomes bf16 -inf (0xff80) in place; a column outside the target
         // vocabulary (negative, or at or past it) reads 0 (masked) on either path
         if (u.g && rs.glds) {
-            // Staged row (stage_grammar): a column is clamped to lim, the first bit of the zero
-            // words past the row, and the bits past the vocabulary in its last word are clear,
-            // so the lookup needs no range branch. The pair's two keep bits become a 16-bit mask
-            // per half that selects between the pair and two -inf halves.
+            // Staged row (stage_grammar): a column's word index is clamped to that of lim, the
+            // first bit of the zero words past the row, and the bits past the vocabulary in its
+            // last word are clear, so the lookup needs no range branch. v_bfe reads the low five
+            // bits of its offset operand, the column's bit within the word; a signed one-bit field
+            // is 0 or all ones, and the pair's two of them select, half by half, between the pair
+            // and two -inf halves.
             const lds_cu32p gl = (lds_cu32p)rs.glds;
-            const uint32_t lim = (uint32_t)(stage_quads(rs.vt) * 128);
+            const uint32_t wlim = (uint32_t)(stage_quads(rs.vt) * 4);
 #pragma unroll
             for (int i = 0; i < E / 2; ++i) {
-                const uint32_t t0 = min((uint32_t)tcol[2 * i], lim), t1 = min((uint32_t)tcol[2 * i + 1], lim);
-                const uint32_t b0 = (gl[t0 >> 5] >> (t0 & 31)) & 1u;
-                const uint32_t b1 = (gl[t1 >> 5] >> (t1 & 31)) & 1u;
-                const uint32_t keep = ((b1 << 16) | b0) * 0xffffu;
+                const uint32_t t0 = (uint32_t)tcol[2 * i], t1 = (uint32_t)tcol[2 * i + 1];
+                const uint32_t w0 = gl[min(__builtin_amdgcn_ubfe(t0, 5u, 27u), wlim)];
+                const uint32_t w1 = gl[min(__builtin_amdgcn_ubfe(t1, 5u, 27u), wlim)];
+                const uint32_t k0 = (uint32_t)__builtin_amdgcn_sbfe((int)w0, t0, 1u);
+                const uint32_t k1 = (uint32_t)__builtin_amdgcn_sbfe((int)w1, t1, 1u);
+                const uint32_t keep = (k0 & 0xffffu) | (k1 & 0xffff0000u);
                 const uint32_t p = (i & 1) ? lv[i >> 1].y : lv[i >> 1].x;
                 const uint32_t m = (p & keep) | (0xff80ff80u & ~keep);
                 if (i & 1) lv[i >> 1].y = m; else lv[i >> 1].x = m;

@@ -217,11 +217,14 @@ constexpr int NT = 2;  // non-temporal: each plane is read once
 typedef short s2v __attribute__((ext_vector_type(2)));
 typedef unsigned short u2v __attribute__((ext_vector_type(2)));
 
-// key16 of the two bf16 halves of `u` at once, with packed 16-bit integer operations.
+// key16 of the two bf16 halves of `u` at once, with packed 16-bit integer operations: with m the
+// half's sign mask (0 or 0xffff), (u ^ (m | 0x8000)) - m is u + 0x8000 for a positive half and
+// (0x7fff - magnitude) + 1 = 0x8000 - magnitude for a negative one (-0 and +0 both 0x8000). The
+// xor-or is one three-input bit operation: three instructions a pair.
 __device__ __forceinline__ uint32_t packed_keys(uint32_t u) {
     const uint32_t m = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s2v, u) >> (s2v){15, 15});
-    const uint32_t neg = __builtin_bit_cast(uint32_t, (u2v){0, 0} - __builtin_bit_cast(u2v, u));
-    return (neg & m) | ((u | 0x80008000u) & ~m);
+    const uint32_t t = u ^ (m | 0x80008000u);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u2v, t) - __builtin_bit_cast(u2v, m));
 }
 
 // bf16 rounding of one value (round-to-nearest-even): converted into the high half of a packed

@@ -479,3 +479,39 @@ def test_xcd_grouped_is_a_bijection_with_contiguous_xcd_ranges():
 
         row = xcd_grouped(L, 1024) // tiles
         assert all(xcd_grouped(M, 1024) // tiles != row or M % 8 == L % 8 for M in range(L % 8, 1024, 1))
+
+
+def packed_keys(u: int) -> int:
+    """csrc/ss_sampling.h packed_keys on one 32-bit word (two bf16 halves), as 16-bit lane
+    operations: m = arithmetic shift of each half by 15, t = u ^ (m | 0x80008000), t - m per half."""
+
+    m = sum((0xffff if (u >> s) & 0x8000 else 0) << s for s in (0, 16))
+    t = u ^ (m | 0x80008000)
+
+    return sum(((((t >> s) & 0xffff) - ((m >> s) & 0xffff)) & 0xffff) << s for s in (0, 16))
+
+
+def test_packed_keys_follow_the_order_of_the_values():
+    """Keys of every non-NaN bf16 value sort as the values do, equal values (+0 and -0) share a
+    key, and the two halves of a word are keyed independently (no carry between them)."""
+
+    import torch
+
+    bits = np.arange(0x10000, dtype=np.uint32)
+    values = torch.from_numpy(bits.astype(np.int32).astype(np.int16)).view(torch.bfloat16).float().numpy()
+    finite = ~np.isnan(values)
+    keys = np.array([packed_keys(int(b)) & 0xffff for b in bits])
+    v, k = values[finite], keys[finite]
+    order = np.argsort(v, kind="stable")
+    sv, sk = v[order], k[order]
+    assert np.all(np.diff(sk) >= 0)
+    assert np.all((np.diff(sk) == 0) == (np.diff(sv) == 0))
+    assert packed_keys(0x80008000) == packed_keys(0x00000000) == 0x80008000
+    assert (k > 0).all()
+
+    rng = np.random.default_rng(7)
+
+    for lo, hi in rng.integers(0, 0x10000, (2000, 2)).tolist():
+
+        both = packed_keys(lo | (hi << 16))
+        assert both & 0xffff == keys[lo] and both >> 16 == keys[hi]

@@ -100,7 +100,7 @@ typedef struct ss_topk_args {
     int32_t vocab_size;
     int32_t k;           /* power of two, 1 <= k <= 128 */
     int32_t block_n;     /* tile width: 1024, 2048, 4096, 8192 or 16384 */
-    int32_t strategy;    /* ss_strategy: 0 automatic (tile grid; one workgroup per row for >= 128 rows
+    int32_t strategy;    /* ss_strategy: 0 automatic (tile grid; one workgroup per row for >= 48 rows
                             of 16385-32768 columns at k <= 32), 2 one workgroup per row (V <= 32768) */
     void *scratch;       /* rows * stride_scratch elements (uint32 or uint64) */
     int64_t stride_scratch;

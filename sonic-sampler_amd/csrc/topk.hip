@@ -778,15 +778,15 @@ extern "C" int ss_topk(const ss_topk_args *a) {
     if (a->rows == 0) return SS_OK;
     if (a->strategy < SS_STRATEGY_AUTO || a->strategy > SS_STRATEGY_ROWWISE) return SS_ERR_INVALID_ARGUMENT;
     // One 1024-thread workgroup per row (one launch) serves rows of at most 32768 columns on
-    // request. AUTO takes it where it measured faster than the tile grid at every width: at least
-    // 128 rows of more than 16384 columns and k <= 32 (256 rows of 32000 fp32 columns at k = 32:
-    // 12.1 us against 17.0; 1024 rows: 42.5 against 47.6). Fewer rows leave CUs idle while one CU
-    // streams each row (8 rows of 32000 fp32: 9.6 against 8.6 us), narrower rows leave most of a
-    // thread's 32 elements empty, and a larger k overflows the survivor list into the exact
-    // selection.
+    // request. AUTO takes it where it measured faster than the tile grid at the tuned widths: at
+    // least 48 rows of more than 16384 columns and k <= 32 (rows of 32000 columns at k = 32, back
+    // to back: fp32 48 rows 9.3 us against 9.6, 128 rows 9.7 against 11.3, 256 rows 12.1 against
+    // 17.0; bf16 64 rows 8.8 against 9.5). Fewer rows leave CUs idle while one CU streams each
+    // row (fp32 32 rows: 9.2 against 8.6 us), narrower rows leave most of a thread's 32 elements
+    // empty, and a larger k overflows the survivor list into the exact selection.
     if (a->strategy == SS_STRATEGY_ROWWISE && a->vocab_size > ss::TOPK_WIDE_THREADS * ss::TOPK_WIDE_E) return SS_ERR_UNSUPPORTED;
     const bool wide = a->strategy == SS_STRATEGY_ROWWISE ||
-                      (a->strategy == SS_STRATEGY_AUTO && a->rows >= 128 && a->k <= 32 && a->vocab_size > 16384 &&
+                      (a->strategy == SS_STRATEGY_AUTO && a->rows >= 48 && a->k <= 32 && a->vocab_size > 16384 &&
                        a->vocab_size <= ss::TOPK_WIDE_THREADS * ss::TOPK_WIDE_E);
     if (wide)
         return a->dtype == SS_DTYPE_F32 ? ss::launch_topk_rows<true>(a) : ss::launch_topk_rows<false>(a);

@@ -2,7 +2,7 @@
 
 ``ss_topk`` makes two launches: a tile stage that writes the exact top-k of every (row, tile)
 workgroup as a sorted candidate list, then a merge stage that takes the row's top-k from those
-lists in descending order; for at least 128 rows of 16385-32768 columns at k <= 32 it makes one
+lists in descending order; for at least 48 rows of 16385-32768 columns at k <= 32 it makes one
 launch instead, a 1024-thread workgroup per row. Ties go to the lowest column. bfloat16 and
 float32 logits are accepted; values come back in the logits' dtype.
 

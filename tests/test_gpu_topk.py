@@ -176,15 +176,16 @@ def test_merge_paths_at_128_tiles(k, dtype):
     check(logits.to(dtype), k, block)
 
 
+@pytest.mark.parametrize("rows", [48, 160])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_many_narrow_rows_take_one_launch(dtype):
-    """160 rows of 32000 columns at k = 32 through the interface: the library's automatic choice
-    is one 1024-thread workgroup per row; bit-exact against the oracle, with tied and crowded rows
-    among them."""
+def test_many_narrow_rows_take_one_launch(dtype, rows):
+    """48 and 160 rows of 32000 columns at k = 32 through the interface: the library's automatic
+    choice is one 1024-thread workgroup per row; bit-exact against the oracle, with tied and
+    crowded rows among them."""
 
     from bench import spiked_logits
 
-    rows, vocab, k = 160, 32000, 32
+    vocab, k = 32000, 32
     g = torch.Generator().manual_seed(11)
     logits = spiked_logits(rows, vocab, seed=12, dtype=torch.float32)
     logits[5] = torch.randint(-3, 4, (vocab,), generator=g).float()
@@ -192,5 +193,5 @@ def test_many_narrow_rows_take_one_launch(dtype):
     cols = torch.randperm(vocab, generator=g)[:300]
     logits[7, cols] = 30.0 + 10.0 * torch.rand(300, generator=g)
     logits = logits.to(dtype)
-    print(f"many narrow rows, one launch: {dtype}", flush=True)
+    print(f"many narrow rows, one launch: {rows} rows {dtype}", flush=True)
     check(logits, k, 1024)

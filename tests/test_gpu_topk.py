@@ -105,7 +105,8 @@ def test_one_launch_rows_concentrated_values():
 
 
 @pytest.mark.parametrize("vocab,k,dtype", [(32000, 32, torch.float32), (30001, 128, torch.bfloat16),
-                                           (8192, 8, torch.float32)])
+                                           (8192, 8, torch.float32), (32768, 1, torch.bfloat16),
+                                           (16385, 2, torch.float32)])
 def test_one_workgroup_per_row_strategy(vocab, k, dtype):
     """ss_topk with strategy ROWWISE (one launch, one 1024-thread workgroup per row), called
     through the C-ABI: bit-exact against the oracle, including rows whose survivors need two sorting

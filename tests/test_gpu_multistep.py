@@ -236,3 +236,83 @@ def test_config2_all_greedy_hint():
     assert torch.equal(hinted.offsets.cpu(), plain.offsets.cpu())
     assert torch.equal(verifier2.indices[:, 0].cpu(), plain_indices.cpu())
     assert torch.all(verifier2.values[:, 0].cpu() == 0)
+
+
+def test_graph_replay_config2_all_greedy_hint():
+    """Config 2 with the all_greedy hint captured in a hipGraph (tile and request launches only)
+    and replayed over new logits, drafts and decode counts copied into the captured tensors: every
+    replay equals the eager call, and the first ones the oracle."""
+
+    from bench import c2_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    sets = [c2_workload(seed=1002 + 10 * k) for k in range(3)]
+    base = sets[0]
+    batch, n = len(base.cu_seqlens) - 1, base.lookahead + 1
+    buffers = to_device(base.buffers, DEV)
+    logits = base.logits.view(batch, n, -1).to(DEV)
+    drafted = base.drafted.view(batch, n).to(DEV)
+    decode = buffers.repetition.counts.decode
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=base.vocab, lookahead=base.lookahead,
+                                                  batch_size=batch, max_top_logprobs=base.max_top_logprobs,
+                                                  device=DEV)
+
+    def load(k):
+
+        logits.copy_(sets[k].logits.view(batch, n, -1))
+        drafted.copy_(sets[k].drafted.view(batch, n))
+        decode.copy_(sets[k].buffers.repetition.counts.decode)
+
+    def call():
+
+        return verifier(logits, drafted, buffers, update_counts=True, logprobs=True, all_greedy=True)
+
+    def outputs(v):
+
+        return [v.offsets.clone(), v.tokens.clone(), decode.clone()]
+
+    eager = []
+
+    for k in range(3):
+
+        load(k)
+        eager.append(outputs(call()))
+
+    torch.cuda.synchronize()
+    print("config 2 with the all_greedy hint, eager outputs for 3 input sets; capturing", flush=True)
+    load(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        call()
+
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(graph):
+
+        captured = call()
+
+    for rnd, k in enumerate([1, 2, 0, 2, 1]):
+
+        load(k)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"replay {rnd}: input set {k}", flush=True)
+        got = outputs(captured)
+
+        for a, b in zip(got, eager[k]):
+
+            assert torch.equal(a, b), f"replay {rnd} of input set {k} differs from the eager call"
+
+        if rnd < 3:
+
+            work = sets[k]
+            state = oracle.State.from_buffers(work.buffers)
+            expected = oracle.multistep(work.logits, state, work.drafted, work.cu_seqlens, logprobs=True)
+            check_multistep(captured, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.0)
+            counts = oracle.apply_multistep_counts(state.decode, expected, None)
+            assert torch.equal(got[-1].cpu(), counts)

@@ -196,3 +196,57 @@ def test_many_narrow_rows_take_one_launch(dtype, rows):
     logits = logits.to(dtype)
     print(f"many narrow rows, one launch: {rows} rows {dtype}", flush=True)
     check(logits, k, 1024)
+
+
+@pytest.mark.parametrize("rows", [8, 64])
+def test_graph_replay(rows):
+    """ss_topk captured in a hipGraph (8 rows: tile and merge launches; 64 rows: one workgroup per
+    row) and replayed over new logits copied into the captured input: every replay equals the
+    eager call and the oracle."""
+
+    from bench import spiked_logits
+    from sonic_sampler.interface import UnshardedBoundedTopK
+
+    vocab, k = 32000, 32
+    sets = [spiked_logits(rows, vocab, seed=500 + i, dtype=torch.float32) for i in range(3)]
+    x = sets[0].to(DEV)
+    topk = UnshardedBoundedTopK.initialize(vocab_size=vocab, batch_size=rows, k=k, device=DEV)
+    eager = []
+
+    for s in sets:
+
+        x.copy_(s)
+        values, indices = topk(x)
+        eager.append((values.clone(), indices.clone()))
+
+    torch.cuda.synchronize()
+    print(f"top-k graph replay: {rows} rows; capturing", flush=True)
+    x.copy_(sets[0])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        topk(x)
+
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(graph):
+
+        captured = topk(x)
+
+    for rnd, i in enumerate([1, 2, 0, 2, 1]):
+
+        x.copy_(sets[i])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"replay {rnd}: input set {i}", flush=True)
+        assert torch.equal(captured[0], eager[i][0]) and torch.equal(captured[1], eager[i][1])
+
+        if rnd < 3:
+
+            ev, ei = oracle_topk(sets[i], k)
+            assert torch.equal(captured[1].cpu(), ei)
+            assert torch.equal(captured[0].cpu().view(torch.int32), ev.view(torch.int32))

@@ -420,6 +420,93 @@ def test_graph_replay_autoregressive_config1():
                 assert torch.equal(got[-1].cpu(), counts)
 
 
+def test_graph_replay_drafting_config4():
+    """Config 4 (drafting through d2t into a 262144-token target vocabulary, staged grammar)
+    captured in a hipGraph and replayed over new logits, buffers, drafts, slots and d2t copied
+    into the captured tensors: every replay equals the eager call, and the first ones the
+    oracle."""
+
+    from bench import c4_workload, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    sets = [c4_workload(seed=1004 + 10 * k) for k in range(3)]
+    base = sets[0]
+    rows, slots = base.logits.size(0), base.buffers.layout.rows
+    buffers = to_device(base.buffers, DEV)
+    logits = base.logits.to(DEV)
+    tokens = base.tokens.to(DEV)
+    slot_mapping = base.slot_mapping.to(DEV)
+    d2t = base.d2t.to(DEV)
+    probs = torch.zeros(slots, base.target_vocab, dtype=torch.bfloat16, device=DEV)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=base.vocab, batch_size=rows, lookahead=4,
+                                                max_top_logprobs=5, device=DEV)
+
+    def load(k):
+
+        work = sets[k]
+        load_into(buffers, work.buffers)
+        logits.copy_(work.logits)
+        tokens.copy_(work.tokens)
+        slot_mapping.copy_(work.slot_mapping)
+        d2t.copy_(work.d2t)
+        probs.zero_()
+
+    def call():
+
+        return sampler.drafting(logits, buffers, timestep=base.timestep, tokens=tokens, probabilities=probs,
+                                slot_mapping=slot_mapping, d2t_mapping=d2t, target_vocab=base.target_vocab,
+                                in_place=True)
+
+    eager = []
+
+    for k in range(3):
+
+        load(k)
+        selection = call()
+        eager.append([selection.tokens.clone(), probs.clone()])
+
+    torch.cuda.synchronize()
+    print("config 4 eager outputs for 3 input sets; capturing", flush=True)
+    load(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        call()
+
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+
+    with torch.cuda.graph(graph):
+
+        captured = call()
+
+    for rnd, k in enumerate([1, 2, 0, 2, 1]):
+
+        load(k)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"replay {rnd}: input set {k}", flush=True)
+        got = [captured.tokens.clone(), probs.clone()]
+
+        for a, b in zip(got, eager[k]):
+
+            assert torch.equal(a, b), f"replay {rnd} of input set {k} differs from the eager call"
+
+        if rnd < 3:
+
+            work = sets[k]
+            state = oracle.State.from_buffers(work.buffers)
+            expected = oracle.singular(work.logits, state, scope="draft", timestep=work.timestep,
+                                       slot_mapping=work.slot_mapping.tolist(), d2t=work.d2t,
+                                       drafted=work.tokens, history=work.timestep, probs=True,
+                                       max_top_logprobs=5)
+            check_singular(captured, expected, logprobs=False, probabilities=probs,
+                           slot_mapping=work.slot_mapping)
+
+
 def test_graph_replay_verifier_config3():
 
     from bench import c3_workload, to_device

@@ -137,12 +137,14 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_rows_kernel(uint32_t *p_sc
                                                                   ss_multistep_args a) {
     __shared__ SampleSmem sm;
     const int row = blockIdx.x;
-    touch_kernargs<sizeof(ss_multistep_args)>();
     uint32_t *scr = p_scratch + (int64_t)row * p_stride;
-    const int pivot = request_pivot(a);
     const ListMap lm = make_list_map(tiles, 0, p_block_n);
+    // the merge samples depend on the row and the preloaded arguments only: issued first, ahead
+    // of the argument lines the rest of the row stage reads
     RowSamples smp;
-    load_samples(scr, tiles, lm, smp);  // depends on the row only: issued early
+    load_samples<true>(scr, tiles, lm, smp);
+    touch_kernargs<sizeof(ss_multistep_args)>();
+    const int pivot = request_pivot(a);
     const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;

@@ -1233,8 +1233,21 @@ __device__ __forceinline__ int merge_run(int kp) {
     return (kp >= 8 && kp <= 64 && (kp & (kp - 1)) == 0) ? kp : 1;
 }
 
+// BUF: `scr` is a global scratch row of tiles * 128 words, read by range-checked buffer loads (an
+// entry outside the row reads 0), so that every load issues unbranched, ahead of whatever the
+// kernel waits for next; else `scr` may be workgroup memory.
+template <bool BUF = false>
 __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, const ListMap &lm,
                                              RowSamples &smp) {
+    const int words = tiles * SS_K;
+    auto at = [&](bool ok, int w) -> uint32_t {
+        if constexpr (BUF) {
+            const __amdgpu_buffer_rsrc_t rb = row_buffer(scr, (int64_t)words * 4);
+            return __builtin_amdgcn_raw_buffer_load_b32(rb, (ok ? w : words) * 4, 0, 0);
+        } else {
+            return ok ? scr[w] : 0u;
+        }
+    };
     const int kp = merge_prefix(tiles);
     smp.kp = kp;
     // above 512 tiles kp is 0: nothing is merged and the exactness check sends the row to the
@@ -1245,27 +1258,36 @@ __device__ __forceinline__ void load_samples(const uint32_t *scr, int tiles, con
     const int wave = (int)threadIdx.x >> 6, lane = lane_id();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+        // run > 1: element e = 2 * lane + i of the wave is in run r = e / kp, i.e. list
+        // 128 / kp * wave + r; else any placement. With BUF both are computed and one is
+        // selected, so that no branch separates the loads below from the kernel's start (the
+        // singular row kernel measured faster with the branch).
         int s, list;
-        if (run > 1) {
-            // element e = 2 * lane + i of the wave: run r = e / kp, i.e. list 128 / kp * wave + r
-            const int lr = __builtin_ctz((unsigned)run);
-            const int e = 2 * lane + i;
-            const int r = e >> lr, q = e & (run - 1);
+        const int lr = __builtin_ctz((unsigned)run);
+        const int e = 2 * lane + i;
+        const int r = e >> lr, q = e & (run - 1);
+        if (BUF) {
+            const int list_r = wave * (SS_K >> lr) + r;
+            const int s_r = (list_r << lr) + ((r & 1) ? run - 1 - q : q);
+            const int s_a = 2 * (int)threadIdx.x + i;
+            s = run > 1 ? s_r : s_a;
+            list = run > 1 ? list_r : slot_list(smp, s_a);
+        } else if (run > 1) {
             list = wave * (SS_K >> lr) + r;
             s = (list << lr) + ((r & 1) ? run - 1 - q : q);
         } else {
-            s = 2 * (int)threadIdx.x + i;  // any placement
+            s = 2 * (int)threadIdx.x + i;
             list = slot_list(smp, s);
         }
         smp.slot[i] = s;
         smp.base[i] = lm.base(list);
-        smp.raw[i] = s < ns ? scr[list * SS_K + (s - list * kp)] : 0u;
+        smp.raw[i] = at(s < ns, list * SS_K + (s - list * kp));
     }
     const int t = (int)threadIdx.x;
-    smp.next = (t < 64 && t < tiles && kp < SS_K) ? scr[t * SS_K + kp] : 0u;
+    smp.next = at(t < 64 && t < tiles && kp < SS_K, t * SS_K + kp);
     // read before the row's indicator is known, so that a greedy row's merge waits for no
     // further load
-    smp.greedy = (t < 64 && t < tiles) ? scr[lm.greedy_entry(t)] : 0u;
+    smp.greedy = at(t < 64 && t < tiles, lm.greedy_entry(t));
 }
 
 // Lists that merge_refill merges whole; a row with more lists beating its sampled top-128 takes

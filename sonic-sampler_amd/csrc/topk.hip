@@ -55,8 +55,8 @@ struct TopkTraits<true> {
 // Merge stage: grid rows.
 template <bool F32>
 __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, int64_t p_stride, int p_vocab,
-                                                              int p_k, int tiles, ss_topk_args a) {
-    touch_kernargs<sizeof(ss_topk_args)>();
+                                                              int p_k, int p_block_n, int tiles,
+                                                              ss_topk_args a) {
     using Tr = TopkTraits<F32>;
     using Cand = typename Tr::Cand;
     constexpr int CH = 4;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, i
         const int lk = __builtin_ctz((unsigned)k), lkp = __builtin_ctz((unsigned)kp64);
         auto composite = [&](int p) {
             const Cand cd = scr[p];
-            const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
+            const uint32_t col = (uint32_t)((p >> lk) * p_block_n + Tr::cand_li(cd));
             return ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
         };
         const int s = (int)threadIdx.x;
@@ -88,6 +88,9 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, i
         // wave 0: the first unsampled entry of list t = lane, read with the samples so that the
         // exactness check below waits for no further load
         const uint64_t head = threadIdx.x < 64 && kp64 < k && lane < tiles ? composite(lane * k + kp64) : 0ull;
+        // the samples depend on the row and the preloaded arguments only: in flight before the
+        // argument lines the rest of the merge reads
+        touch_kernargs<sizeof(ss_topk_args)>();
         wave_sort64_desc(c);
         sm.runs[wave][lane] = c;
         __syncthreads();
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, i
         const int lk = __builtin_ctz((unsigned)k), lkp = __builtin_ctz((unsigned)kp);  // powers of two
         auto composite = [&](int p) {
             const Cand cd = scr[p];
-            const uint32_t col = (uint32_t)((p >> lk) * a.block_n + Tr::cand_li(cd));
+            const uint32_t col = (uint32_t)((p >> lk) * p_block_n + Tr::cand_li(cd));
             return ((uint64_t)Tr::cand_key(cd) << 32) | (uint64_t)(0xffffffffu - col);
         };
         uint64_t c[2];
@@ -166,6 +169,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, i
         }
         // wave 0: the first unsampled entry of list t = lane, read with the samples
         const uint64_t head = threadIdx.x < 64 && kp < k && lane < tiles ? composite(lane * k + kp) : 0ull;
+        touch_kernargs<sizeof(ss_topk_args)>();
         wave_sort128_desc(c[0], c[1]);
         sm.runs[wave][2 * lane] = c[0];
         sm.runs[wave][2 * lane + 1] = c[1];
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(SS_BLOCK) void topk_merge_kernel(void *p_scratch, i
         if (pos >= (uint32_t)k) return;
         const int p = order_pos<EM, CH>(sc, j);
         const Cand c = scr[p];
-        const int idx = (p / k) * a.block_n + Tr::cand_li(c);
+        const int idx = (p / k) * p_block_n + Tr::cand_li(c);
         sm.cand[pos] = ((uint64_t)Tr::cand_key(c) << 8) | (uint64_t)(127u - pos);
         sm.idx[pos] = idx < V ? idx : V - 1;
     });
@@ -757,7 +761,8 @@ static int launch_topk(const ss_topk_args *a, int tiles) {
                                     : launch_topk_tiles<F32, false>(a, tiles, grid, block, s);
     if (st != SS_OK) return st;
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;
-    hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, a->scratch, a->stride_scratch, a->vocab_size, a->k, tiles, *a);
+    hipLaunchKernelGGL((topk_merge_kernel<F32>), dim3((unsigned)a->rows), block, 0, s, a->scratch, a->stride_scratch, a->vocab_size, a->k,
+                       a->block_n, tiles, *a);
     return hipGetLastError() == hipSuccess ? SS_OK : SS_ERR_LAUNCH;
 }
 

@@ -55,7 +55,8 @@ __device__ __forceinline__ RowState singular_row_state(const ss_singular_args &a
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t *p_logits, int64_t p_stride,
                                                                   int p_block_n, int p_vocab, int tiles,
-                                                                  int stage_words, ss_singular_args a) {
+                                                                  int stage_words, const int32_t *p_slots,
+                                                                  const uint16_t *p_ind, ss_singular_args a) {
     // the tile stage's memory and, overlaying its runs and keys, a staged grammar row (dynamic
     // shared memory of tile_smem_bytes)
     extern __shared__ __align__(16) uint32_t tile_smem[];
@@ -71,8 +72,9 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t
     }
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(p_logits + (int64_t)row * p_stride, tile * p_block_n, p_vocab, lw);
-    const int slot = a.slot_mapping ? a.slot_mapping[row] : row;
-    const uint32_t ind = uniform_u16(a.indicators, slot);
+    // the row's slot and indicator decide which planes the tile reads: through preloaded pointers
+    const int slot = p_slots ? uniform_i32(p_slots, row) : row;
+    const uint32_t ind = uniform_u16(p_ind, slot);
     RowState rs = singular_row_state(a, row, slot, ind);
     bool sync = false;
     if (MODE != MODE_DIRECT && stage_words > 0) {
@@ -351,11 +353,11 @@ static int launch_singular(const ss_singular_args *a, int tiles) {
     const int stages = a->stages ? a->stages : (SS_STAGE_TILES | SS_STAGE_ROWS);
     if (stages & SS_STAGE_TILES) {
         switch (a->block_n) {
-            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, tile_smem_bytes<4>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
-            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
-            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
-            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
-            case 16384: launch_timed((singular_tiles_kernel<64, MODE>), grid, block, tile_smem_bytes<64>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, *a); break;
+            case 1024: launch_timed((singular_tiles_kernel<4, MODE>), grid, block, tile_smem_bytes<4>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, a->slot_mapping, a->indicators, *a); break;
+            case 2048: launch_timed((singular_tiles_kernel<8, MODE>), grid, block, tile_smem_bytes<8>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, a->slot_mapping, a->indicators, *a); break;
+            case 4096: launch_timed((singular_tiles_kernel<16, MODE>), grid, block, tile_smem_bytes<16>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, a->slot_mapping, a->indicators, *a); break;
+            case 8192: launch_timed((singular_tiles_kernel<32, MODE>), grid, block, tile_smem_bytes<32>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, a->slot_mapping, a->indicators, *a); break;
+            case 16384: launch_timed((singular_tiles_kernel<64, MODE>), grid, block, tile_smem_bytes<64>(a), s, a->tile_start, a->tile_end, (const uint16_t *)a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, stage, a->slot_mapping, a->indicators, *a); break;
             default: return SS_ERR_UNSUPPORTED;
         }
         if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;

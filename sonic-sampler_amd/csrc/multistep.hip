@@ -23,10 +23,14 @@ struct Request {
 // step = ceil(batch / 64) (INT_MAX past the end; 0 without cu_seqlens). Kernels issue it ahead of
 // their bulk loads: vector loads return in order, so behind a tile of logits it would wait for the
 // whole tile, and the request's reads that depend on it would start only then.
+__device__ __forceinline__ int request_pivot(const int32_t *cu_seqlens, int batch) {
+    if (!cu_seqlens) return 0;
+    const int p = lane_id() * ((batch + 63) >> 6);
+    return p < batch ? cu_seqlens[p] : INT_MAX;
+}
+
 __device__ __forceinline__ int request_pivot(const ss_multistep_args &a) {
-    if (!a.cu_seqlens) return 0;
-    const int p = lane_id() * ((a.batch + 63) >> 6);
-    return p < a.batch ? a.cu_seqlens[p] : INT_MAX;
+    return request_pivot(a.cu_seqlens, a.batch);
 }
 
 __device__ __forceinline__ Request resolve_request(const ss_multistep_args &a, int row, int pivot) {
@@ -100,18 +104,21 @@ __device__ __forceinline__ bool row_in_contract(const ss_multistep_args &a, cons
 template <int E, int MODE>
 __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(const uint16_t *p_logits, int64_t p_stride,
                                                                    int p_block_n, int p_vocab, int tiles,
+                                                                   const int32_t *p_cu, int p_batch,
+                                                                   const int32_t *p_slots, const uint16_t *p_ind,
                                                                    ss_multistep_args a) {
     __shared__ TileSmem<E> sm;
     const int row = blockIdx.y;
     const int tile = blockIdx.x;
-    const int pivot = request_pivot(a);
+    // the request search, the slot and the indicator start from preloaded pointers
+    const int pivot = request_pivot(p_cu, p_batch);
     u32x2 lw[E / 4];
     if (MODE != MODE_SCALAR) load_logits_vec<E>(p_logits + (int64_t)row * p_stride, tile * p_block_n, p_vocab, lw);
     const Request rq = resolve_request(a, row, pivot);
     const int step = row - rq.margin;
     if (!row_in_contract(a, rq, step)) return;
-    const int slot = a.slot_mapping ? uniform_i32(a.slot_mapping, rq.b) : rq.b;
-    const uint32_t ind = uniform_u16(a.indicators, slot);
+    const int slot = p_slots ? uniform_i32(p_slots, rq.b) : rq.b;
+    const uint32_t ind = uniform_u16(p_ind, slot);
     RowState rs = multistep_row_state(a, row, step, slot, ind);
     if (step > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         // Step s of a request sees the drafts of steps < s as extra decode history
@@ -398,11 +405,11 @@ static int launch_multistep(const ss_multistep_args *a, int tiles) {
     dim3 grid((unsigned)tiles, (unsigned)a->rows), block(SS_BLOCK);
     hipStream_t s = (hipStream_t)a->stream;
     switch (a->block_n) {
-        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
-        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
-        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
-        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
-        case 16384: launch_timed((multistep_tiles_kernel<64, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, *a); break;
+        case 1024: launch_timed((multistep_tiles_kernel<4, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, a->cu_seqlens, a->batch, a->slot_mapping, a->indicators, *a); break;
+        case 2048: launch_timed((multistep_tiles_kernel<8, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, a->cu_seqlens, a->batch, a->slot_mapping, a->indicators, *a); break;
+        case 4096: launch_timed((multistep_tiles_kernel<16, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, a->cu_seqlens, a->batch, a->slot_mapping, a->indicators, *a); break;
+        case 8192: launch_timed((multistep_tiles_kernel<32, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, a->cu_seqlens, a->batch, a->slot_mapping, a->indicators, *a); break;
+        case 16384: launch_timed((multistep_tiles_kernel<64, MODE>), grid, block, 0, s, a->tile_start, a->tile_end, a->logits, a->stride_logits, a->block_n, a->vocab_size, tiles, a->cu_seqlens, a->batch, a->slot_mapping, a->indicators, *a); break;
         default: return SS_ERR_UNSUPPORTED;
     }
     if (hipGetLastError() != hipSuccess) return SS_ERR_LAUNCH;

@@ -79,7 +79,9 @@ typedef struct ss_philox {
 /* Kernel layout of ss_fused_singular and ss_topk. TILES: a tile grid (rows x tiles) writes every tile's
  * top-128 to the scratchpad, then one workgroup per row merges and selects (two launches).
  * ROWWISE: one workgroup per row streams the row tile by tile and selects in the same launch
- * (rows of at most 16 tiles; the scratchpad is not touched). AUTO currently picks TILES. */
+ * (rows of at most 16 tiles; the scratchpad is not touched). AUTO: ss_fused_singular always takes
+ * TILES; ss_topk takes ROWWISE for at least 48 rows of 16385-32768 columns at k <= 32 and TILES
+ * otherwise. */
 typedef enum ss_strategy {
     SS_STRATEGY_AUTO = 0,
     SS_STRATEGY_TILES = 1,
@@ -191,7 +193,10 @@ int ss_fused_singular(const ss_singular_args *args);
  * lists (rows * ceil(vocab_size / block_n) * 128 * 4 bytes) go to a static device array of
  * SS_STATIC_SCRATCH_BYTES that every device the library runs on holds until the process ends.
  * A larger call fails with SS_ERR_SCRATCH_LIMIT. The call allocates nothing; the first call on a
- * device only looks up that device's copy of the array. All calls on one device share the array:
+ * device (the device of args->stream) only looks up that device's copy of the array. That lookup
+ * is not a stream operation, so the first call on a device must be made outside graph capture: a
+ * first call while args->stream is capturing fails with SS_ERR_UNSUPPORTED, and every later call
+ * on that device may be captured. All calls on one device share the array:
  * calls that overlap on one device (two streams, or two threads) race, so they must be ordered.
  * Every other argument, output and error is that of ss_fused_singular.
  * ------------------------------------------------------------------------------------------- */

@@ -97,27 +97,44 @@ def truncate(values: Tensor, st: State, bits: Tensor) -> Tensor:
 
 
 def singular(logits: Tensor, st: State, *, noise: Optional[Tensor] = None,
-             max_top_logprobs: int = 5) -> BatchResult:
+             max_top_logprobs: int = 5, bounded: str = "sort") -> BatchResult:
     """One autoregressive step over the batch (target indicators, row b at slot b, timestep 0),
     with logprobs and top-Z logprobs; ``noise`` is the [B, V] Gumbel plane (default: the state's
-    target plane at timestep 0)."""
+    target plane at timestep 0).
+
+    ``bounded`` picks the bounded top-128: ``"sort"`` (the default) is a stable descending sort,
+    ties to the lowest index as the parity contract requires (hazard H1); ``"topk"`` is the
+    reference's own ``logits.topk(k=128)`` (``core/naive.py:336``), whose order among equal values
+    torch leaves unspecified. Both select the same 128 values; ``"topk"`` is the formulation whose
+    CPU time ``bench.py`` reports as the reference's."""
 
     B = logits.size(0)
     bits = torch.tensor(st.target[:B], dtype=I64)
     x = process(logits, st, bits)
     plane = (noise if noise is not None else st.gumbel_target[:B, 0]).to(BF16)
 
-    # bounded top-128 as a stable descending sort (ties to the lowest index, hazard H1)
-    ordered, order = x.sort(dim=-1, stable=True, descending=True)
-    values = truncate(ordered[:, :MAX_K].contiguous(), st, bits)
-    indices = order[:, :MAX_K]
+    if bounded == "topk":
+
+        top, indices = x.topk(k=MAX_K, dim=-1)
+        values = truncate(top, st, bits)
+
+    elif bounded == "sort":
+
+        # bounded top-128 as a stable descending sort (ties to the lowest index, hazard H1)
+        ordered, order = x.sort(dim=-1, stable=True, descending=True)
+        values = truncate(ordered[:, :MAX_K].contiguous(), st, bits)
+        indices = order[:, :MAX_K]
+
+    else:
+
+        raise ValueError(f"unknown bounded top-128 formulation {bounded!r}")
 
     pick = (values - plane.gather(-1, indices)).argmax(dim=-1, keepdim=True)
     lse = values.to(F32).logsumexp(dim=-1, keepdim=True)
     shifted = values.to(F32) - lse
 
     greedy = (bits & GREEDY) != 0
-    tokens = torch.where(greedy, order[:, 0], indices.gather(-1, pick)[:, 0])
+    tokens = torch.where(greedy, indices[:, 0], indices.gather(-1, pick)[:, 0])
     logprobs = torch.where(greedy, torch.zeros(B), shifted.gather(-1, pick)[:, 0])
 
     limit = torch.where((bits & TOP_K_LOGPROBS) != 0, st.top_logprobs[:B].to(I64).clamp(max=max_top_logprobs), 0)

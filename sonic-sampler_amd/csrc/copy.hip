@@ -8,7 +8,8 @@
 
 namespace ss {
 
-constexpr int COPY_CHUNK = SS_BLOCK * 4 * 8;  // 16 KB of uint16 elements per workgroup
+// Elements one workgroup copies: four 16-byte (8-element) accesses per thread, 16 KB of uint16.
+constexpr int COPY_CHUNK = SS_BLOCK * 4 * 8;
 
 typedef int32_t i32x4c __attribute__((ext_vector_type(4)));
 
@@ -19,8 +20,8 @@ __global__ __launch_bounds__(SS_BLOCK) void indexed_copy_kernel(ss_indexed_copy_
     if (a.indicators && (a.indicators[slot] & 0x40u)) return;  // greedy: nothing to stage
     const uint16_t *src = a.source + slot * a.stride_source;
     uint16_t *dst = a.target + slot * a.stride_target;
-    const int64_t begin = (int64_t)blockIdx.y * (COPY_CHUNK / 2);
-    const int64_t end = min(begin + COPY_CHUNK / 2, a.cols);
+    const int64_t begin = (int64_t)blockIdx.y * COPY_CHUNK;
+    const int64_t end = min(begin + (int64_t)COPY_CHUNK, a.cols);
     if (VEC) {
         // 8 elements (16 bytes) per access; cols is a multiple of 8
         i32x4c q[4];
@@ -47,7 +48,7 @@ extern "C" int ss_indexed_copy(const ss_indexed_copy_args *a) {
     if (a->count < 0 || a->slots < 0 || a->cols < 0) return SS_ERR_INVALID_ARGUMENT;
     if (a->stride_source < a->cols || a->stride_target < a->cols) return SS_ERR_INVALID_ARGUMENT;
     if (a->count == 0 || a->cols == 0) return SS_OK;
-    const int64_t blocks = (a->cols + COPY_CHUNK / 2 - 1) / (COPY_CHUNK / 2);
+    const int64_t blocks = (a->cols + COPY_CHUNK - 1) / COPY_CHUNK;
     if (a->count > 0x7fffffff || blocks > 65535) return SS_ERR_UNSUPPORTED;
     const bool vec = ((uintptr_t)a->source % 16) == 0 && ((uintptr_t)a->target % 16) == 0 &&
                      a->stride_source % 8 == 0 && a->stride_target % 8 == 0 && a->cols % 8 == 0;

@@ -433,22 +433,43 @@ constexpr int MAX_DEVICES = 64;
 static std::atomic<uint32_t *> g_static_scratch[MAX_DEVICES];
 static std::mutex g_static_scratch_lock;
 
-// The current device's copy of `scratch`, looked up on the first call on that device (with the
-// device current, as hipGetSymbolAddress resolves the symbol for the current device).
-static uint32_t *static_scratch() {
+// The copy of `scratch` on the device that runs `stream` (the current device for the null
+// stream), looked up on the first call on that device: hipGetSymbolAddress resolves the symbol for
+// the current device, so that device is made current for the lookup and the caller's device is
+// restored. The lookup may load the code object on the device, which is not a stream operation a
+// graph can record: a first call on a device while `stream` is capturing is refused
+// (SS_ERR_UNSUPPORTED), so the first call must be made eagerly, before any capture.
+static int static_scratch(hipStream_t stream, uint32_t **out) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    if (stream) {
+        if (hipStreamGetDevice(stream, &dev) != hipSuccess) return SS_ERR_LAUNCH;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return SS_ERR_LAUNCH;
+    }
+    if (dev < 0 || dev >= MAX_DEVICES) return SS_ERR_UNSUPPORTED;
     uint32_t *p = g_static_scratch[dev].load(std::memory_order_acquire);
-    if (p) return p;
+    if (p) {
+        *out = p;
+        return SS_OK;
+    }
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) return SS_ERR_LAUNCH;
+    if (capture != hipStreamCaptureStatusNone) return SS_ERR_UNSUPPORTED;
     std::lock_guard<std::mutex> lock(g_static_scratch_lock);
     p = g_static_scratch[dev].load(std::memory_order_relaxed);
     if (!p) {
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) return SS_ERR_LAUNCH;
+        if (current != dev && hipSetDevice(dev) != hipSuccess) return SS_ERR_LAUNCH;
         void *addr = nullptr;
-        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return nullptr;
+        const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (current != dev && hipSetDevice(current) != hipSuccess) return SS_ERR_LAUNCH;
+        if (e != hipSuccess || !addr) return SS_ERR_LAUNCH;
         p = static_cast<uint32_t *>(addr);
         g_static_scratch[dev].store(p, std::memory_order_release);
     }
-    return p;
+    *out = p;
+    return SS_OK;
 }
 
 }  // namespace ss
@@ -462,8 +483,9 @@ extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
     const int64_t world = a->world_size > 1 ? a->world_size : 1;
     if ((int64_t)a->rows * world * tiles * SS_K * (int64_t)sizeof(uint32_t) > (int64_t)SS_STATIC_SCRATCH_BYTES)
         return SS_ERR_SCRATCH_LIMIT;
-    uint32_t *ptr = static_scratch();
-    if (!ptr) return SS_ERR_LAUNCH;
+    uint32_t *ptr = nullptr;
+    const int st = static_scratch((hipStream_t)a->stream, &ptr);
+    if (st != SS_OK) return st;
     // Every list entry the row stage uses is written by the tile stage of the same call (a greedy
     // row's merge samples are read but ignored), so the array needs no clearing between calls.
     ss_singular_args b = *a;

@@ -671,6 +671,10 @@ __global__ __launch_bounds__(TOPK_WIDE_THREADS) void topk_wide_kernel(const void
     }
 
     // ---- exact selection: the k-th largest key T, then every key > T and the first ties --------
+    // Every wave has read the survivor counts in sm.red before any wave passes this barrier, so
+    // the first wide_sum below cannot overwrite a count a slower wave still has to read (which
+    // could send that wave down the other branch).
+    __syncthreads();
     uint32_t key[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) key[j] = col_of(j) < V ? float_key(v[j]) : 0u;

@@ -28,7 +28,6 @@ import random as _random
 
 from contextlib import nullcontext
 from dataclasses import dataclass
-from itertools import compress
 from typing import List, Optional, Tuple
 
 import torch
@@ -78,6 +77,21 @@ def _rows(positions: Optional[List[int]], size: int) -> List[int]:
     """The rows an update touches: `positions`, or every row in order."""
 
     return list(positions) if positions else list(range(size))
+
+
+def _present(items, positions: Optional[List[int]] = None):
+    """(row, item) for every item that is not None: item j belongs to row positions[j], or to row
+    j when no positions are given (the parallel-list convention of every population call)."""
+
+    rows = positions if positions else range(len(items))
+
+    return [(row, item) for row, item in zip(rows, items) if item is not None]
+
+
+def _log_exponential_(plane: Tensor, generator: Optional[Generator]) -> None:
+    """Fills `plane` with log(Exp(1)) draws, the Gumbel noise the kernels subtract."""
+
+    plane.exponential_(1.0, generator=generator).log_()
 
 
 def _send(device_rows: Tensor, host_rows: Tensor, positions: Optional[List[int]], stream=None) -> None:
@@ -179,33 +193,40 @@ class GumbelNoise(SliceBuffer):
             layout=Layout(indices.size(0), self.layout.cols),
         )
 
+    def planes(self, row, prefill: bool, draft: bool) -> List[Tensor]:
+        """The noise one refresh of `row` redraws. At prefill a single logit row is sampled, so
+        the verifier needs timestep 0 only, and a stochastic drafter all of its timesteps. During
+        decoding a stochastic drafter's noise is redrawn (the verifier's was staged from it by
+        stage_weights just before); with a greedy drafter the verifier's own noise is."""
+
+        if not prefill:
+
+            return [self.draft[row] if draft else self.target[row]]
+
+        return [self.target[row, 0], self.draft[row]] if draft else [self.target[row, 0]]
+
     def populate(self, row, generator: Optional[Generator], prefill: bool = False, draft: bool = False):
 
-        if prefill:
+        for plane in self.planes(row, prefill, draft):
 
-            tensors = (self.target[row, 0], self.draft[row]) if draft else (self.target[row, 0],)
-
-        else:
-
-            tensors = ((self.draft if draft else self.target)[row],)
-
-        for weight in tensors:
-
-            weight.exponential_(1.0, generator=generator).log_()
+            _log_exponential_(plane, generator)
 
         return self
 
     def update(self, targets: List[Optional[Tensor]], positions: Optional[List[int]] = None, stream=None):
+        """Carried-over drafter noise ([T, V] device tensors, None to leave a row alone) replaces
+        the verifier's noise of its row (just-in-time batching, reference
+        ``core/buffer.py:121-149``)."""
 
-        if any(selectors := [t is not None for t in targets]):
+        moves = _present(targets, positions)
 
-            iterator = zip(positions, targets) if positions else enumerate(targets)
+        if moves:
 
             with (stream or nullcontext()):
 
-                for i, target in compress(iterator, selectors):
+                for row, noise in moves:
 
-                    self.target[i].copy_(target, non_blocking=True)
+                    self.target[row].copy_(noise, non_blocking=True)
 
         return self
 
@@ -275,14 +296,18 @@ class StochasticWeights(SliceBuffer):
         )
 
     def refresh(self, position, generator, prefill: bool, draft: bool) -> None:
+        """Redraws row `position` (every row when None): its Gumbel noise (GumbelNoise.planes),
+        and outside prefill its acceptance uniforms on [TINY, 1), TINY keeping log(u) finite. A
+        prefill row has nothing to verify yet."""
 
-        row = slice(None) if position is None else position
+        rows = slice(None) if position is None else position
+        self.gumbel.populate(row=rows, generator=generator, prefill=prefill, draft=draft)
 
-        self.gumbel.populate(row=row, generator=generator, prefill=prefill, draft=draft)
+        if prefill:
 
-        if not prefill:
+            return
 
-            self.uniform[row].uniform_(TINY, 1.0, generator=generator)
+        self.uniform[rows].uniform_(TINY, 1.0, generator=generator)
 
     def update(self, generator=None, selectors=None, targets=None, positions=None, prefill=False,
                stream=None, event=None) -> "StochasticWeights":
@@ -365,17 +390,17 @@ class TokenCounts(SliceBuffer):
         return self
 
     def allocate(self, encodings: List[Tensor], positions: List[int], stream=None) -> "TokenCounts":
-        """Request admission (reference ``core/buffer.py:434-457``): the prompts' histograms become
-        the context counts of `positions` and their decode counts restart at zero."""
+        """Request admission (reference ``core/buffer.py:434-457``): the prompts' histograms,
+        staged in pinned memory, become the context counts of `positions`, and the decode counts
+        of those rows restart at zero (one fill over all of them)."""
 
         self.populate(encodings, positions)
+        _send(self.context, self.pinned, positions, stream)
 
         with (stream or nullcontext()):
 
-            for i in positions:
-
-                self.context[i].copy_(self.pinned[i], non_blocking=True)
-                self.decode[i].zero_()
+            rows = torch.tensor(positions, dtype=I64).to(self.decode.device, non_blocking=True)
+            self.decode.index_fill_(0, rows, 0)
 
         return self
 
@@ -763,23 +788,29 @@ class SamplingBuffers(SliceBuffer):
         )
 
     def step_grammar(self, bitmasks, positions=None, timestep=None, stream=None, event=None):
+        """Writes grammar bitmasks (host int32 words, pinned for an asynchronous copy): bitmasks[j]
+        goes to row positions[j] (row j without positions) at `timestep`, or at every timestep when
+        `timestep` is None; None entries leave their rows alone (reference
+        ``core/buffer.py:1026-1052``, whose positional form reads bitmasks[positions[j]] and so
+        needs a full-batch list; this one follows the parallel lists its callers pass). Nothing
+        is issued, and `event` is not recorded, when every entry is None."""
 
-        if bitmasks and any(selectors := [m is not None for m in bitmasks]):
+        moves = _present(bitmasks or [], positions)
 
-            iterator = positions or range(len(bitmasks))
+        if not moves:
 
-            with (stream or nullcontext()):
+            return self
 
-                for k, i in enumerate(iterator):
+        with (stream or nullcontext()):
 
-                    if selectors[k]:
+            for row, words in moves:
 
-                        target = self.grammar[i] if timestep is None else self.grammar[i, timestep]
-                        target.copy_(bitmasks[k].view(target.dtype), non_blocking=True)
+                target = self.grammar[row] if timestep is None else self.grammar[row, timestep]
+                target.copy_(words.view(target.dtype), non_blocking=True)
 
-                if event:
+            if event:
 
-                    event.record(stream)
+                event.record(stream)
 
         return self
 

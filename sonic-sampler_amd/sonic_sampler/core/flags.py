@@ -343,26 +343,27 @@ class ScopedIndicators(SliceBuffer):
         return torch.tensor(values, dtype=torch.int32, **kwargs).to(U16)
 
     def subset(self, indices: List[int]) -> "ScopedIndicators":
+        """The (target, draft) pairs of rows `indices`, in that order, as a new instance with the
+        same timestep extent."""
 
-        return ScopedIndicators(
-            target=[self.target[i] for i in indices],
-            draft=[self.draft[i] for i in indices],
-            layout=Layout(rows=len(indices), cols=self.layout.cols),
-        )
+        pairs = [(self.target[i], self.draft[i]) for i in indices]
+
+        if not pairs:
+
+            return ScopedIndicators(target=[], draft=[], layout=Layout(rows=0, cols=self.layout.cols))
+
+        return ScopedIndicators.from_pairs(pairs, timesteps=self.layout.cols)
 
     def update(self, other: "ScopedIndicators", positions: Optional[List[int]] = None):
+        """Row j of `other` replaces row positions[j]; without positions, row j replaces row j
+        (`other` then covers the leading rows)."""
 
-        if positions:
+        rows = positions if positions else range(len(other.target))
 
-            for i, j in enumerate(positions):
+        for row, target, draft in zip(rows, other.target, other.draft):
 
-                self.target[j] = other.target[i]
-                self.draft[j] = other.draft[i]
-
-        else:
-
-            self.target[:] = other.target
-            self.draft[:] = other.draft
+            self.target[row] = target
+            self.draft[row] = draft
 
         return self
 
@@ -453,27 +454,36 @@ class Flags(SliceBuffer):
         return torch.tensor([(flag in v) for v in self.indicators.target], dtype=BOOL)
 
     def update(self, indicators: ScopedIndicators, positions: Optional[List[int]], stream=None) -> "Flags":
+        """Installs `indicators` at rows `positions` (the leading rows when None): the readable
+        lists, the pinned [B, 2] mirror, and an asynchronous copy of those rows of the mirror to
+        the device words the kernels read (on `stream` when given)."""
 
         self.indicators.update(indicators, positions)
-        values = indicators.as_tensor(host=True)
+        words = indicators.as_tensor(host=True).T  # [n, 2]: (target, draft) of each new row
+        n = words.size(0)
+        rows = list(positions) if positions else list(range(n))
+        leading = rows == list(range(n))
 
-        if positions:
+        if leading:
 
-            index = torch.tensor(positions, dtype=I64, device="cpu")
-            self.pinned.view(I16).index_copy_(0, index, values.T.view(I16))
-
-            with (stream or nullcontext()):
-
-                for i in positions:
-
-                    self.packed[i].copy_(self.pinned[i], non_blocking=True)
+            self.pinned[:n].copy_(words)
 
         else:
 
-            self.pinned.copy_(values.T)
+            index = torch.tensor(rows, dtype=I64)
+            self.pinned.view(I16).index_copy_(0, index, words.view(I16))
 
-            with (stream or nullcontext()):
+        with (stream or nullcontext()):
 
-                self.packed.copy_(self.pinned, non_blocking=True)
+            if leading:
+
+                # one strided copy covers the leading rows of both columns
+                self.packed[:n].copy_(self.pinned[:n], non_blocking=True)
+
+            else:
+
+                for row in rows:
+
+                    self.packed[row].copy_(self.pinned[row], non_blocking=True)
 
         return self

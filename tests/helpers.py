@@ -4,15 +4,12 @@ from __future__ import annotations
 
 import torch
 
+import dataclasses
+
+from types import SimpleNamespace
+
+from oracle import sampler as oracle
 from oracle.sampler import LOGPROB_FLOOR, bf16_within
-
-
-def assert_tokens(actual, expected, what: str, allow_fraction: float = 0.05):
-    """Tokens must match exactly except on rows the oracle marks knife-edge."""
-
-    mismatched = [i for i, e in enumerate(expected) if int(actual[i]) != e]
-
-    return mismatched
 
 
 def check_singular(selection, expected, *, logprobs: bool, probabilities=None, slot_mapping=None,
@@ -120,6 +117,63 @@ def check_multistep(verification, expected, cu_seqlens, *, logprobs: bool,
                     assert bf16_within(float(top_values[margin + i, z]), v, floor=LOGPROB_FLOOR), (b, i, z, float(top_values[margin + i, z]), v)
 
     return mismatched
+
+
+def expected_singular_counts(decode, expected, selection, mismatched, slot_mapping=None, prefill=False):
+    """Decode counts a singular call with ``update_counts`` must leave: the oracle's update on every
+    row that matches it, and on a knife-edge row (whose token may legitimately differ) the update
+    of the token the GPU selected. Every row's counts are compared, also in runs with knife-edge
+    rows."""
+
+    tokens = selection.tokens[:, 0].cpu()
+    chosen = [SimpleNamespace(token=int(tokens[r]) if r in mismatched else e.token)
+              for r, e in enumerate(expected)]
+
+    return oracle.apply_singular_counts(decode, chosen, slot_mapping, prefill=prefill)
+
+
+def expected_multistep_counts(decode, expected, verification, cu_seqlens, mismatched, slot_mapping=None):
+    """Decode counts a verifier call with ``update_counts`` must leave: +1 per emitted token, the
+    oracle's tokens for every request that matches it and the GPU's emitted span for a knife-edge
+    request, so no request's counts go unchecked."""
+
+    tokens = verification.tokens.reshape(-1).cpu()
+    offsets = verification.offsets.reshape(-1).cpu()
+    emitted = []
+
+    for b, e in enumerate(expected):
+
+        if b in mismatched:
+
+            m = cu_seqlens[b]
+            emitted.append(SimpleNamespace(tokens=[int(t) for t in tokens[m: m + int(offsets[b]) + 1]]))
+
+        else:
+
+            emitted.append(e)
+
+    return oracle.apply_multistep_counts(decode, emitted, slot_mapping)
+
+
+def load_into(dst, src):
+    """Copies every device tensor of a (device) SamplingBuffers from a CPU one of the same layout,
+    in place, so that a captured graph sees the new contents at the same addresses."""
+
+    from sonic_sampler.core.flags import Flags
+
+    if isinstance(dst, Flags):
+
+        dst.packed.copy_(src.packed)
+
+    elif dataclasses.is_dataclass(dst):
+
+        for f in dataclasses.fields(dst):
+
+            load_into(getattr(dst, f.name), getattr(src, f.name))
+
+    elif isinstance(dst, torch.Tensor) and dst.device.type == "cuda":
+
+        dst.copy_(src)
 
 
 def run_verifier(work, *, in_place=False, update_counts=False, logprobs=True, block_size=None,

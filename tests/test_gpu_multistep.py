@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from helpers import check_multistep, run_verifier
+from helpers import check_multistep, expected_multistep_counts, run_verifier
 from oracle import sampler as oracle
 
 pytestmark = pytest.mark.gpu
@@ -50,10 +50,8 @@ def test_config3_stochastic_varlen():
 
             assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i)
 
-    if not mismatched:
-
-        counts = oracle.apply_multistep_counts(state.decode, expected, None)
-        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
 
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
@@ -88,10 +86,9 @@ def test_random_buffers_fixed_gamma_slots(seed):
                                 probabilities=probabilities, logprobs=True, max_top_logprobs=4)
     mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
 
-    if not mismatched:
-
-        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
-        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched,
+                                       slot_mapping.tolist())
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
 
 
 def test_all_accepted_emits_bonus_from_last_step():

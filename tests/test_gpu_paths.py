@@ -12,12 +12,11 @@
   docs/slot-based.md:351-378).
 """
 
-import dataclasses
-
 import pytest
 import torch
 
-from helpers import check_multistep, check_singular, run_verifier
+from helpers import (check_multistep, check_singular, expected_multistep_counts, expected_singular_counts,
+                     load_into, run_verifier)
 from oracle import sampler as oracle
 
 pytestmark = pytest.mark.gpu
@@ -59,10 +58,8 @@ def autoregressive_case(logits, host, block, *, prefill=False, slot_mapping=None
                                logprobs=True, max_top_logprobs=5)
     mismatched, checked = check_singular(selection, expected, logprobs=True)
 
-    if not mismatched:
-
-        counts = oracle.apply_singular_counts(state.decode, expected, slots, prefill=prefill)
-        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    counts = expected_singular_counts(state.decode, expected, selection, mismatched, slots, prefill=prefill)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
 
     return checked
 
@@ -200,10 +197,9 @@ def test_scalar_path_multistep(seed):
                                 probabilities=probabilities, logprobs=True, max_top_logprobs=4)
     mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
 
-    if not mismatched:
-
-        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
-        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched,
+                                       slot_mapping.tolist())
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -300,36 +296,14 @@ def test_8192_tiles_multistep_every_processor(vocab, block):
                                 probabilities=probabilities, logprobs=True, max_top_logprobs=4)
     mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.25)
 
-    if not mismatched:
-
-        counts = oracle.apply_multistep_counts(state.decode, expected, slot_mapping.tolist())
-        assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched,
+                                       slot_mapping.tolist())
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
 
 
 # ------------------------------------------------------------------------------------------------
 # hipGraph replay
 # ------------------------------------------------------------------------------------------------
-
-def load_into(dst, src):
-    """Copies every device tensor of a (device) SamplingBuffers from a CPU one of the same layout,
-    in place, so that a captured graph sees the new contents at the same addresses."""
-
-    from sonic_sampler.core.flags import Flags
-
-    if isinstance(dst, Flags):
-
-        dst.packed.copy_(src.packed)
-
-    elif dataclasses.is_dataclass(dst):
-
-        for f in dataclasses.fields(dst):
-
-            load_into(getattr(dst, f.name), getattr(src, f.name))
-
-    elif isinstance(dst, torch.Tensor) and dst.device.type == "cuda":
-
-        dst.copy_(src)
-
 
 def singular_outputs(selection):
 
@@ -414,10 +388,8 @@ def test_graph_replay_autoregressive_config1():
                                        logprobs=True, max_top_logprobs=5)
             mismatched, _ = check_singular(captured, expected, logprobs=True)
 
-            if not mismatched:
-
-                counts = oracle.apply_singular_counts(state.decode, expected, slots.tolist(), prefill=False)
-                assert torch.equal(got[-1].cpu(), counts)
+            counts = expected_singular_counts(state.decode, expected, captured, mismatched, slots.tolist())
+            assert torch.equal(got[-1].cpu(), counts)
 
 
 def test_graph_replay_drafting_config4():

@@ -3,7 +3,7 @@
 import pytest
 import torch
 
-from helpers import check_singular
+from helpers import check_singular, expected_singular_counts
 from oracle import sampler as oracle
 
 pytestmark = pytest.mark.gpu
@@ -31,8 +31,53 @@ def test_config1_autoregressive():
     print(f"knife-edge mismatches: {mismatched}, fully checked rows: {checked}", flush=True)
     assert checked >= batch - 4
 
-    counts = oracle.apply_singular_counts(state.decode, expected, None, prefill=False)
+    counts = expected_singular_counts(state.decode, expected, selection, mismatched)
     assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def test_min_p_rounds_scores_to_bf16():
+    """The kernel's min-p test compares bf16 scores with a bf16 threshold, as the reference's
+    PyTorch path does (core/naive.py:316-326). Each row holds the logits (0, -1.203125, -4) at three
+    columns in different tiles and -60 elsewhere, under min_p = bf16(0.3): in bf16 the second
+    score (0.2275390625) equals the threshold bf16(0.30078125 * 0.7578125) and stays, while fp32
+    scores would mask it (0.227712 < 0.228112). Noise of +10 on the first column makes the kept
+    second column the selected token; a kernel with fp32 scores would select the first."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, ScopedIndicators
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import to_device
+
+    rows, vocab = 8, 16384
+    scoped = ScopedIndicators.from_params(
+        size=rows, timesteps=1, multiplicative=[1.0] * rows, frequency=[0.0] * rows,
+        presence=[0.0] * rows, biases=[{} for _ in range(rows)], temperature=[1.0] * rows,
+        top_k=[128] * rows, top_p=[1.0] * rows, min_p=[0.3] * rows, top_logprobs=[0] * rows,
+    )
+    host = SamplingBuffers.default(size=rows, timesteps=1, vocab_size=vocab, device="cpu", noise=False)
+    host.flags = Flags.from_scoped(scoped, device="cpu")
+    host.min_p.fill_(0.3)
+    assert float(host.min_p[0]) == 0.30078125
+    host.weights.gumbel.target.zero_()
+    logits = torch.full((rows, vocab), -60.0, dtype=torch.bfloat16)
+    cols = [(1000 * r + 7, 5000 + 13 * r, 16000 + r) for r in range(rows)]
+
+    for r, (c0, c1, c2) in enumerate(cols):
+
+        logits[r, c0], logits[r, c1], logits[r, c2] = 0.0, -1.203125, -4.0
+        host.weights.gumbel.target[r, 0, c0] = 10.0
+
+    buffers = to_device(host, DEV)
+    print("min-p at the bf16 rounding point", flush=True)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, block_size=2048, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    assert [int(t) for t in selection.tokens[:, 0].cpu()] == [c1 for _, c1, _ in cols]
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True)
+    assert [e.token for e in expected] == [c1 for _, c1, _ in cols]
+    check_singular(selection, expected, logprobs=True, max_knife_fraction=0.0)
 
 
 def test_config1_philox_matches_materialized_noise():

@@ -84,8 +84,10 @@ def test_signed_zeros_and_infinities():
     (32000, 1, torch.float32), (32000, 128, torch.float32), (30001, 64, torch.float32),
     (32768, 16, torch.bfloat16), (20001, 128, torch.bfloat16), (1500, 8, torch.float32)])
 def test_one_launch_rows(vocab, k, dtype):
-    """Rows of at most 32768 columns take the one-workgroup-per-row kernel: several k, a
-    vocabulary that is not a multiple of 4 (per-element loads), 64 rows."""
+    """64 rows under the automatic layout choice, several k, a vocabulary that is not a multiple of
+    4 (per-element loads). The cases with 16385-32768 columns at k <= 32 (k = 1 at 32000, k = 16 at
+    32768) take the one-workgroup-per-row kernel; the other four take the tile grid (k > 32, or
+    at most 16384 columns)."""
 
     from bench import spiked_logits
 

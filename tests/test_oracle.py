@@ -243,6 +243,26 @@ def test_min_p_hand_case():
     assert torch.isfinite(v[0]).tolist() == [True, True, False]
 
 
+def test_min_p_compares_bf16_scores():
+    """min-p compares bf16 scores with a bf16 threshold (reference core/naive.py:316-326: the
+    softmax of bf16 values is bf16, and so is min_p times its first entry). Logits (0, -1.203125,
+    -4) have probabilities 0.758397, 0.227712, 0.013891 and min_p = bf16(0.3) = 0.30078125. In
+    bf16 the scores are 0.7578125 and 0.2275390625, and the threshold bf16(0.30078125 * 0.7578125
+    = 0.227936) = 0.2275390625 equals the second score, which stays. With fp32 scores the second
+    (0.227712) falls below 0.30078125 * 0.758397 = 0.228112 and would be masked. Every rounding
+    above sits at least 0.1 bf16 ulp from a rounding boundary."""
+
+    st = tiny_state(min_p=torch.tensor([0.3]).to(BF16))
+    assert float(st.min_p[0]) == 0.30078125
+    x = torch.tensor([[0.0, -1.203125, -4.0]]).to(BF16)
+    v, knife = oracle.truncate(x.clone(), oracle.MIN_P, st, 0)
+    assert torch.isfinite(v[0]).tolist() == [True, True, False]
+    assert not knife
+    # the fp32 formulation decides the other way on the same row
+    s32 = x.float().softmax(-1)
+    assert float(s32[0, 1]) < 0.30078125 * float(s32[0, 0])
+
+
 # ------------------------------------------------------------------------------------------------
 # Selection and verification invariants
 # ------------------------------------------------------------------------------------------------
@@ -588,6 +608,24 @@ def test_batched_oracle_on_config1_rows():
     res = oracle.singular(work.logits, st, scope="target", logprobs=True, max_top_logprobs=5)
     assert got.tokens.tolist() == [r.token for r in res]
     assert got.logprobs.tolist() == [r.logprob for r in res]
+
+
+def test_batched_oracle_reference_topk_formulation():
+    """The reference's own bounded path, ``logits.topk(k=128)`` (core/naive.py:336), which the CPU
+    baseline times, selects the same 128 values per row as the stable sort; on rows whose
+    selection involves no tied value it also picks the same tokens with the same logprobs."""
+
+    import bench
+    from oracle import batch
+
+    work = bench.c1_workload(batch=8, vocab=32768)
+    st = oracle.State.from_buffers(work.buffers)
+    by_sort = batch.singular(work.logits, st, max_top_logprobs=5)
+    by_topk = batch.singular(work.logits, st, max_top_logprobs=5, bounded="topk")
+    assert by_topk.tokens.tolist() == by_sort.tokens.tolist()
+    assert by_topk.logprobs.tolist() == by_sort.logprobs.tolist()
+    with pytest.raises(ValueError):
+        batch.singular(work.logits, st, bounded="heap")
 
 
 def test_logprob_tolerance_floor():

@@ -3,7 +3,8 @@
 Both entry points are called through the C-ABI on identical inputs; every output must be
 bit-identical. The no-allocation calls run twice in a row, the second on a smaller input (fewer
 rows and tiles), so a stale candidate list left in the shared static array by the first call would
-show. A call larger than the static array must be refused with SS_ERR_SCRATCH_LIMIT.
+show. A call larger than the static array must be refused with SS_ERR_SCRATCH_LIMIT. After an eager
+call on the device, the entry point is captured in a hipGraph and replayed over new inputs.
 """
 
 import ctypes
@@ -26,15 +27,14 @@ def build_case(rows, vocab, seed):
     return host, spiked_logits(rows, vocab, seed=900 + seed)
 
 
-def run(host, logits, block, static_scratch):
-    """One autoregressive call with logprobs, top-5 and count updates on fresh device buffers."""
+def call(buffers, logits, block, static_scratch):
+    """One autoregressive call with logprobs, top-5 and count updates (no synchronization)."""
 
-    from bench import to_device
     from sonic_sampler.interface.functional import fused_singular
 
-    buffers = to_device(host, DEV)
     rep = buffers.repetition
-    selection = fused_singular(
+
+    return fused_singular(
         logits=logits.to(DEV), indicators=buffers.flags.target, max_top_logprobs=5, update_counts=True,
         return_logprobs=True, block_n=block, grammar=buffers.grammar[:, 0],
         context_counts=rep.counts.context, decode_counts=rep.counts.decode,
@@ -44,19 +44,35 @@ def run(host, logits, block, static_scratch):
         top_k_logprobs=buffers.top_logprobs, gumbel_noise=buffers.weights.gumbel.target[:, 0],
         static_scratch=static_scratch,
     )
-    torch.cuda.synchronize()
+
+
+def outputs(selection, host, rows, decode):
+    """The outputs a call defines: tokens, logprobs, the written top logprobs, decode counts."""
+
     lp = selection.logprobs
     # top logprobs are written up to the row's limit only (per-row count, bit 0x400, non-greedy)
     written = torch.zeros(lp.top_k.tokens.shape, dtype=torch.bool)
 
-    for r, ind in enumerate(host.flags.indicators.target[:logits.size(0)]):
+    for r, ind in enumerate(host.flags.indicators.target[:rows]):
 
         if int(ind) & 0x400 and not int(ind) & 0x40:
 
             written[r, :min(int(host.top_logprobs[r]), 5)] = True
 
     return [selection.tokens.cpu(), lp.selected.cpu(), lp.top_k.tokens.cpu()[written],
-            lp.top_k.logprobs.cpu()[written], rep.counts.decode.cpu()]
+            lp.top_k.logprobs.cpu()[written], decode.cpu()]
+
+
+def run(host, logits, block, static_scratch):
+    """One call on fresh device buffers, synchronized, and its outputs."""
+
+    from bench import to_device
+
+    buffers = to_device(host, DEV)
+    selection = call(buffers, logits.to(DEV), block, static_scratch)
+    torch.cuda.synchronize()
+
+    return outputs(selection, host, logits.size(0), buffers.repetition.counts.decode)
 
 
 def test_noalloc_matches_scratchpad_entry_point_on_consecutive_calls():
@@ -93,3 +109,59 @@ def test_noalloc_refuses_calls_beyond_the_static_scratch():
     print(f"oversize static-scratch call: rows={rows} tiles={tiles} (checked before any launch)", flush=True)
     assert lib.ss_fused_singular_noalloc(ctypes.byref(args)) == _native.SS_ERR_SCRATCH_LIMIT
     assert b"static scratch" in lib.ss_status_string(_native.SS_ERR_SCRATCH_LIMIT)
+
+
+def test_noalloc_captured_in_a_graph():
+    """The device's first call is eager (a first call while its stream captures is refused); then
+    the entry point is captured in a hipGraph and replayed over three input sets copied into the
+    captured tensors, with eager work and synchronization between replays. Every replay must equal
+    an eager ss_fused_singular call on the same inputs."""
+
+    from bench import to_device
+    from helpers import load_into
+
+    rows, vocab, block = 16, 32768, 4096
+    cases = [build_case(rows, vocab, seed) for seed in (21, 22, 23)]
+    want = []
+
+    for k, (host, logits) in enumerate(cases):
+
+        print(f"scratchpad entry point, input set {k}: rows={rows} V={vocab}", flush=True)
+        want.append(run(host, logits, block, static_scratch=False))
+
+    buffers = to_device(cases[0][0], DEV)
+    logits = cases[0][1].to(DEV)
+    print("eager static-scratch call before capture", flush=True)
+    call(buffers, logits, block, static_scratch=True)
+    torch.cuda.synchronize()
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    with torch.cuda.stream(side):
+
+        call(buffers, logits, block, static_scratch=True)
+
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    print("capturing the static-scratch call", flush=True)
+
+    with torch.cuda.graph(graph):
+
+        captured = call(buffers, logits, block, static_scratch=True)
+
+    for rnd, k in enumerate([0, 2, 1, 2]):
+
+        host, fresh = cases[k]
+        load_into(buffers, host)
+        logits.copy_(fresh)
+        torch.cuda.synchronize()
+        print(f"replay {rnd}: input set {k}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = outputs(captured, host, rows, buffers.repetition.counts.decode)
+
+        for name, a, b in zip(("tokens", "logprobs", "top tokens", "top logprobs", "decode counts"), got, want[k]):
+
+            assert torch.equal(a, b), f"{name} differ on replay {rnd} (input set {k})"

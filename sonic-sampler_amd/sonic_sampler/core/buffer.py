@@ -233,23 +233,19 @@ class GumbelNoise(SliceBuffer):
     def stage_weights(self, indices: Tensor, indicator: Tensor, stream=None):
         """Copies draft noise into target noise for the rows in ``indices`` whose draft indicator
         is stochastic, so verification sees the noise the drafter used (reference
-        ``core/buffer.py:151-159``, ``ops/copy.py:21-127``). On the GPU this is the library's
-        ``ss_indexed_copy`` kernel; host-resident buffers are copied with torch."""
+        ``core/buffer.py:151-159``, ``ops/copy.py:21-127``), with the library's
+        ``ss_indexed_copy`` kernel. The planes must be device-resident: there is no host path."""
+
+        if self.target.device.type != "cuda":
+
+            raise RuntimeError("stage_weights copies with the ss_indexed_copy kernel: the noise planes "
+                               f"must be on a GPU, not {self.target.device}")
+
+        from sonic_sampler import _native
 
         with (stream or nullcontext()):
 
-            if self.target.device.type == "cuda":
-
-                from sonic_sampler import _native
-
-                _native.indexed_copy(self.draft, self.target, indices, indicator)
-
-            else:
-
-                rows = indices.to(I64)
-                stochastic = (indicator.to(I32).index_select(0, rows) & int(Indicator.GREEDY)) == 0
-                keep = rows[stochastic]
-                self.target.index_copy_(0, keep, self.draft.index_select(0, keep))
+            _native.indexed_copy(self.draft, self.target, indices, indicator)
 
         return self
 
@@ -315,7 +311,10 @@ class StochasticWeights(SliceBuffer):
         refresh of ``resolve_updates`` whose target selector is set redraws its row (prefill: the
         target noise of step 0, plus the draft noise when drafting is stochastic; decode: the
         selected plane and the uniforms), then ``targets`` (device noise rows from the drafter, at
-        ``positions`` or in order) replace the target noise outside prefill."""
+        ``positions`` or in order) replace the target noise of every row that is not in prefill.
+        The reference skips ``targets`` altogether whenever ``prefill`` is a non-empty list, which
+        is how its just-in-time guide passes it; this follows the guide's per-request contract
+        (docs/just-in-time.md:174-199)."""
 
         with (stream or nullcontext()):
 
@@ -326,9 +325,14 @@ class StochasticWeights(SliceBuffer):
 
                     self.refresh(position=row, generator=rng, prefill=initial, draft=draft)
 
-            if targets and not prefill:
+            if targets:
 
-                self.gumbel.update(targets=targets, positions=positions, stream=stream)
+                # carried noise replaces the verifier's on decode rows only (a prefill row has
+                # nothing carried); `prefill` may be one flag or one per row
+                initial = prefill if isinstance(prefill, list) and prefill else [bool(prefill)] * len(targets)
+                decode = [None if first else noise for noise, first in zip(targets, initial)]
+                # already on `stream`: a torch stream context cannot be entered twice
+                self.gumbel.update(targets=decode, positions=positions)
 
             if event is not None:
 

@@ -1,6 +1,7 @@
 """The host population path of SamplingBuffers (reference core/buffer.py:166-764, 1026-1352) on
 CPU-resident buffers: request admission, per-iteration updates, weight refresh and staging."""
 
+import pytest
 import torch
 
 from sonic_sampler.core.buffer import SamplingBuffers, TokenCounts, resolve_updates
@@ -72,6 +73,22 @@ def test_update_refreshes_parameters_and_counts_in_order():
     assert torch.equal(b.weights.gumbel.target[1], torch.zeros(2, 64, dtype=BF16))   # the drafter's noise
 
 
+def test_update_takes_carried_noise_on_decode_rows_with_per_request_prefill():
+    """With ``prefill`` given per request (the just-in-time guide's form), the carried drafter noise
+    of each decode row replaces its verifier noise; a prefill row keeps what it drew."""
+
+    b = SamplingBuffers.default(size=3, timesteps=2, vocab_size=64, device="cpu")
+    counts = [(torch.zeros(64, dtype=torch.int32), torch.zeros(64, dtype=torch.int32))] * 3
+    carried = [torch.full((2, 64), -1.5, dtype=BF16), torch.full((2, 64), -2.5, dtype=BF16), None]
+    b.update(counts=counts, target_gumbel=carried, multiplicative=[1.0] * 3, frequency=[0.0] * 3,
+             presence=[0.0] * 3, biases=[None] * 3, temperature=[0.9] * 3, top_k=[50] * 3, top_p=[1.0] * 3,
+             min_p=[0.0] * 3, top_logprobs=[0] * 3, prefill=[False, True, False],
+             generator=[torch.Generator().manual_seed(i) for i in range(3)])
+    assert torch.equal(b.weights.gumbel.target[0], carried[0])
+    assert not torch.equal(b.weights.gumbel.target[1], carried[1])
+    assert bool(torch.isfinite(b.weights.gumbel.target[2].float()).all())
+
+
 def test_resolve_updates_shapes():
 
     g = torch.Generator()
@@ -90,13 +107,29 @@ def test_token_counts_populate_histograms_prompts():
     assert c.context[0].tolist()[2] == 1 and int(c.context[1].sum()) == 0
 
 
-def test_step_weights_stages_draft_noise_for_stochastic_drafters():
+def test_step_weights_redraws_noise_of_positions_on_host_buffers():
+    """Without device rows to stage from (``indices=None``) step_weights only redraws: the
+    drafter's noise of stochastic drafters, and the acceptance uniforms, of `positions` only."""
 
     b = SamplingBuffers.default(size=4, timesteps=2, vocab_size=512, device="cpu")
     admit(b, [1, 2])   # slot 1 stochastic (top-k 20, temperature), slot 2 stochastic (min-p)
     draft = b.weights.gumbel.draft.clone()
-    b.step_weights(positions=[1, 2], indices=torch.tensor([1, 2]), generator=torch.Generator().manual_seed(3))
-    # the verifier's noise of a stochastic drafter is the drafter's noise of the last iteration
-    assert torch.equal(b.weights.gumbel.target[1], draft[1])
-    # and the drafter's noise is redrawn
+    uniform = b.weights.uniform.clone()
+    b.step_weights(positions=[1], generator=torch.Generator().manual_seed(3))
     assert not torch.equal(b.weights.gumbel.draft[1], draft[1])
+    assert not torch.equal(b.weights.uniform[1], uniform[1])
+    assert torch.equal(b.weights.gumbel.draft[2], draft[2])
+    assert torch.equal(b.weights.uniform[2], uniform[2])
+
+
+def test_noise_staging_needs_device_buffers():
+    """Staging the drafter's noise is the ss_indexed_copy kernel's job: host-resident planes are
+    refused rather than copied by a host fallback."""
+
+    b = SamplingBuffers.default(size=4, timesteps=2, vocab_size=512, device="cpu")
+    admit(b, [1, 2])
+
+    with pytest.raises(RuntimeError, match="on a GPU"):
+
+        b.step_weights(positions=[1, 2], indices=torch.tensor([1, 2]), generator=torch.Generator().manual_seed(3))
+

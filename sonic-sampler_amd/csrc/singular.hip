@@ -77,13 +77,18 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t
     const uint32_t ind = uniform_u16(p_ind, slot);
     RowState rs = singular_row_state(a, row, slot, ind);
     bool sync = false;
-    if (MODE != MODE_DIRECT && stage_words > 0) {
-        const Uses u = row_uses(rs);
-        if (u.g && u.remap) {
-            stage_grammar(rs.grammar, rs.vt, grammar_words);
-            rs.glds = grammar_words;
-            sync = true;
-        }
+    const Uses u = row_uses(rs);
+    if (MODE != MODE_DIRECT && stage_words > 0 && u.g && u.remap) {
+        stage_grammar(rs.grammar, rs.vt, grammar_words);
+        rs.glds = grammar_words;
+        sync = true;
+    }
+    // the d2t targets of the tile's columns, requested while the grammar row is staged: the
+    // workgroup barrier below then waits for both rounds of loads at once
+    constexpr bool PRE = MODE == MODE_GATHER_VEC && E <= 32;
+    int32_t pre[PRE ? E : 1];
+    if constexpr (PRE) {
+        if (u.remap) load_d2t<E>(rs, tile * a.block_n, a.vocab_size, pre);
     }
     if (a.drafted_tokens && a.timestep > 0 && (ind & (IND_MULT | IND_FREQ | IND_PRES))) {
         rs.nhist = a.timestep;
@@ -91,9 +96,10 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t
             sm.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
         sync = true;
     }
+    if (rs.glds) stage_grammar_finish(rs.vt, grammar_words);
     if (sync) __syncthreads();
     Keys<E> keys;
-    prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
+    prologue_keys<E, MODE, PRE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys, pre);
     // this shard's slice of the row's [world_size, tiles, 128] lists
     uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch + (a.world_size > 1 ? a.local_rank * tiles * SS_K : 0);
     tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, scr, tile);
@@ -274,6 +280,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rowwise_kernel(ss_singular_
         if ((int)threadIdx.x < rs.nhist)
             sm.tile.hist[threadIdx.x] = a.drafted_tokens[(int64_t)row * a.stride_drafted + threadIdx.x];
     }
+    if (rs.glds) stage_grammar_finish(rs.vt, grammar_words);
     __syncthreads();
     const bool greedy = (ind & IND_GREEDY) != 0;
 #pragma unroll 1
@@ -313,10 +320,11 @@ static int staged_grammar_words(const ss_singular_args *a) {
     return (a->d2t && a->grammar && words <= SS_STAGE_MAX_WORDS) ? words : 0;
 }
 
-// Workgroup memory of a staged grammar row (stage_grammar): its quads and one quad of zeros.
+// Workgroup memory of a staged grammar row (stage_grammar): whole 64-quad blocks, at least one
+// quad of zeros after the row.
 static size_t staged_grammar_bytes(const ss_singular_args *a) {
     const int vt = a->target_vocab > 0 ? a->target_vocab : a->vocab_size;
-    return staged_grammar_words(a) ? (size_t)(stage_quads(vt) + 1) * 16 : 0;
+    return staged_grammar_words(a) ? (size_t)stage_region_quads(vt) * 16 : 0;
 }
 
 // Dynamic shared memory of singular_tiles_kernel<E>: its TileSmem, or a staged grammar row from

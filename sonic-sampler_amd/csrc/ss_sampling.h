@@ -584,10 +584,26 @@ constexpr int SS_STAGE_MAX_WORDS = 8192;
 
 __host__ __device__ __forceinline__ int stage_quads(int vt) { return (((vt + 31) >> 5) + 3) >> 2; }
 
-template <int E, bool VEC>
+// The d2t targets of a tile's E columns (GATHER_VEC layout: each 4-column chunk is one 16-byte
+// load), for callers that issue them ahead of the prologue.
+template <int E>
+__device__ __forceinline__ void load_d2t(const RowState &rs, int col0, int V, int32_t (&tcol)[E]) {
+    const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)(rs.shard + V) * 4);
+    const int lane4 = (int)threadIdx.x * 4;
+#pragma unroll
+    for (int c = 0; c < E / 4; ++c) {
+        const i32x4 t = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(m, lane4 * 4, (rs.shard + col0 + c * (SS_BLOCK * 4)) * 4, 0));
+        tcol[4 * c + 0] = t.x; tcol[4 * c + 1] = t.y; tcol[4 * c + 2] = t.z; tcol[4 * c + 3] = t.w;
+    }
+}
+
+// PRE: the d2t targets of the E columns come in `pre` (load_d2t, issued by the caller before the
+// grammar staging's barrier, so that both round trips overlap) instead of being loaded here.
+template <int E, bool VEC, bool PRE = false>
 __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, int col0, int V,
                                             const int32_t *hist, const u32x2 (&lw)[E / 4],
-                                            Keys<E> &keys) {
+                                            Keys<E> &keys, const int32_t *pre = nullptr) {
     constexpr int NCH = E / 4;
     const int lane4 = (int)threadIdx.x * 4;
     bool all_exc;
@@ -631,7 +647,10 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
         int tcol[E];
 #pragma unroll
         for (int j = 0; j < E; ++j) tcol[j] = rs.shard + col0 + tile_col(j);
-        if (u.remap) {
+        if (u.remap && PRE) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) tcol[j] = pre[j];
+        } else if (u.remap) {
             const __amdgpu_buffer_rsrc_t m = row_buffer(rs.d2t, (int64_t)(rs.shard + V) * 4);
             if (VEC) {
                 // the 4 columns of a chunk are consecutive (and V % 4 == 0): one 16-byte load
@@ -718,39 +737,49 @@ __device__ __forceinline__ void gather_keys(const RowState &rs, const Uses &u, i
                    dec, ctx, bb, bw, keys);
 }
 
+// Quads of workgroup memory a staged grammar row occupies: stage_grammar fills whole blocks of 64
+// quads (one wave's load), and the row is followed by at least one quad of zeros.
+__host__ __device__ __forceinline__ int stage_region_quads(int vt) {
+    const int quads = stage_quads(vt);
+    const int blocks = (quads + 63) >> 6;
+    return blocks * 64 > quads ? blocks * 64 : quads + 1;
+}
+
 // Copies the grammar row of a `vt`-token vocabulary (ceil(vt / 32) words) into workgroup memory
-// `dst` (16-byte aligned, 4 * (stage_quads(vt) + 1) words): one round of 16-byte loads, at most 8
-// per thread (at most SS_STAGE_MAX_WORDS words), all issued before any is stored. The bits past
-// the vocabulary in the last word are cleared, the words past it up to the next multiple of 4
-// read 0 (the load's range check) and one more quad of zeros follows, so every column at or past
-// vt clamped to 128 * stage_quads(vt) reads a clear bit. The caller synchronizes the workgroup
-// before reading `dst`.
+// `dst` (16-byte aligned, 4 * stage_region_quads(vt) words) with direct global-to-LDS loads
+// (buffer_load_dwordx4 ... lds): wave w moves quads [256 i + 64 w, 256 i + 64 w + 64) of the row
+// into the same quads of `dst` (the wave's LDS base in M0, 16 bytes per lane), for the blocks that
+// start inside the row, so the row passes through no vector registers and the loads stay in
+// flight while the wave issues its other loads. Words past the row read 0 (the load's range
+// check, dword by dword), so every quad of the last block past the row is zero. Nothing waits
+// here: each wave calls stage_grammar_finish after its own loads, and the caller synchronizes the
+// workgroup before reading `dst`.
 __device__ __forceinline__ void stage_grammar(const uint32_t *grammar, int vt, uint32_t *dst) {
     const int words = (vt + 31) >> 5;
     const __amdgpu_buffer_rsrc_t g = row_buffer(grammar, (int64_t)words * 4);
     const int quads = stage_quads(vt);
-    const int last = vt >> 5;                               // the word holding bit vt
-    const uint32_t keep = (1u << (vt & 31)) - 1u;           // its bits below vt (0: vt % 32 == 0)
-    i32x4 q[SS_STAGE_MAX_WORDS / 4 / SS_BLOCK];
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    typedef __attribute__((address_space(3))) void *lds_vp;
 #pragma unroll
     for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
-        const int w4 = (int)threadIdx.x + i * SS_BLOCK;
-        q[i] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(g, w4 * 16, 0, 0));
+        const int q0 = i * SS_BLOCK + wave * 64;  // the wave's first quad (uniform)
+        if (q0 < quads)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(g, (lds_vp)(dst + 4 * q0), 16, lane_id() * 16, q0 * 16, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < SS_STAGE_MAX_WORDS / 4 / SS_BLOCK; ++i) {
-        const int w4 = (int)threadIdx.x + i * SS_BLOCK;
-        if (w4 == last >> 2) {
-            // a word past the row (vt % 32 == 0) reads 0 already
-            const int c = last & 3;
-            q[i].x = c == 0 ? q[i].x & keep : q[i].x;
-            q[i].y = c == 1 ? q[i].y & keep : q[i].y;
-            q[i].z = c == 2 ? q[i].z & keep : q[i].z;
-            q[i].w = c == 3 ? q[i].w & keep : q[i].w;
-        }
-        if (w4 < quads) *(i32x4 *)(dst + 4 * w4) = q[i];
-    }
-    if (threadIdx.x == 0) *(i32x4 *)(dst + 4 * quads) = i32x4{0, 0, 0, 0};
+}
+
+// Completes a staged grammar row once the calling wave's loads have landed (it waits for them):
+// the wave that loaded the row's last word clears its bits past the vocabulary, and when the row
+// ends exactly on a 64-quad block, the quad of zeros after it is written. Then every column at or
+// past vt, clamped to word 4 * stage_quads(vt), reads a clear bit. All threads call, before the
+// workgroup barrier that publishes `dst`.
+__device__ __forceinline__ void stage_grammar_finish(int vt, uint32_t *dst) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's loads (into LDS too) are done
+    const int quads = stage_quads(vt);
+    const int last = vt >> 5;  // the word holding bit vt
+    if ((vt & 31) != 0 && (int)threadIdx.x == ((last >> 2) & (SS_BLOCK - 1) & ~63))
+        dst[last] &= (1u << (vt & 31)) - 1u;
+    if ((quads & 63) == 0 && threadIdx.x == 0) *(i32x4 *)(dst + 4 * quads) = i32x4{0, 0, 0, 0};
 }
 
 // Memory layouts of the prologue, fixed per launch by the host:
@@ -785,10 +814,12 @@ __device__ __forceinline__ void gather_pass(const RowState &rs, const Uses &u, i
 
 // Streams one tile of one row through the processor chain and returns the keys (0 = absent).
 // `lw` holds the tile's logits from load_logits_vec unless MODE is MODE_SCALAR.
-template <int E, int MODE>
+// PRE (GATHER_VEC, E <= 32): the d2t targets of the tile's columns come in `pre` (load_d2t).
+template <int E, int MODE, bool PRE = false>
 __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int V,
                                               const int32_t *hist, const u32x2 (&lw)[E / 4],
-                                              Keys<E> &keys) {
+                                              Keys<E> &keys, const int32_t *pre = nullptr) {
+    static_assert(!PRE || (MODE == MODE_GATHER_VEC && E <= 32), "pre-loaded d2t targets: GATHER_VEC, E <= 32");
     const Uses u = row_uses(rs);
     if constexpr (MODE == MODE_DIRECT) {
         if (!(u.g || u.rep || u.mult || u.bias)) {
@@ -838,13 +869,14 @@ __device__ __forceinline__ void prologue_keys(const RowState &rs, int col0, int 
                     for (int c = 0; c < 4; ++c) lh[c] = lw[4 * h + c];
                 }
                 Keys<16> kh;
-                gather_keys<16, MODE == MODE_GATHER_VEC>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh);
+                gather_keys<16, MODE == MODE_GATHER_VEC, PRE>(rs, u, col0 + 4 * 4 * SS_BLOCK * h, V, hist, lh, kh,
+                                                              PRE ? pre + 16 * h : nullptr);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) keys.p[8 * h + i] = kh.p[i];
             }
         }
     } else {
-        gather_keys<E, MODE == MODE_GATHER_VEC>(rs, u, col0, V, hist, lw, keys);
+        gather_keys<E, MODE == MODE_GATHER_VEC, PRE>(rs, u, col0, V, hist, lw, keys, pre);
     }
 }
 

@@ -515,3 +515,95 @@ def test_packed_keys_follow_the_order_of_the_values():
 
         both = packed_keys(lo | (hi << 16))
         assert both & 0xffff == keys[lo] and both >> 16 == keys[hi]
+
+
+# ------------------------------------------------------------------------------------------------
+# Grammar staging with direct global-to-LDS loads (stage_grammar / stage_grammar_finish)
+# ------------------------------------------------------------------------------------------------
+
+STAGE_MAX_WORDS, BLOCK = 8192, 256
+
+
+def stage_quads(vt):
+
+    return (((vt + 31) >> 5) + 3) >> 2
+
+
+def stage_region_quads(vt):
+
+    quads = stage_quads(vt)
+    blocks = (quads + 63) >> 6
+
+    return blocks * 64 if blocks * 64 > quads else quads + 1
+
+
+def emulate_staging(row_words, vt):
+    """The workgroup memory stage_grammar + stage_grammar_finish leave for a grammar row: wave w of
+    iteration i copies quads [256 i + 64 w, +64) when that block starts inside the row, lane l
+    loading row quad q0 + l through the range-checked buffer (words past the row read 0) into
+    region quad q0 + l; then the last word's bits past vt are cleared and, when the row ends on a
+    block, the quad after it is zeroed. Returns the region (None: never written) and the set of
+    written quads."""
+
+    words = (vt + 31) >> 5
+    quads = stage_quads(vt)
+    region = [None] * (4 * stage_region_quads(vt))
+    written = set()
+
+    for i in range(STAGE_MAX_WORDS // 4 // BLOCK):
+
+        for w in range(BLOCK // WAVE):
+
+            q0 = i * BLOCK + w * WAVE
+
+            if q0 >= quads:
+
+                continue
+
+            for lane in range(WAVE):
+
+                q = q0 + lane
+                written.add(q)
+
+                for k in range(4):
+
+                    word = 4 * q + k
+                    region[word] = int(row_words[word]) if word < words else 0
+
+    last = vt >> 5
+
+    if vt & 31:
+
+        owner = ((last >> 2) & (BLOCK - 1)) & ~63          # lane 0 of the wave holding that word
+        assert (last >> 2) in written and (((last >> 2) % BLOCK) // WAVE) * WAVE == owner
+        region[last] &= (1 << (vt & 31)) - 1
+
+    if quads % 64 == 0:
+
+        written.add(quads)
+        region[4 * quads: 4 * quads + 4] = [0, 0, 0, 0]
+
+    return region, written
+
+
+@pytest.mark.parametrize("vt", [1, 31, 32, 33, 127, 128, 129, 4096, 4099, 8191, 8192, 32000, 32768,
+                                65536 - 32, 65536 + 5, 131072 - 1, 200003, 262144 - 128, 262144])
+def test_direct_grammar_staging_stays_in_its_region_and_reproduces_the_row(vt):
+
+    rng = np.random.default_rng(vt)
+    words = (vt + 31) >> 5
+    row = rng.integers(0, 2 ** 32, size=words + 8, dtype=np.uint64)   # garbage past the row too
+    region, written = emulate_staging(row, vt)
+    quads = stage_quads(vt)
+    # every written quad lies inside the allocated region
+    assert max(written) < stage_region_quads(vt)
+    # every quad a lookup can reach (word index clamped to 4 * quads) was written
+    assert all(q in written for q in range(quads + 1))
+    # bit v of the staged row is bit v of the grammar for v < vt, and clear for v >= vt up to the clamp
+    for v in list(range(0, min(vt, 4096))) + list(range(max(0, vt - 4096), vt)):
+
+        assert (region[v >> 5] >> (v & 31)) & 1 == (int(row[v >> 5]) >> (v & 31)) & 1
+
+    for v in range(vt, min(128 * quads + 32, vt + 4096)):
+
+        assert (region[min(v >> 5, 4 * quads)] >> (v & 31)) & 1 == 0

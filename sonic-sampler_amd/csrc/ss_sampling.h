@@ -1047,24 +1047,41 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
         }
         return;
     }
-    // The lane's largest and second-largest key: the two largest of its even and of its odd
-    // elements with packed 16-bit max / min, then the two largest of those four.
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 a1 = {0, 0}, a2 = {0, 0};
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) {
-        const u16x2 v = __builtin_bit_cast(u16x2, keys.p[i]);
-        a2 = __builtin_elementwise_max(a2, __builtin_elementwise_min(a1, v));
-        a1 = __builtin_elementwise_max(a1, v);
-    }
-    const uint32_t m1 = max((uint32_t)a1.x, (uint32_t)a1.y);
-    const uint32_t m2 = max(min((uint32_t)a1.x, (uint32_t)a1.y), max((uint32_t)a2.x, (uint32_t)a2.y));
-    // 14 of the 16 key bits: the bound may sit up to 3 keys low, which only adds a few survivors
     uint32_t bound = 0;
+    if constexpr (E >= 64) {
+        // At 64 elements a lane its largest key alone bounds well: the bound is the largest t (to
+        // 14 of the 16 key bits) that at least 32 lane maxima reach, so the wave holds at least 32
+        // keys >= t. One packed max a pair, one ballot a bisection step.
+        u16x2 a1 = {0, 0};
 #pragma unroll
-    for (int b = 15; b >= 2; --b) {
-        const uint32_t c = bound | (1u << b);
-        if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= 32) bound = c;
+        for (int i = 0; i < E / 2; ++i) a1 = __builtin_elementwise_max(a1, __builtin_bit_cast(u16x2, keys.p[i]));
+        const uint32_t m1 = max((uint32_t)a1.x, (uint32_t)a1.y);
+#pragma unroll
+        for (int b = 15; b >= 2; --b) {
+            const uint32_t c = bound | (1u << b);
+            if (__popcll(__ballot(m1 >= c)) >= 32) bound = c;
+        }
+    } else {
+        // The lane's largest and second-largest key: the two largest of its even and of its odd
+        // elements with packed 16-bit max / min, then the two largest of those four. With few
+        // elements a lane (and on the partial last tile of a row) the second-largest keeps the
+        // bound tight enough that the survivors fit a wave's run.
+        u16x2 a1 = {0, 0}, a2 = {0, 0};
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+            const u16x2 v = __builtin_bit_cast(u16x2, keys.p[i]);
+            a2 = __builtin_elementwise_max(a2, __builtin_elementwise_min(a1, v));
+            a1 = __builtin_elementwise_max(a1, v);
+        }
+        const uint32_t m1 = max((uint32_t)a1.x, (uint32_t)a1.y);
+        const uint32_t m2 = max(min((uint32_t)a1.x, (uint32_t)a1.y), max((uint32_t)a2.x, (uint32_t)a2.y));
+        // 14 of the 16 key bits: the bound may sit up to 3 keys low, which only adds a few survivors
+#pragma unroll
+        for (int b = 15; b >= 2; --b) {
+            const uint32_t c = bound | (1u << b);
+            if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= 32) bound = c;
+        }
     }
     if (lane == 0) sm.red[wave] = bound;
     __syncthreads();

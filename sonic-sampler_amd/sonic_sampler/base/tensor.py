@@ -7,7 +7,9 @@
 
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import weakref
+
+from typing import Dict, Optional, Tuple
 
 from torch import Tensor
 
@@ -73,3 +75,37 @@ class TimeDifferentiatedTensor(PrefixContiguousTensor):
 def prefix_contiguous(tensor: Tensor) -> PrefixContiguousTensor:
 
     return tensor.as_subclass(PrefixContiguousTensor)
+
+
+# id(plane) -> (weak reference to the plane, {index: plain view})
+_PLAIN_VIEWS: Dict[int, Tuple["weakref.ref[Tensor]", Dict[object, Tensor]]] = {}
+
+
+def plain_view(plane: Tensor, column: Optional[int] = None) -> Tensor:
+    """`plane`, or `plane[:, column]`, as a plain ``torch.Tensor`` view of the same memory, built
+    once per plane object. Every operation on a tensor subclass (including reading a stride or a
+    data pointer) dispatches through Python, a few microseconds each on the host; the entry points
+    only pass the view's pointer and strides on. Entries whose plane has been freed are replaced
+    (the weak reference tells a reused id apart)."""
+
+    entry = _PLAIN_VIEWS.get(id(plane))
+
+    if entry is None or entry[0]() is not plane:
+
+        if len(_PLAIN_VIEWS) > 4096:
+
+            for key in [k for k, (ref, _) in _PLAIN_VIEWS.items() if ref() is None]:
+
+                del _PLAIN_VIEWS[key]
+
+        entry = _PLAIN_VIEWS[id(plane)] = (weakref.ref(plane), {})
+
+    views = entry[1]
+    view = views.get(column)
+
+    if view is None:
+
+        base = plane.as_subclass(Tensor) if type(plane) is not Tensor else plane
+        view = views[column] = base if column is None else base[:, column]
+
+    return view

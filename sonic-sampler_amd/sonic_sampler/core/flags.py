@@ -22,6 +22,7 @@ import torch
 from torch import Tensor
 
 from sonic_sampler.base import Layout, SliceBuffer
+from sonic_sampler.base.tensor import plain_view
 from sonic_sampler.ops import MAX_K
 
 
@@ -421,12 +422,12 @@ class Flags(SliceBuffer):
     @property
     def target(self) -> Tensor:
 
-        return self.packed[:, 0]
+        return plain_view(self.packed, 0)
 
     @property
     def draft(self) -> Tensor:
 
-        return self.packed[:, 1]
+        return plain_view(self.packed, 1)
 
     def subset(self, host_indices: List[int], device_indices: Tensor) -> "Flags":
 

@@ -10,6 +10,7 @@ import torch
 from torch import Tensor
 
 from sonic_sampler.base.sampler import Verification, DEFAULT_TOP_LOGPROBS
+from sonic_sampler.base.tensor import plain_view
 from sonic_sampler.core.buffer import SamplingBuffers
 from sonic_sampler.interface.base import TwoStageTiling, TopKStrategy
 from sonic_sampler.interface.dispatch import ThreeStageWarpConfig
@@ -132,7 +133,7 @@ class UnshardedFusedMultistep(TwoStageTiling):
             draft_probabilities=probabilities,
             slot_mapping=slot_mapping,
             cu_seqlens=cu_seqlens,
-            grammar=buffers.grammar,
+            grammar=plain_view(buffers.grammar),
             context_counts=counts.context,
             decode_counts=counts.decode,
             repetition_penalties=penalties.multiplicative,
@@ -144,8 +145,8 @@ class UnshardedFusedMultistep(TwoStageTiling):
             top_p=buffers.top_p,
             min_p=buffers.min_p,
             top_k_logprobs=buffers.top_logprobs,
-            gumbel_noise=None if philox_seed is not None else weights.gumbel.target,
-            uniform_noise=weights.uniform,
+            gumbel_noise=None if philox_seed is not None else plain_view(weights.gumbel.target),
+            uniform_noise=plain_view(weights.uniform),
             output_tokens=tokens if in_place else None,
             topk_strategy=k_strategy,
             warp_config=config,

@@ -10,6 +10,7 @@ import torch
 from torch import Tensor
 
 from sonic_sampler.base.sampler import Selection, DEFAULT_TOP_LOGPROBS
+from sonic_sampler.base.tensor import plain_view
 from sonic_sampler.core.buffer import SamplingBuffers
 from sonic_sampler.interface.base import TwoStageTiling, TopKStrategy
 from sonic_sampler.interface.dispatch import TwoStageWarpConfig
@@ -118,7 +119,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             block_n=block_n,
             scratchpad=self.scratchpad,
             slot_mapping=slot_mapping,
-            grammar=buffers.grammar[:, 0],
+            grammar=plain_view(buffers.grammar, 0),
             context_counts=counts.context,
             decode_counts=counts.decode,
             repetition_penalties=penalties.multiplicative,
@@ -130,7 +131,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             top_p=buffers.top_p,
             min_p=buffers.min_p,
             top_k_logprobs=buffers.top_logprobs,
-            gumbel_noise=None if philox_seed is not None else buffers.weights.gumbel.target[:, 0],
+            gumbel_noise=None if philox_seed is not None else plain_view(buffers.weights.gumbel.target, 0),
             topk_strategy=k_strategy,
             warp_config=config,
             philox_seed=philox_seed,
@@ -182,7 +183,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             scratchpad=self.scratchpad,
             slot_mapping=slot_mapping,
             d2t_mapping=d2t_mapping,
-            grammar=buffers.grammar[:, timestep],
+            grammar=plain_view(buffers.grammar, timestep),
             context_counts=counts.context,
             decode_counts=counts.decode,
             drafted_tokens=drafted_tokens,
@@ -195,7 +196,7 @@ class UnshardedFusedSingular(TwoStageTiling):
             top_p=buffers.top_p,
             min_p=buffers.min_p,
             top_k_logprobs=buffers.top_logprobs,
-            gumbel_noise=None if philox_seed is not None else buffers.weights.gumbel.draft[:, timestep],
+            gumbel_noise=None if philox_seed is not None else plain_view(buffers.weights.gumbel.draft, timestep),
             output_tokens=output_tokens,
             draft_probabilities=probabilities,
             topk_strategy=k_strategy,

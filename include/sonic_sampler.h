@@ -256,8 +256,9 @@ typedef struct ss_multistep_args {
     void *tile_end;
     /* 1: the caller knows that every row's indicator has SS_GREEDY (for example from its host
        copy of the indicators): the request stage takes each row's argmax from the tiles' maxima
-       itself and the row launch is skipped, one launch fewer. A row without SS_GREEDY is then
-       not served (its request's outputs are unspecified). 0: any mix of rows. */
+       itself and the row launch is skipped, one launch fewer. A request whose indicator lacks
+       SS_GREEDY is then not served: its offsets entry is set to -1 (outside 0..gamma) and no
+       other output of it is written. 0: any mix of rows. */
     int32_t all_greedy;
 } ss_multistep_args;
 

@@ -294,6 +294,12 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(const int32_t *p_c
                             : nullptr;
 
     const bool want_lp = a.return_logprobs && a.logprobs;
+    if (a.all_greedy && !greedy) {
+        // The caller's all_greedy hint is wrong for this request: no row launch left its records.
+        // It is not served, and says so: offsets -1 (outside 0..gamma), nothing else written.
+        if (lane == 0) a.offsets[rq.b] = -1;
+        return;
+    }
     int j = n - 1;
     int token;
     if (greedy && a.all_greedy) {

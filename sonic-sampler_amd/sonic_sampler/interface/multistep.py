@@ -107,7 +107,8 @@ class UnshardedFusedMultistep(TwoStageTiling):
         ``cu_seqlens`` (an addition) selects the variable-lookahead layout: ``logits`` is
         ``[sum_i (gamma_i + 1), V]`` and ``tokens`` the matching flat ``[sum_i (gamma_i + 1)]``.
         ``all_greedy`` (an addition) tells the library that every row of `buffers.flags.target` is
-        greedy, which saves a launch; rows that are not greedy are then not served.
+        greedy, which saves a launch; a request that is not greedy is then not served, and its
+        ``offsets`` entry reads -1.
         """
 
         penalties = buffers.repetition

@@ -235,6 +235,45 @@ def test_config2_all_greedy_hint():
     assert torch.all(verifier2.values[:, 0].cpu() == 0)
 
 
+def test_wrong_all_greedy_hint_marks_the_request():
+    """A request whose indicator is not greedy under the all_greedy hint is not served and says
+    so (offsets -1); the greedy requests of the same call still match the oracle."""
+
+    from bench import MultistepWorkload, spiked_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    batch, gamma, vocab = 6, 3, 16384
+    n = gamma + 1
+    logits = spiked_logits(batch * n, vocab, seed=17)
+    g = torch.Generator().manual_seed(17)
+    argmax = logits.float().argmax(-1)
+    drafted = torch.where(torch.rand(batch * n, generator=g) < 0.7, argmax,
+                          torch.randint(1, vocab, (batch * n,), generator=g)).to(torch.int32)
+    host = SamplingBuffers.default(size=batch, timesteps=n, vocab_size=vocab, device="cpu")
+    indicators = [Indicator.GREEDY] * batch
+    indicators[2] = Indicator.TEMPERATURE        # the hint is wrong for request 2
+    host.flags = Flags.from_values(batch, n, indicators, device="cpu")
+    host.top_k.copy_(torch.tensor([1, 1, 128, 1, 1, 1], dtype=torch.int32))
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=5)
+    print("wrong all_greedy hint for request 2", flush=True)
+    verification, _, _ = run_verifier(work, all_greedy=True, block_size=1024)
+
+    offsets = verification.offsets.reshape(-1).cpu().tolist()
+    assert offsets[2] == -1
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, logprobs=True)
+    tokens = verification.tokens.reshape(-1).cpu()
+
+    for b in (0, 1, 3, 4, 5):
+
+        assert offsets[b] == expected[b].offset, b
+        m = work.cu_seqlens[b]
+        assert [int(t) for t in tokens[m: m + offsets[b] + 1]] == expected[b].tokens, b
+
+
 def test_graph_replay_config2_all_greedy_hint():
     """Config 2 with the all_greedy hint captured in a hipGraph (tile and request launches only)
     and replayed over new logits, drafts and decode counts copied into the captured tensors: every

@@ -552,3 +552,167 @@ def test_just_in_time_loop_with_carried_state():
             r.draft_weights = noise
             r.decode = dec
             r.started = True
+
+
+class JitEngine:
+    """A just-in-time template with its engine-owned buffers and the per-request state carried
+    between iterations (context and decode counts, drafter noise, generator)."""
+
+    def __init__(self, pool, rows, d2t):
+
+        from sonic_sampler.core.buffer import TINY, SamplingBuffers
+        from sonic_sampler.interface import UnshardedFusedMultistep, UnshardedFusedSingular
+
+        self.template = SamplingBuffers.default(size=JIT_CAPACITY, timesteps=GAMMA + 1,
+                                                vocab_size=TARGET_VOCAB, device=DEV, noise=False)
+        # the same initial noise in every template: prefill redraws only the planes it needs
+        w = self.template.weights
+        g = torch.Generator(DEV).manual_seed(78)
+        w.gumbel.target.exponential_(1.0, generator=g).log_()
+        w.gumbel.draft.exponential_(1.0, generator=g).log_()
+        w.uniform.uniform_(TINY, 1.0, generator=g)
+        self.template.prepopulate(schedule=[rows])
+        self.active = self.template[:rows]
+        assert self.template[:rows] is self.active          # the cached slice a graph can bind to
+        self.rows, self.d2t = rows, d2t
+        self.sampler = UnshardedFusedSingular.initialize(vocab_size=JIT_VOCAB_DRAFT, batch_size=rows,
+                                                         lookahead=GAMMA, max_top_logprobs=TOP_Z, device=DEV)
+        self.verifier = UnshardedFusedMultistep.initialize(vocab_size=TARGET_VOCAB, lookahead=GAMMA,
+                                                           batch_size=rows, max_top_logprobs=TOP_Z, device=DEV)
+        self.tokens = torch.zeros(rows, GAMMA + 1, dtype=torch.int32, device=DEV)
+        self.draft_probs = torch.zeros(rows, GAMMA, TARGET_VOCAB, dtype=torch.bfloat16, device=DEV)
+        self.draft_inputs = torch.zeros(GAMMA, rows, JIT_VOCAB_DRAFT, dtype=torch.bfloat16, device=DEV)
+        self.target_inputs = torch.zeros(rows, GAMMA + 1, TARGET_VOCAB, dtype=torch.bfloat16, device=DEV)
+        self.state = {}
+
+        for j, r in enumerate(pool):
+
+            self.state[j] = SimpleNamespace(
+                context=torch.bincount(r.prompt, minlength=TARGET_VOCAB).to(torch.int32).to(DEV),
+                decode=torch.zeros(TARGET_VOCAB, dtype=torch.int32, device=DEV), draft_weights=None,
+                started=False, generator=torch.Generator(DEV).manual_seed(r.seed))
+
+    def populate(self, pool, members, iteration, copy_stream):
+
+        batch = [pool[j] for j in members]
+        st = [self.state[j] for j in members]
+        carried = [s.draft_weights if (s.started and not r.greedy_draft and r.top_k != 1) else None
+                   for r, s in zip(batch, st)]
+        copy_stream.wait_stream(torch.cuda.current_stream())
+        event = self.active.update(
+            counts=[(s.context, s.decode) for s in st], target_gumbel=carried,
+            multiplicative=[r.multiplicative for r in batch], frequency=[r.frequency for r in batch],
+            presence=[r.presence for r in batch], biases=[r.bias for r in batch],
+            temperature=[r.temperature for r in batch], top_k=[r.top_k for r in batch],
+            top_p=[r.top_p for r in batch], min_p=[r.min_p for r in batch],
+            top_logprobs=[r.top_logprobs for r in batch], prefill=[not s.started for s in st],
+            greedy_drafts=[r.greedy_draft for r in batch], bitmasks=[bitmask(r, iteration, 0) for r in batch],
+            generator=[s.generator for s in st], stream=copy_stream)
+        torch.cuda.current_stream().wait_event(event)
+
+    def draft(self, t):
+
+        return self.sampler.drafting(self.draft_inputs[t], self.active, timestep=t, tokens=self.tokens,
+                                     probabilities=self.draft_probs[:, t], d2t_mapping=self.d2t,
+                                     target_vocab=TARGET_VOCAB, in_place=True)
+
+    def verify(self):
+
+        return self.verifier(self.target_inputs, self.tokens, self.active, probabilities=self.draft_probs,
+                             update_counts=True, logprobs=True, in_place=True)
+
+    def step_grammar(self, pool, members, iteration, timestep):
+
+        self.active.step_grammar(bitmasks=[bitmask(pool[j], iteration, timestep) for j in members],
+                                 timestep=timestep)
+
+    def read_back(self, members):
+
+        weights = self.active.weights.gumbel.draft.clone()
+        decode = self.active.repetition.counts.decode.clone()
+
+        for j, noise, dec in zip(members, weights.unbind(), decode.unbind()):
+
+            s = self.state[j]
+            s.draft_weights, s.decode, s.started = noise, dec, True
+
+
+def test_just_in_time_loop_captured_in_a_graph():
+    """The just-in-time loop at one batch size captured once (reference docs/just-in-time.md:
+    289-330): the template's prefix slice is prepopulated, the gamma drafting calls and the
+    verifier are captured against that fixed `buffers[:rows]` slice, and each iteration replays the
+    graph after `update` has repopulated the slice and `step_grammar` has written the timesteps'
+    masks (both outside the graph). A second template fed the same requests runs every iteration
+    eagerly; replay and eager iteration must agree bit for bit, read-back state included, over
+    three iterations whose batches differ in membership, order and prefill."""
+
+    pool = make_requests(48, seed=3)
+    rows = 32
+    g = torch.Generator().manual_seed(13)
+    d2t = torch.randperm(TARGET_VOCAB, generator=g)[:JIT_VOCAB_DRAFT].to(torch.int32).to(DEV)
+    copy_stream = torch.cuda.Stream()
+    eager, graphed = JitEngine(pool, rows, d2t), JitEngine(pool, rows, d2t)
+    batches = [list(range(0, 32)), list(range(16, 48))[::-1], torch.randperm(48, generator=g)[:32].tolist()]
+    graph = captured = None
+
+    for it, members in enumerate(batches):
+
+        print(f"jit capture iteration {it}: {sum(not eager.state[j].started for j in members)} joining", flush=True)
+
+        for eng in (eager, graphed):
+
+            eng.populate(pool, members, it, copy_stream)
+
+            for t in range(GAMMA):
+
+                eng.draft_inputs[t].copy_(draft_logits(it, t, rows)[:, :JIT_VOCAB_DRAFT])
+
+        # eager iteration
+        eager.draft_probs.zero_()
+
+        for t in range(GAMMA):
+
+            eager.draft(t)
+            eager.step_grammar(pool, members, it, t + 1)
+
+        targets = target_logits(it, eager.tokens.cpu())
+        eager.target_inputs.copy_(targets)
+        graphed.target_inputs.copy_(targets)
+        verification = eager.verify()
+
+        # graph iteration: the masks of timesteps 1..gamma go in before the replay
+        for t in range(1, GAMMA + 1):
+
+            graphed.step_grammar(pool, members, it, t)
+
+        torch.cuda.synchronize()
+
+        if graph is None:
+
+            graph = torch.cuda.CUDAGraph()
+
+            with torch.cuda.graph(graph):
+
+                graphed.draft_probs.zero_()
+
+                for t in range(GAMMA):
+
+                    graphed.draft(t)
+
+                captured = graphed.verify()
+
+        graph.replay()
+        torch.cuda.synchronize()
+        emitted = torch.arange(GAMMA + 1, device=DEV)[None] <= verification.offsets.view(-1, 1)
+        pairs = [("tokens", eager.tokens, graphed.tokens), ("offsets", verification.offsets, captured.offsets),
+                 ("logprobs", verification.logprobs.selected[emitted], captured.logprobs.selected[emitted]),
+                 ("decode counts", eager.active.repetition.counts.decode, graphed.active.repetition.counts.decode),
+                 ("draft probabilities", eager.draft_probs, graphed.draft_probs),
+                 ("verifier noise", eager.active.weights.gumbel.target, graphed.active.weights.gumbel.target)]
+
+        for name, a, b in pairs:
+
+            assert torch.equal(a, b), f"iteration {it}: graph replay {name} differ from the eager loop"
+
+        eager.read_back(members)
+        graphed.read_back(members)

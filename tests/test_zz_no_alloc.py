@@ -4,10 +4,15 @@ Both entry points are called through the C-ABI on identical inputs; every output
 bit-identical. The no-allocation calls run twice in a row, the second on a smaller input (fewer
 rows and tiles), so a stale candidate list left in the shared static array by the first call would
 show. A call larger than the static array must be refused with SS_ERR_SCRATCH_LIMIT. After an eager
-call on the device, the entry point is captured in a hipGraph and replayed over new inputs.
+call on the device, the entry point is captured in a hipGraph and replayed over new inputs; a fresh
+process whose first call on the device comes under capture must see that call refused.
 """
 
 import ctypes
+import subprocess
+import sys
+
+from pathlib import Path
 
 import pytest
 import torch
@@ -165,3 +170,49 @@ def test_noalloc_captured_in_a_graph():
         for name, a, b in zip(("tokens", "logprobs", "top tokens", "top logprobs", "decode counts"), got, want[k]):
 
             assert torch.equal(a, b), f"{name} differ on replay {rnd} (input set {k})"
+
+
+# Run in a fresh process, so that no earlier call has looked up the device's copy of the array.
+FIRST_CALL_UNDER_CAPTURE = """
+import sys
+sys.path[:0] = %r
+import torch
+from bench import to_device
+from test_zz_no_alloc import build_case, call, outputs, DEV
+host, logits = build_case(8, 16384, 31)
+buffers = to_device(host, DEV)
+logits = logits.to(DEV)
+call(buffers, logits, 4096, static_scratch=False)
+torch.cuda.synchronize()
+print("scratchpad warm-up done", flush=True)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    try:
+        call(buffers, logits, 4096, static_scratch=True)
+        print("first call captured", flush=True)
+    except RuntimeError as e:
+        print("first call refused:", e, flush=True)
+torch.cuda.synchronize()
+want = outputs(call(to_device(host, DEV), logits, 4096, static_scratch=False), host, 8,
+               torch.zeros(1))[:4]
+eager = to_device(host, DEV)
+got = outputs(call(eager, logits, 4096, static_scratch=True), host, 8, torch.zeros(1))[:4]
+torch.cuda.synchronize()
+print("eager call after refusal equal:", all(torch.equal(a, b) for a, b in zip(got, want)), flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused():
+    """A device's first no-allocation call must be eager: made while the stream captures, it is
+    refused (status unsupported) before anything is recorded, and the next eager call works."""
+
+    root = Path(__file__).resolve().parent.parent
+    paths = [str(root), str(root / "sonic-sampler_amd"), str(root / "tests")]
+    print("fresh process: first static-scratch call under capture", flush=True)
+    out = subprocess.run([sys.executable, "-u", "-c", FIRST_CALL_UNDER_CAPTURE % paths],
+                         capture_output=True, text=True, timeout=100)
+    text = out.stdout + out.stderr
+
+    assert out.returncode == 0, text
+    assert "first call refused:" in out.stdout and "unsupported" in out.stdout.lower(), text
+    assert "eager call after refusal equal: True" in out.stdout, text

@@ -673,9 +673,10 @@ def _time_graphs(step, steps: int, sets: int) -> tuple:
     return whole_us, single_us
 
 
-def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
+def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -> dict:
     """Eager timing (launches queued back to back; per-step event pairs as a second figure) and
-    hipGraph replay timing of `step(i)`."""
+    hipGraph replay timing of `step(i)`. With `tiles`, `step(i, events)` also takes an event pair
+    that the tile kernel's own dispatch records, and a second pass times the tile kernel alone."""
 
     stream = torch.cuda.current_stream()
 
@@ -698,10 +699,32 @@ def _time_steps(step, steps: int, warmup: int, sets: int) -> dict:
     eager = [a.elapsed_time(b) * 1e3 for a, b in events]
     back_to_back = _time_back_to_back(step, steps)
     graph_us, graph_single_us = _time_graphs(step, steps, sets)
+    tile_us = None
+
+    if tiles:
+
+        from sonic_sampler import _native
+
+        tile_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                       for _ in range(steps)]
+
+        for pair in tile_events:
+
+            _native.event_pair(pair)
+
+        torch.cuda.synchronize()
+        _queue_behind_sleep(max(60.0, steps * 0.3))
+
+        for i in range(steps):
+
+            step(i, tile_events[i])
+
+        torch.cuda.synchronize()
+        tile_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
 
     return {"eager_us": back_to_back, "event_pair_us": statistics.mean(eager),
             "median_event_pair_us": statistics.median(eager), "graph_us": graph_us,
-            "graph_single_us": graph_single_us}
+            "graph_single_us": graph_single_us, "tile_us": tile_us}
 
 
 CONFIG_NAMES = {
@@ -796,14 +819,14 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
 
             staged.append((logits, tokens, buffers, probs, cu))
 
-        def step(i):
+        def step(i, tile_events=None):
 
             logits, tokens, buffers, probs, cu = staged[i % sets]
 
             # config 2's requests are all greedy, which an engine running greedy verification
             # knows: it says so, and the request stage takes the argmaxes itself
             return verifier(logits, tokens, buffers, probabilities=probs, logprobs=True, cu_seqlens=cu,
-                            philox_seed=None, all_greedy=config == 2)
+                            philox_seed=None, all_greedy=config == 2, tile_events=tile_events)
 
         rows = works[0].logits.size(0)
         algorithmic = rows * works[0].vocab * 2
@@ -816,13 +839,13 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
                                                     max_top_logprobs=5, block_size=block_n, device=device)
         staged = c4_rotation(w0, sets, device)
 
-        def step(i):
+        def step(i, tile_events=None):
 
             logits, buffers, tokens, probs, slots, d2t = staged[i % sets]
 
             return sampler.drafting(logits, buffers, timestep=w0.timestep, tokens=tokens, probabilities=probs,
                                     slot_mapping=slots, d2t_mapping=d2t, target_vocab=w0.target_vocab,
-                                    in_place=True)
+                                    in_place=True, tile_events=tile_events)
 
         words = w0.target_vocab // 32
         algorithmic = rows * w0.vocab * 2 + rows * words * 4 + w0.vocab * 4 + 2 * rows * 128 * 2
@@ -831,7 +854,7 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
 
         raise ValueError(f"unknown config {config}")
 
-    t = _time_steps(step, steps, warmup, sets)
+    t = _time_steps(step, steps, warmup, sets, tiles=config != 0)
     us = t["eager_us"]
 
     return {
@@ -859,6 +882,7 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
             "median_event_pair_us": round(t["median_event_pair_us"], 3),
             "graph_replay_us_per_step": round(t["graph_us"], 3),
             "graph_replay_single_step_us": round(t["graph_single_us"], 3),
+            "tile_kernel_us": None if t["tile_us"] is None else round(t["tile_us"], 3),
         },
     }
 

@@ -537,7 +537,7 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
     torch.cuda.synchronize()
     tile_kernel_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
 
-    graph_us, graph_single_us = _time_graphs(step, steps, sets)
+    graph_us, graph_single_us, graph_median_us = _time_graphs(step, steps, sets)
 
     algorithmic = c1_algorithmic_bytes(batch, vocab)
     tile_bytes = c1_tile_bytes(batch, vocab)
@@ -574,6 +574,7 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
             "tile_kernel_us": round(tile_kernel_us, 3),
             "graph_replay_us_per_step": round(graph_us, 3),
             "graph_replay_single_step_us": round(graph_single_us, 3),
+            "graph_replay_median_us": round(graph_median_us, 3),
             "host_us_per_eager_call": round(statistics.median(enqueue) * 1e6, 1),
         },
         "roofline": {
@@ -620,8 +621,8 @@ def _time_back_to_back(step, steps: int) -> float:
 
 def _time_graphs(step, steps: int, sets: int) -> tuple:
     """Microseconds per step replayed from hipGraphs, back to back behind a GPU sleep: (a) one
-    graph holding the steps of every input set in turn, replayed steps // sets times, and (b) one
-    graph per step. A graph launch costs about 4 us of GPU time of its own, which (b) pays on every
+    graph holding the steps of every input set in turn, replayed steps // sets times, (b) one
+    graph per step, and (c) the median of (b)'s replays timed one by one. A graph launch costs about 4 us of GPU time of its own, which (b) pays on every
     step; an engine's graph holds its whole decode step (forward pass and sampling) and pays it
     once per step whatever the sampler, so (a) is the sampler's share."""
 
@@ -670,7 +671,24 @@ def _time_graphs(step, steps: int, sets: int) -> tuple:
     whole_us = timed(rounds, lambda i: whole.replay()) / (rounds * sets)
     single_us = timed(steps, lambda i: singles[i % sets].replay()) / steps
 
-    return whole_us, single_us
+    # the measure of the baseline's plan: the median over at least 200 single-step replays, each
+    # bracketed by its own event pair (queued back to back behind a GPU sleep)
+    replays = max(200, steps)
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(replays)]
+    torch.cuda.synchronize()
+    _queue_behind_sleep(max(60.0, replays * 0.05))
+
+    for i, (a, b) in enumerate(pairs):
+
+        a.record(stream)
+        singles[i % sets].replay()
+        b.record(stream)
+
+    torch.cuda.synchronize()
+    median_us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in pairs)
+
+    return whole_us, single_us, median_us
 
 
 def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -> dict:
@@ -698,7 +716,7 @@ def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -
     torch.cuda.synchronize()
     eager = [a.elapsed_time(b) * 1e3 for a, b in events]
     back_to_back = _time_back_to_back(step, steps)
-    graph_us, graph_single_us = _time_graphs(step, steps, sets)
+    graph_us, graph_single_us, graph_median_us = _time_graphs(step, steps, sets)
     tile_us = None
 
     if tiles:
@@ -724,7 +742,7 @@ def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -
 
     return {"eager_us": back_to_back, "event_pair_us": statistics.mean(eager),
             "median_event_pair_us": statistics.median(eager), "graph_us": graph_us,
-            "graph_single_us": graph_single_us, "tile_us": tile_us}
+            "graph_single_us": graph_single_us, "graph_median_us": graph_median_us, "tile_us": tile_us}
 
 
 CONFIG_NAMES = {
@@ -882,6 +900,7 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
             "median_event_pair_us": round(t["median_event_pair_us"], 3),
             "graph_replay_us_per_step": round(t["graph_us"], 3),
             "graph_replay_single_step_us": round(t["graph_single_us"], 3),
+            "graph_replay_median_us": round(t["graph_median_us"], 3),
             "tile_kernel_us": None if t["tile_us"] is None else round(t["tile_us"], 3),
         },
     }

@@ -300,4 +300,11 @@ class TwoStageTiling:
                 config, block_size = best.warp_config, best.block_n
                 k_strategy = k_strategy or TopKStrategy.resolve(best)
 
+        # A vocabulary bucket spans many sizes, and a width tuned for its larger ones can leave a
+        # smaller vocabulary in one tile, which the kernels do not take: the width the buffers
+        # were made for (at least two tiles, checked at initialization) is used instead.
+        if cdiv(self.vocabulary.size, block_size) < 2:
+
+            block_size = self.block_n
+
         return config or TwoStageWarpConfig.default(), k_strategy or TopKStrategy(), block_size

@@ -200,6 +200,30 @@ def test_tiling_buffers():
     assert values.shape == indices.shape == (32, MAX_K)
 
 
+@pytest.mark.parametrize("vocab", [2049, 3000, 4096, 5000, 8192, 9000, 20000])
+def test_launch_width_never_leaves_a_single_tile(vocab):
+    """A vocabulary bucket's tuned widths are measured on its larger sizes; at every batch size the
+    launch width must still split the vocabulary into at least two tiles, and never into more
+    than the scratchpad holds (the top-k table tunes V = 3000 at 4 rows to 4096: the buffers'
+    2048 is used)."""
+
+    for kinds in ((None,), ("topk",)):
+
+        tiling, _, _ = TwoStageTiling.factory(vocab_size=vocab, batch_size=8, arch="gfx950", device="cpu",
+                                              kinds=kinds)
+
+        for rows in (1, 2, 4, 8, 16, 64, 256, 1024):
+
+            block_n = tiling.tuning(rows)[2]
+            tiles = -(-vocab // block_n)
+
+            assert 2 <= tiles <= tiling.vocabulary.blocks, (kinds, rows, block_n)
+
+        if vocab == 3000 and kinds == ("topk",):
+
+            assert tiling.tuning(4)[2] == tiling.block_n == 2048
+
+
 def test_single_tile_vocabulary_is_rejected():
 
     with pytest.raises(ValueError, match="greater than 1"):

@@ -899,10 +899,26 @@ __device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
 // A wave's keys as wave_survivors_masked spilled them to workgroup memory (pair i of lane l at
 // TileSmem::keys[wave][i * 64 + l]), read through a volatile pointer: every use is a fresh LDS
 // read, so the rare exact cut keeps no copy of the keys in registers and does not set the tile
-// kernels' register allocation (at E = 32 it would hold 92 VGPRs instead of 57).
+// kernels' register allocation (at E = 32 it would hold 92 VGPRs instead of 57). The pointer is
+// in the LDS address space: through a generic one each read is a flat load that waits for all of
+// the wave's memory operations (s_waitcnt vmcnt(0)), one full round trip per key pair.
+typedef const volatile __attribute__((address_space(3))) uint32_t *lds_cvu32p;
+
 struct SpilledKeys {
-    const volatile uint32_t *p;
+    lds_cvu32p p;
     __device__ __forceinline__ uint32_t pair(int i) const { return p[i * 64]; }
+    // this lane's count of keys >= t in the high half and of keys > t in the low half (each at
+    // most E, so a workgroup sum of them keeps the halves apart)
+    template <int E>
+    __device__ __forceinline__ uint32_t count_at(uint32_t t) const {
+        uint32_t n = 0;
+#pragma unroll 4
+        for (int i = 0; i < E / 2; ++i) {
+            const uint32_t w = pair(i), a = w & 0xffffu, b = w >> 16;
+            n += (a >= t ? 0x10000u : 0u) + (a > t ? 1u : 0u) + (b >= t ? 0x10000u : 0u) + (b > t ? 1u : 0u);
+        }
+        return n;
+    }
     // count of this lane's keys k with pred(k)
     template <int E, class Pred>
     __device__ __forceinline__ uint32_t count(Pred pred) const {
@@ -1108,9 +1124,9 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
         // Exact cut, from the spilled keys. T is the 128th key: usually the bound itself (ties at
         // lo, e.g. the -inf of grammar-masked elements), which one pair of counts confirms;
         // otherwise bisection.
-        const SpilledKeys sk{sm.keys[wave] + lane};
-        const uint32_t above_lo = block_count(sk.count<E>([&](uint32_t k) { return k > lo; }), sm.red);
-        const uint32_t from_lo = block_count(sk.count<E>([&](uint32_t k) { return k >= lo; }), sm.red);
+        const SpilledKeys sk{(lds_cvu32p)(sm.keys[wave] + lane)};
+        const uint32_t at_lo = block_count(sk.count_at<E>(lo), sm.red);
+        const uint32_t above_lo = at_lo & 0xffffu, from_lo = at_lo >> 16;
         uint32_t above;  // keys > T
         if (lo != 0 && above_lo < (uint32_t)SS_K && from_lo >= (uint32_t)SS_K) {
             T = lo;
@@ -1132,8 +1148,11 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
         const uint32_t need = (uint32_t)SS_K - above;
         uint64_t tie_keep = 0;
         uint32_t before = 0;
+        // `before` (ties in earlier chunks) is a workgroup total, so every thread leaves the loop
+        // together once `need` ties are ranked: with many ties (the -inf of a grammar that admits
+        // few tokens) that is usually after the first chunk, and later chunks keep none
 #pragma unroll 1
-        for (int c = 0; c < E / 4; ++c) {
+        for (int c = 0; c < E / 4 && before < need; ++c) {
             const uint32_t w0 = sk.pair(2 * c), w1 = sk.pair(2 * c + 1);
             const uint32_t k4[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
             uint32_t eq[1] = {(uint32_t)(k4[0] == T) + (k4[1] == T) + (k4[2] == T) + (k4[3] == T)}, tot[1];

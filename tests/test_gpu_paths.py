@@ -302,6 +302,77 @@ def test_8192_tiles_multistep_every_processor(vocab, block):
 
 
 # ------------------------------------------------------------------------------------------------
+# Sparse grammars: fewer admitted tokens than a tile's 128 candidates, so every tile's top-128 ends
+# in ties at the -inf of the masked tokens and every tile takes the exact cut
+# ------------------------------------------------------------------------------------------------
+
+def sparse_grammar(host, vocab, allowed, seed):
+    """Each (slot, timestep) grammar row of `host` admits `allowed` random tokens."""
+
+    g = torch.Generator().manual_seed(seed)
+    slots, steps, words = host.grammar.shape
+    bits = torch.zeros(slots * steps, words * 32, dtype=torch.bool)
+
+    for r in range(slots * steps):
+
+        bits[r, torch.randperm(vocab, generator=g)[:allowed]] = True
+
+    packed = (bits.view(-1, words, 32).to(torch.int64) << torch.arange(32, dtype=torch.int64)).sum(-1)
+    host.grammar.view(torch.int32).copy_((packed - ((packed >> 31) << 32)).to(torch.int32).view(slots, steps, words))
+
+
+@pytest.mark.parametrize("allowed,block", [(40, 4096), (3, 4096), (40, 16384), (3, 2048)])
+def test_sparse_grammar_autoregressive(allowed, block):
+    """Config-1 rows with every processor on and a grammar admitting 40 or 3 tokens: the sampled
+    token is admitted, and with 3 admitted the top-5 logprobs end in -inf entries at the lowest
+    masked columns, which only an exact tie rule at the cut gets right."""
+
+    from bench import spiked_logits
+
+    rows, vocab = 24, 128256
+    print(f"sparse grammar, autoregressive: allowed={allowed} block={block}", flush=True)
+    host = random_host(rows, 1, vocab, 60 + allowed, EVERY_PROCESSOR)
+    sparse_grammar(host, vocab, allowed, seed=61 + allowed)
+    logits = spiked_logits(rows, vocab, seed=62 + allowed).to(DEV)
+    assert autoregressive_case(logits, host, block) >= rows - 1
+
+
+@pytest.mark.parametrize("allowed", [40, 3])
+def test_sparse_grammar_multistep(allowed):
+
+    from bench import MultistepWorkload, spiked_logits
+
+    slots, batch, gamma, vocab = 8, 4, 3, 128256
+    n = gamma + 1
+    g = torch.Generator().manual_seed(allowed)
+    host = random_host(slots, n, vocab, 70 + allowed, EVERY_PROCESSOR, max_top_logprobs=4)
+    sparse_grammar(host, vocab, allowed, seed=71 + allowed)
+    logits = spiked_logits(batch * n, vocab, seed=72 + allowed)
+    drafted = torch.randint(1, vocab, (batch * n,), generator=g).to(torch.int32)
+    probabilities = torch.softmax(torch.randn(slots, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print(f"sparse grammar, multistep: allowed={allowed}", flush=True)
+    verification, buffers, verifier = run_verifier(work, update_counts=True, block_size=16384)
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, probabilities=probabilities,
+                                logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.25)
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[work.cu_seqlens[b] + i], idx), (b, i)
+
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+# ------------------------------------------------------------------------------------------------
 # hipGraph replay
 # ------------------------------------------------------------------------------------------------
 

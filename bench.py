@@ -972,6 +972,83 @@ def run_indexed_copy(steps: int, warmup: int) -> dict:
     }
 
 
+def run_sparse_grammar(admitted: list, steps: int, warmup: int) -> dict:
+    """Config 1's shape (B=64, V=128256 bf16) with a grammar mask as the rows' only processor,
+    admitting `n` random tokens per row for each n of `admitted` (0: every token): below 128
+    admitted tokens in a 4096-column tile, its top-128 ends in -inf ties, the case constrained
+    decoding meets. Per n: the tile kernel (its own dispatch events, mean of `steps`) and the
+    step (event pair around `steps` eager steps back to back). One input set, not rotated (17 MB
+    of logits and grammar words fit the MALL): the figures compare admitted counts with each other
+    and with the unconstrained row, not with the HBM roofline."""
+
+    from sonic_sampler import _native
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    rows, vocab = 64, 128256
+    dev = torch.device("cuda:0")
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, device=dev)
+    results = {}
+
+    for n in admitted:
+
+        g = torch.Generator("cpu").manual_seed(5)
+        logits = spiked_logits(rows, vocab, 5).to(dev)
+        host = SamplingBuffers.default(size=rows, timesteps=1, vocab_size=vocab, device="cpu", noise=False)
+        host.flags = Flags.from_values(rows, 1, Indicator.GRAMMAR, Indicator.GRAMMAR, device="cpu")
+        host.weights.gumbel.target.exponential_(1.0, generator=g).log_()
+        words = (vocab + 31) // 32
+        bits = torch.zeros(rows, words * 32, dtype=torch.bool)
+
+        for r in range(rows):
+
+            bits[r, torch.randperm(vocab, generator=g)[: n or vocab]] = True
+
+        packed = (bits.view(rows, words, 32).to(torch.int64) << torch.arange(32, dtype=torch.int64)).sum(-1)
+        host.grammar.view(torch.int32)[:, 0] = (packed - ((packed >> 31) << 32)).to(torch.int32)
+        buffers = to_device(host, dev)
+        step = lambda events=None: sampler.autoregressive(logits, buffers, tile_events=events)  # noqa: E731
+
+        for _ in range(warmup):
+
+            step()
+
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+
+        for pair in pairs:
+
+            _native.event_pair(pair)
+
+        torch.cuda.synchronize()
+
+        for pair in pairs:
+
+            step(pair)
+
+        torch.cuda.synchronize()
+        tile_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in pairs)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+
+        for _ in range(steps):
+
+            step()
+
+        end.record()
+        torch.cuda.synchronize()
+        results[str(n or vocab)] = {"tile_kernel_us": round(tile_us, 3),
+                                    "us_per_step": round(start.elapsed_time(end) * 1e3 / steps, 3)}
+
+    return {
+        "metric": "config-1-shaped decode step with a sparse grammar: tile kernel and step us", "value": None,
+        "unit": "us", "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False, "dtype": "bf16",
+        "data": "synthetic (spiked N(0,3^2) logits, random admitted tokens per row)",
+        "config": {"workload": "UnshardedFusedSingular.autoregressive B=64 V=128256 bf16, grammar only",
+                   "admitted_tokens_per_row": results},
+    }
+
+
 def main(argv=None) -> int:
 
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -986,6 +1063,8 @@ def main(argv=None) -> int:
                         help="read Gumbel noise from the buffers instead of the Philox stream")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a 1 GiB device copy (PMC counter calibration)")
+    parser.add_argument("--sparse-grammar", type=str, default=None, metavar="N,N,...",
+                        help="time config 1's shape under grammars admitting N tokens per row (0: all)")
     parser.add_argument("--indexed-copy", action="store_true",
                         help="time the noise-staging copy (ss_indexed_copy) instead of a sampling config")
     parser.add_argument("--config", type=int, default=1, choices=[0, 1, 2, 3, 4],
@@ -1006,6 +1085,13 @@ def main(argv=None) -> int:
               "shards by batch with no exchange, so N GPUs run N independent copies)", file=sys.stderr)
 
         return 2
+
+    if args.sparse_grammar:
+
+        admitted = [int(n) for n in args.sparse_grammar.split(",")]
+        print(json.dumps(run_sparse_grammar(admitted, args.steps, args.warmup)), flush=True)
+
+        return 0
 
     if args.indexed_copy:
 

@@ -129,7 +129,8 @@ __global__ __launch_bounds__(SS_BLOCK) void multistep_tiles_kernel(const uint16_
     }
     Keys<E> keys;
     prologue_keys<E, MODE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys);
-    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile);
+    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, a.scratch + (int64_t)row * a.stride_scratch, tile,
+                  min(a.block_n, a.vocab_size - tile * a.block_n));
 }
 
 // Row stage: grid rows; merge -> truncation -> fp32 log_softmax into values / indices [row, 128]

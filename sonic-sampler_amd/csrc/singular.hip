@@ -102,7 +102,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_tiles_kernel(const uint16_t
     prologue_keys<E, MODE, PRE>(rs, tile * a.block_n, a.vocab_size, sm.hist, lw, keys, pre);
     // this shard's slice of the row's [world_size, tiles, 128] lists
     uint32_t *scr = a.scratch + (int64_t)row * a.stride_scratch + (a.world_size > 1 ? a.local_rank * tiles * SS_K : 0);
-    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, scr, tile);
+    tile_stage<E>(sm, (ind & IND_GREEDY) != 0, keys, scr, tile, min(a.block_n, a.vocab_size - tile * a.block_n));
 }
 
 // Greedy row (wave 0): the argmax over the tiles' maxima, d2t remap, count update, outputs.
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(SS_BLOCK) void singular_rowwise_kernel(ss_singular_
             load_logits_vec<E>(lrow, (t + 1) * a.block_n, a.vocab_size, nx);
         Keys<E> keys;
         prologue_keys<E, MODE>(rs, t * a.block_n, a.vocab_size, sm.tile.hist, lw, keys);
-        tile_stage<E>(sm.tile, greedy, keys, sm.lists, t);
+        tile_stage<E>(sm.tile, greedy, keys, sm.lists, t, min(a.block_n, a.vocab_size - t * a.block_n));
         // the next tile reuses the tile stage's memory, and the lists feed the row stage
         __syncthreads();
         if (MODE != MODE_SCALAR) {

@@ -197,6 +197,9 @@ __device__ __forceinline__ float div_bf16(float x, const Divisor &v) {
 
 // Order-preserving 16-bit key (key16) of a bf16-exact float: 0x8000 plus the signed magnitude
 // of its top 16 bits (negation by xor with the sign mask and subtraction of it).
+// Key of bf16 -inf (key_of and packed_keys): every finite or +inf value has a larger one.
+constexpr uint32_t KEY_NEG_INF = 0x0080;
+
 __device__ __forceinline__ uint32_t key_of(float x) {
     const uint32_t u = __float_as_uint(x);
     const uint32_t s = (uint32_t)((int32_t)u >> 31);
@@ -1043,7 +1046,7 @@ __device__ __forceinline__ uint32_t wave_survivors_masked(TileSmem<E> &sm, const
 // can exceed 128.
 template <int E>
 __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const Keys<E> &keys,
-                                           uint32_t *scr, int tile) {
+                                           uint32_t *scr, int tile, int valid) {
     const int lane = lane_id();
     const int wave = (int)threadIdx.x >> 6;
     if (greedy) {
@@ -1099,9 +1102,19 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
             if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= 32) bound = c;
         }
     }
+    // A wave with fewer than 32 keys above -inf among its lanes' largest ones (few tokens admitted
+    // by a grammar, or few valid columns on a row's partial last tile) keeps every key above -inf
+    // instead: its bound would otherwise drag the tile's down to -inf, and every other wave's
+    // masked elements would then survive. The tile then holds at least 128 survivors only if the
+    // waves' counts add up to it, which the check after the survivor pass makes. A tile of fewer
+    // than 128 valid columns (`valid`) keeps the plain bounds: all of its columns survive.
+    if (bound <= KEY_NEG_INF && valid >= SS_K) bound = KEY_NEG_INF + 1;
     if (lane == 0) sm.red[wave] = bound;
     __syncthreads();
     const uint32_t lo = min(min(sm.red[0], sm.red[1]), min(sm.red[2], sm.red[3]));
+    // bounds are multiples of 4 but for a floored one, so lo shows whether one was floored; only
+    // then can the survivors of a tile of 128 valid columns or more add up to fewer than 128
+    const bool floored = lo == KEY_NEG_INF + 1;
     uint32_t T = lo ? lo - 1 : 0u;  // key 0 (absent) never survives
     const uint32_t cnt = wave_survivors_masked<E>(sm, keys, T);
     if (cnt <= 64) {
@@ -1120,18 +1133,47 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
     }
     if (lane == 0) sm.cnt[wave] = cnt;
     __syncthreads();
-    if (max(max(sm.cnt[0], sm.cnt[1]), max(sm.cnt[2], sm.cnt[3])) > (uint32_t)SS_K) {
+    const uint32_t n0 = sm.cnt[0], n1 = sm.cnt[1], n2 = sm.cnt[2], n3 = sm.cnt[3];
+    bool exact = max(max(n0, n1), max(n2, n3)) > (uint32_t)SS_K;
+    // Fewer than 128 survivors, all of the keys above -inf: the tile's first 128 are those and
+    // then its first 128 - survivors -inf keys in column order. When the tile's first 256 columns
+    // (wave 0's elements 0-3, whose keys the survivor pass spilled) hold that many, wave 0 appends
+    // them to the merged survivors (`fill`); otherwise the exact cut runs. Every wave counts them
+    // from the spill, so the decision is the same in all of them without another barrier.
+    bool fill = false;
+    uint32_t survivors = 0;
+    if (__builtin_expect(floored, 0)) {
+        survivors = n0 + n1 + n2 + n3;
+        if (survivors < (uint32_t)SS_K) {
+            const uint32_t w0 = sm.keys[0][lane], w1 = sm.keys[0][64 + lane];
+            const uint32_t k4[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
+            uint32_t lead = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lead += (uint32_t)__popcll(__ballot(k4[i] == KEY_NEG_INF));
+            fill = lead >= (uint32_t)SS_K - survivors;
+            exact = !fill;
+        }
+    }
+    if (__builtin_expect(exact, 0)) {
         // Exact cut, from the spilled keys. T is the 128th key: usually the bound itself (ties at
-        // lo, e.g. the -inf of grammar-masked elements), which one pair of counts confirms;
-        // otherwise bisection.
+        // lo), or, when a wave's bound was floored, the -inf key (the tile holds fewer than 128
+        // keys above -inf: ties at the -inf of grammar-masked elements); one pair of counts
+        // confirms a candidate. Otherwise bisection.
         const SpilledKeys sk{(lds_cvu32p)(sm.keys[wave] + lane)};
-        const uint32_t at_lo = block_count(sk.count_at<E>(lo), sm.red);
-        const uint32_t above_lo = at_lo & 0xffffu, from_lo = at_lo >> 16;
-        uint32_t above;  // keys > T
-        if (lo != 0 && above_lo < (uint32_t)SS_K && from_lo >= (uint32_t)SS_K) {
-            T = lo;
-            above = above_lo;
-        } else {
+        uint32_t above = 0;  // keys > T
+        bool found = false;
+        const bool few = floored && n0 + n1 + n2 + n3 < (uint32_t)SS_K;
+#pragma unroll 1
+        for (int i = 0; i < (floored ? 2 : 1) && !found; ++i) {
+            const uint32_t cand = floored && (few == (i == 0)) ? KEY_NEG_INF : lo;
+            const uint32_t at = block_count(sk.count_at<E>(cand), sm.red);
+            if ((at & 0xffffu) < (uint32_t)SS_K && (at >> 16) >= (uint32_t)SS_K) {
+                T = cand;
+                above = at & 0xffffu;
+                found = true;
+            }
+        }
+        if (!found) {
             uint32_t t = 0;  // the largest t with at least 128 keys >= t
 #pragma unroll 1
             for (int b = 15; b >= 0; --b) {
@@ -1186,6 +1228,28 @@ __device__ __forceinline__ void tile_stage(TileSmem<E> &sm, bool greedy, const K
         uint32_t c1 = max(sm.run2[0][2 * lane + 1], sm.run2[1][126 - 2 * lane]);
         wave_bitonic128_desc<128>(c0, c1);
         *(uint2 *)(scr + tile * SS_K + 2 * lane) = make_uint2(c0, c1);
+        if (__builtin_expect(fill, 0)) {
+            // The merged survivors took positions 0 .. survivors - 1 and zeros the rest; the -inf
+            // key of column c = 4 * lane + i (c < 256) with rank r among them overwrites position
+            // survivors + r while r < 128 - survivors. Its keys come from the survivor pass's
+            // spill (nothing has written over them since). The list's store, which other lanes
+            // of the wave made to the same positions, completes before these issue (vmcnt(0)).
+            const uint32_t need = (uint32_t)SS_K - survivors;
+            const uint32_t w0 = sm.keys[0][lane], w1 = sm.keys[0][64 + lane];
+            const uint32_t k4[4] = {w0 & 0xffffu, w0 >> 16, w1 & 0xffffu, w1 >> 16};
+            uint32_t r = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r += mbcnt64(__ballot(k4[i] == KEY_NEG_INF));
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (k4[i] == KEY_NEG_INF) {
+                    if (r < need)
+                        scr[tile * SS_K + survivors + r] = (KEY_NEG_INF << 16) | (0xffffu - (uint32_t)(4 * lane + i));
+                    ++r;
+                }
+            }
+        }
     }
 }
 

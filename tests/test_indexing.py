@@ -607,3 +607,127 @@ def test_direct_grammar_staging_stays_in_its_region_and_reproduces_the_row(vt):
     for v in range(vt, min(128 * quads + 32, vt + 4096)):
 
         assert (region[min(v >> 5, 4 * quads)] >> (v & 31)) & 1 == 0
+
+
+# ------------------------------------------------------------------------------------------------
+# tile_stage's decisions (wave bounds, the floor at -inf, survivors, the exact cut's candidates)
+# ------------------------------------------------------------------------------------------------
+
+KEY_NEG_INF = 0x0080   # key of bf16 -inf; -NaN keys lie below it, absent elements are 0
+
+
+def tile_stage_emulation(keys, E, valid):
+    """The tile's candidate list as tile_stage builds it, restated step by step: `keys` is the
+    tile's 256 * E keys by column (0 past `valid`). Returns the list's (key, column) entries in
+    descending order and the path ("bounds", "fill" or "exact")."""
+
+    block = len(keys)
+    col = lambda t, j: (j >> 2) * 1024 + 4 * t + (j & 3)  # noqa: E731
+    per_thread = [[int(keys[col(t, j)]) for j in range(E)] for t in range(256)]
+    bounds = []
+
+    for w in range(4):
+
+        lanes = per_thread[64 * w: 64 * w + 64]
+        m1 = [max(v) for v in lanes]
+        m2 = [sorted(v)[-2] for v in lanes]
+        bound = 0
+
+        for b in range(15, 1, -1):
+
+            c = bound | (1 << b)
+            n = sum(x >= c for x in m1) + (0 if E >= 64 else sum(x >= c for x in m2))
+            bound = c if n >= 32 else bound
+
+        if bound <= KEY_NEG_INF and valid >= SS_K:
+
+            bound = KEY_NEG_INF + 1
+
+        bounds.append(bound)
+
+    lo = min(bounds)
+    t0 = lo - 1 if lo else 0
+    cnt = [sum(k > t0 for v in per_thread[64 * w: 64 * w + 64] for k in v) for w in range(4)]
+    floored = lo == KEY_NEG_INF + 1
+    few = floored and sum(cnt) < SS_K
+    everything = sorted(((int(k), c) for c, k in enumerate(keys)), key=lambda e: (-e[0], e[1]))
+    lead = [c for c in range(256) if keys[c] == KEY_NEG_INF]   # wave 0's elements 0-3
+
+    if few and len(lead) >= SS_K - sum(cnt):
+
+        # wave 0 appends the first -inf keys of the first 256 columns to the merged survivors
+        survivors = [e for e in everything if e[0] > t0]
+        return survivors + [(KEY_NEG_INF, c) for c in lead[: SS_K - len(survivors)]], "fill"
+
+    if max(cnt) > SS_K or few:
+
+        # the candidates (lo, and -inf when floored) and the bisection all find the 128th key
+        T = 0
+        for b in range(15, -1, -1):
+
+            c = T | (1 << b)
+            T = c if sum(int(k) >= c for k in keys) >= SS_K else T
+
+        above = [e for e in everything if e[0] > T]
+        ties = [e for e in everything if e[0] == T][: SS_K - len(above)]
+        return sorted(above + ties, key=lambda e: (-e[0], e[1])), "exact"
+
+    survivors = [e for e in everything if e[0] > t0]
+    return survivors[:SS_K], "bounds"
+
+
+def tile_cases():
+
+    rng = np.random.default_rng(11)
+
+    for E in (16, 32, 64):
+
+        block = 256 * E
+
+        for valid in (block, block - 1, 1280 if E == 16 else block // 3, 200, 127, 100, 1):
+
+            for admitted in (None, 3, 60, 127, 128, 200, 700):
+
+                keys = rng.integers(0x6000, 0xA000, block)
+                if admitted is not None:
+
+                    keys[:] = KEY_NEG_INF
+                    keys[rng.choice(valid, min(admitted, valid), replace=False)] = rng.integers(0x7000, 0x9000, min(admitted, valid))
+
+                keys[valid:] = 0
+                yield E, valid, admitted, keys
+
+        # -NaN keys below -inf, and a wave with all of its admitted tokens
+        keys = np.full(block, KEY_NEG_INF)
+        keys[rng.choice(block, 50, replace=False)] = 0x40
+        keys[: 64 * 4] = rng.integers(0x8000, 0x8100, 256)
+        yield E, block, "nan", keys
+
+
+@pytest.mark.parametrize("E,valid,admitted,keys", list(tile_cases()),
+                         ids=lambda x: str(x) if not isinstance(x, np.ndarray) else "")
+def test_tile_stage_keeps_the_exact_top_128(E, valid, admitted, keys):
+    """With the bound floored above -inf, every path of the tile stage (bounds with enough
+    survivors, the exact cut after too few or too many) yields the tile's exact first 128 by
+    (key desc, column asc) among its valid columns; absent columns (key 0) never enter."""
+
+    got, path = tile_stage_emulation(keys, E, valid)
+    exact = sorted(((int(k), c) for c, k in enumerate(keys) if k > 0), key=lambda e: (-e[0], e[1]))[:SS_K]
+
+    assert got == exact, (E, valid, admitted, path)
+
+
+def test_tile_stage_paths():
+    """Sparse admissions with full tiles take the bounds path when the tile holds 128 or more
+    tokens and the wave-0 fill when it holds fewer; tiles of fewer than 128 valid columns never
+    take the exact cut."""
+
+    paths = {}
+
+    for E, valid, admitted, keys in tile_cases():
+
+        paths[(E, valid, admitted)] = tile_stage_emulation(keys, E, valid)[1]
+
+    assert paths[(16, 4096, 200)] == "bounds" and paths[(16, 4096, 700)] == "bounds"
+    assert paths[(16, 4096, 60)] == "fill" and paths[(64, 16384, 3)] == "fill"
+    assert all(p == "bounds" for (E, valid, _), p in paths.items() if valid < SS_K)

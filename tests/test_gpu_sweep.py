@@ -8,6 +8,9 @@ tile of a chosen width
 tokens inside one window) and a value distribution (spiked normal logits, a few distinct values so
 that most keys tie, or one value everywhere). Every row runs every processor.
 
+The bounded top-k sweep draws its own shapes (up to 128 tiles, k of 1-128, bf16 and fp32, and
+row counts that take the one-workgroup-per-row launch) and compares values and indices bit for bit.
+
 The multistep verifier's per-row top-128 ids are compared with the oracle's exactly: they are the
 first 128 of the stable descending order of the processed row, so every path of the tile stage
 (lower bounds, the floored bound of masked waves and its fill, the exact cut with its ties, tiles
@@ -192,3 +195,81 @@ def test_sweep_drafting_d2t(block, vocab, grammar, values, seed):
                                max_top_logprobs=5)
     check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=slot_mapping)
     assert torch.equal(dev_tokens[:, t].cpu(), selection.tokens[:, 0].cpu())
+
+
+def topk_cases(count: int, seed: int):
+    """(block, vocab, rows, k, dtype, values, seed) of each bounded top-k case."""
+
+    rng = random.Random(seed)
+    cases = []
+
+    for n in range(count):
+
+        block = rng.choice([1024, 2048, 4096, 8192, 16384])
+        tiles = rng.randint(2, min(128, 131072 // block))
+        last = rng.choice([block, 1, 3, 64, 127, 128, 129, rng.randrange(1, block)])
+        vocab = (tiles - 1) * block + last
+        # 48 and 64 rows of 16385-32768 columns at k <= 32 take the one-workgroup-per-row launch
+        rows = rng.choice([1, 5, 12, 48, 64]) if 16384 < vocab <= 32768 else rng.choice([1, 5, 12])
+        k = 1 << rng.randint(0, 7)
+        dtype = rng.choice(["bf16", "f32"])
+        values = rng.choice(["spiked", "few", "flat", "cluster", "specials"])
+        cases.append((block, vocab, rows, k, dtype, values, seed * 100 + n))
+
+    return cases
+
+
+TOPK_CASES = topk_cases(48, 11)
+
+
+@pytest.mark.parametrize("block,vocab,rows,k,dtype,values,seed", TOPK_CASES)
+def test_sweep_bounded_topk(block, vocab, rows, k, dtype, values, seed):
+    """Bit-exact values and indices of `UnshardedBoundedTopK` against the stable-sort oracle.
+    "cluster" raises 1-300 values inside one 512-column window (one tile holds the whole top-k, or
+    two); "specials" mixes +-0 and +-inf into spiked rows."""
+
+    from bench import spiked_logits
+    from oracle.topk import topk as oracle_topk
+    from sonic_sampler.interface import UnshardedBoundedTopK
+
+    dt = torch.float32 if dtype == "f32" else BF16
+    g = torch.Generator().manual_seed(seed)
+    print(f"sweep top-k: block={block} V={vocab} rows={rows} k={k} {dtype} values={values} seed={seed}",
+          flush=True)
+
+    if values == "few":
+
+        logits = torch.randint(-3, 4, (rows, vocab), generator=g).to(dt)
+
+    elif values == "flat":
+
+        logits = torch.full((rows, vocab), -1.25, dtype=dt)
+
+    else:
+
+        logits = spiked_logits(rows, vocab, seed, dtype=dt)
+
+        for r in range(rows):
+
+            if values == "cluster":
+
+                n = int(torch.randint(1, 301, (1,), generator=g))
+                start = int(torch.randint(0, max(1, vocab - 512), (1,), generator=g))
+                cols = start + torch.randperm(min(512, vocab - start), generator=g)[:n]
+                logits[r, cols] = (40.0 + torch.randint(0, 4, (len(cols),), generator=g).float()).to(dt)
+
+            elif values == "specials":
+
+                for v in (0.0, -0.0, float("inf"), float("-inf")):
+
+                    cols = torch.randperm(vocab, generator=g)[:int(torch.randint(0, 40, (1,), generator=g))]
+                    logits[r, cols] = v
+
+    topk = UnshardedBoundedTopK.initialize(vocab_size=vocab, batch_size=rows, k=k, block_size=block, device=DEV)
+    got_v, got_i = topk(logits.to(DEV))
+    torch.cuda.synchronize()
+    ev, ei = oracle_topk(logits, k)
+    view = torch.int16 if dt == BF16 else torch.int32
+
+    assert torch.equal(got_i.cpu(), ei), (got_i.cpu()[:2, :8], ei[:2, :8])
+    assert torch.equal(got_v.cpu().view(view), ev.view(view))

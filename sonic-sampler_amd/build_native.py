@@ -27,8 +27,6 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Wall",
-    "-Wno-unused-function",
-    "-Wno-unused-variable",
     # no packed fp32 VALU instructions (v_pk_{add,mul,fma}_f32) anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # kernarg preload: the leading scalar arguments of a kernel (up to 16 dwords) arrive in SGPRs

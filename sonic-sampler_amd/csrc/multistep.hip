@@ -289,10 +289,6 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(const int32_t *p_c
     const int32_t *drafted = a.drafted_tokens + rq.margin;
     const float *vals = a.values + (int64_t)rq.margin * SS_K;
     const int32_t *idxs = a.indices + (int64_t)rq.margin * SS_K;
-    const bool svgd = (ind & IND_SVGD) || !a.draft_probabilities;
-    const uint16_t *q = a.draft_probabilities
-                            ? a.draft_probabilities + (int64_t)slot * a.probs_stride_slot
-                            : nullptr;
 
     const bool want_lp = a.return_logprobs && a.logprobs;
     if (a.all_greedy && !greedy) {

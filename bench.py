@@ -719,6 +719,18 @@ def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -
     graph_us, graph_single_us, graph_median_us = _time_graphs(step, steps, sets)
     tile_us = None
 
+    # host cost of one eager call, the GPU idle at its start
+    enqueue = []
+
+    for i in range(min(steps, 50)):
+
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step(i)
+        enqueue.append(time.perf_counter() - t0)
+
+    torch.cuda.synchronize()
+
     if tiles:
 
         from sonic_sampler import _native
@@ -742,7 +754,8 @@ def _time_steps(step, steps: int, warmup: int, sets: int, tiles: bool = False) -
 
     return {"eager_us": back_to_back, "event_pair_us": statistics.mean(eager),
             "median_event_pair_us": statistics.median(eager), "graph_us": graph_us,
-            "graph_single_us": graph_single_us, "graph_median_us": graph_median_us, "tile_us": tile_us}
+            "graph_single_us": graph_single_us, "graph_median_us": graph_median_us, "tile_us": tile_us,
+            "host_us": statistics.median(enqueue) * 1e6}
 
 
 CONFIG_NAMES = {
@@ -902,6 +915,7 @@ def run_config(config: int, steps: int, warmup: int, sets: Optional[int] = None,
             "graph_replay_single_step_us": round(t["graph_single_us"], 3),
             "graph_replay_median_us": round(t["graph_median_us"], 3),
             "tile_kernel_us": None if t["tile_us"] is None else round(t["tile_us"], 3),
+            "host_us_per_eager_call": round(t["host_us"], 1),
         },
     }
 

@@ -44,13 +44,13 @@ class TopTargets:
         return None
 
     @classmethod
-    def empty_varlen(cls, num_tokens: int, targets: int) -> Optional["TopTargets"]:
+    def empty_varlen(cls, num_tokens: int, targets: int, device=None) -> Optional["TopTargets"]:
 
         if targets > 0:
 
             return cls(
-                tokens=torch.empty(num_tokens, targets, dtype=I32),
-                logprobs=torch.empty(num_tokens, targets, dtype=BF16),
+                tokens=torch.empty(num_tokens, targets, dtype=I32, device=device),
+                logprobs=torch.empty(num_tokens, targets, dtype=BF16, device=device),
             )
 
         return None
@@ -76,11 +76,11 @@ class LogProbabilities:
         return cls(selected=selected, top_k=TopTargets.empty_blocked(batch_size, top_k, timesteps, device=device))
 
     @classmethod
-    def empty_varlen(cls, num_tokens: int, top_k: int = 0) -> "LogProbabilities":
+    def empty_varlen(cls, num_tokens: int, top_k: int = 0, device=None) -> "LogProbabilities":
 
-        selected = torch.empty(num_tokens, dtype=BF16)
+        selected = torch.empty(num_tokens, dtype=BF16, device=device)
 
-        return cls(selected=selected, top_k=TopTargets.empty_varlen(num_tokens, top_k))
+        return cls(selected=selected, top_k=TopTargets.empty_varlen(num_tokens, top_k, device=device))
 
 
 @dataclass(eq=False)
@@ -157,19 +157,17 @@ class Verification:
     ) -> "Verification":
 
         buffer = None
+        device = tokens.device
+        offsets = tokens.new_empty(batch_size, 1, dtype=I32)
 
-        with torch.device(tokens.device):
+        if logprobs:
 
-            offsets = tokens.new_empty(batch_size, 1, dtype=I32)
+            if varlen:
 
-            if logprobs:
+                buffer = LogProbabilities.empty_varlen(tokens.size(0), top_k=top_logprobs, device=device)
 
-                if varlen:
+            else:
 
-                    buffer = LogProbabilities.empty_varlen(tokens.size(0), top_k=top_logprobs)
+                buffer = LogProbabilities.empty_blocked(batch_size, timesteps, top_k=top_logprobs, device=device)
 
-                else:
-
-                    buffer = LogProbabilities.empty_blocked(batch_size, timesteps, top_k=top_logprobs)
-
-            return cls(tokens=tokens, offsets=offsets, logprobs=buffer)
+        return cls(tokens=tokens, offsets=offsets, logprobs=buffer)

@@ -72,15 +72,6 @@ def unit_stride(name: str, tensor: Optional[Tensor]) -> None:
         raise ValueError(f"`{name}` must be contiguous along its last dimension")
 
 
-def philox(seed: Optional[int], offset: int) -> _native.Philox:
-
-    if seed is None:
-
-        return _native.Philox(0, 0, 0)
-
-    return _native.Philox(seed & 0xFFFFFFFFFFFFFFFF, offset & 0xFFFFFFFF, 1)
-
-
 def fresh_seed() -> int:
     """A seed drawn from torch's default CPU generator (fresh noise for a call without noise)."""
 

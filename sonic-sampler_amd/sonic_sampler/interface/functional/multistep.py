@@ -17,7 +17,6 @@ stores their exponentials); ``indices`` the matching token ids.
 
 from __future__ import annotations
 
-import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -33,7 +32,6 @@ from sonic_sampler.interface.functional.base import (
     I32,
     collapse_2d,
     fresh_seed,
-    philox,
     resolve_scratchpad,
     unit_stride,
     validate_block,
@@ -44,6 +42,9 @@ from sonic_sampler.ops.base import MAX_K
 
 FP32 = torch.float32
 TINY: float = torch.finfo(BF16).tiny
+
+MULTISTEP_ARGS = _native.Packer(_native.MultistepArgs)
+MULTISTEP_FIELDS = MULTISTEP_ARGS.fields
 
 
 def resolve_batch_vocab(logits: Tensor, cu_seqlens: Optional[Tensor], lookahead: Optional[int]):
@@ -250,49 +251,40 @@ def fused_multistep(
             top_values = collapse_2d(verification.logprobs.top_k.logprobs)
             top_tokens = collapse_2d(verification.logprobs.top_k.tokens)
 
-    p = _native.ptr
+    a = _native.addr
     s = _native.stride0
 
     def step_stride(t: Optional[Tensor]) -> int:
 
         return 0 if t is None else (t.stride(1) if t.dim() >= 3 else 0)
 
-    use_noise = philox_seed is None
+    philox_on = philox_seed is not None
+    tile_start, tile_end = _native.event_pair(tile_events)
 
-    args = _native.MultistepArgs(
-        logits=p(flat_logits), stride_logits=flat_logits.stride(0), rows=rows, batch=batch_size,
-        vocab_size=vocab_size, block_n=block_n, lookahead=gamma,
-        max_top_logprobs=max_top_logprobs if top_values is not None else 0,
-        update_counts=int(update_counts), return_logprobs=int(token_logprobs is not None),
-        cu_seqlens=p(cu_seqlens), indicators=p(indicators), slot_mapping=p(slot_mapping),
-        drafted_tokens=p(drafted_tokens),
-        grammar=p(grammar), grammar_stride_slot=s(grammar), grammar_stride_step=step_stride(grammar),
-        context_counts=p(context_counts), stride_context=s(context_counts),
-        decode_counts=p(decode_counts), stride_decode=s(decode_counts),
-        repetition=p(repetition_penalties), frequency=p(frequency_penalties),
-        presence=p(presence_penalties),
-        logit_bias=p(logit_bias), stride_bias=s(logit_bias),
-        temperature=p(temperature), top_k=p(top_k), top_p=p(top_p), min_p=p(min_p),
-        top_logprobs=p(top_k_logprobs),
-        draft_probabilities=p(draft_probabilities), probs_stride_slot=s(draft_probabilities),
-        probs_stride_step=step_stride(draft_probabilities),
-        uniform=p(uniform_weights), stride_uniform=s(uniform_weights),
-        gumbel=p(gumbel_noise) if use_noise else None,
-        gumbel_stride_slot=s(gumbel_noise) if use_noise else 0,
-        gumbel_stride_step=step_stride(gumbel_noise) if use_noise else 0,
-        philox=philox(philox_seed, philox_offset),
-        out_tokens=p(tokens), offsets=p(verification.offsets), logprobs=p(token_logprobs),
-        top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
-        values=p(values_buffer), indices=p(indices_buffer),
-        scratch=p(bitpacked), stride_scratch=bitpacked.stride(0),
-        stream=_native.stream_of(logits),
+    # ss_multistep_args, field by field in declaration order (MULTISTEP_FIELDS names them).
+    # all_greedy: the caller vouches that every row is greedy, so each request's argmax is taken in
+    # the request stage and the row launch is skipped. A hint, never inferred here: a captured graph
+    # replays whatever was decided at capture while the indicators may change in place between
+    # replays.
+    packed = MULTISTEP_ARGS.pack(
+        a(flat_logits), flat_logits.stride(0), rows, batch_size, vocab_size, block_n, gamma,
+        max_top_logprobs if top_values is not None else 0, int(update_counts), int(token_logprobs is not None),
+        a(cu_seqlens), a(indicators), a(slot_mapping), a(drafted_tokens),
+        a(grammar), s(grammar), step_stride(grammar),
+        a(context_counts), s(context_counts), a(decode_counts), s(decode_counts),
+        a(repetition_penalties), a(frequency_penalties), a(presence_penalties), a(logit_bias), s(logit_bias),
+        a(temperature), a(top_k), a(top_p), a(min_p), a(top_k_logprobs),
+        a(draft_probabilities), s(draft_probabilities), step_stride(draft_probabilities),
+        a(uniform_weights), s(uniform_weights),
+        0 if philox_on else a(gumbel_noise), 0 if philox_on else s(gumbel_noise),
+        0 if philox_on else step_stride(gumbel_noise),
+        philox_seed & 0xFFFFFFFFFFFFFFFF if philox_on else 0, philox_offset & 0xFFFFFFFF if philox_on else 0,
+        int(philox_on),
+        a(tokens), a(verification.offsets), a(token_logprobs), a(top_values), a(top_tokens), s(top_values),
+        a(values_buffer), a(indices_buffer), a(bitpacked), bitpacked.stride(0), _native.stream_of(logits),
+        tile_start or 0, tile_end or 0, int(bool(all_greedy)),
     )
-    args.tile_start, args.tile_end = _native.event_pair(tile_events)
-    # The caller vouches that every row is greedy: each request's argmax is taken in the request
-    # stage and the row launch is skipped. A hint, never inferred here: a captured graph replays
-    # whatever was decided at capture while the indicators may change in place between replays.
-    args.all_greedy = int(bool(all_greedy))
 
-    _native.check(_native.load().ss_fused_multistep(ctypes.byref(args)), "ss_fused_multistep")
+    _native.check(_native.packed_entry("ss_fused_multistep")(packed), "ss_fused_multistep")
 
     return verification

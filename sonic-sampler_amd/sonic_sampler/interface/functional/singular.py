@@ -31,7 +31,6 @@ Additions to the reference's keywords (all optional):
 
 from __future__ import annotations
 
-import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -46,7 +45,6 @@ from sonic_sampler.interface.functional.base import (
     BF16,
     I32,
     fresh_seed,
-    philox,
     unit_stride,
     validate_block,
     validate_count_update,
@@ -58,6 +56,9 @@ KERNEL_LAYOUTS = {None: _native.STRATEGY_AUTO, "tiles": _native.STRATEGY_TILES,
                   "rowwise": _native.STRATEGY_ROWWISE}
 
 STAGES = {None: 0, "tiles": _native.STAGE_TILES, "rows": _native.STAGE_ROWS}
+
+SINGULAR_ARGS = _native.Packer(_native.SingularArgs)
+SINGULAR_FIELDS = SINGULAR_ARGS.fields
 
 
 def resolve_tokens(buffer: Optional[Tensor], batch_size: int, source: Tensor) -> Tensor:
@@ -234,43 +235,34 @@ def fused_singular(
         history = timestep if timestep is not None else min(lookahead, drafted_tokens.size(1))
         history = max(0, min(history, drafted_tokens.size(1)))
 
-    p = _native.ptr
+    a = _native.addr
     s = _native.stride0
+    philox_on = philox_seed is not None
+    tile_start, tile_end = _native.event_pair(tile_events)
 
-    args = _native.SingularArgs(
-        logits=p(logits), stride_logits=logits.stride(0), rows=batch_size,
-        vocab_size=vocab_size,
-        target_vocab=target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size),
-        block_n=block_n, lookahead=lookahead, timestep=history,
-        max_top_logprobs=max_top_logprobs if top_values is not None else 0,
-        is_prefill=int(is_prefill), update_counts=int(update_counts),
-        return_logprobs=int(token_logprobs is not None),
-        return_probabilities=int(probabilities is not None), strategy=KERNEL_LAYOUTS[kernel_layout],
-        indicators=p(indicators), slot_mapping=p(slot_mapping), d2t=p(d2t_mapping),
-        grammar=p(grammar), stride_grammar=s(grammar),
-        context_counts=p(context_counts), stride_context=s(context_counts),
-        decode_counts=p(decode_counts), stride_decode=s(decode_counts),
-        drafted_tokens=p(drafted_tokens) if history else None, stride_drafted=s(drafted_tokens),
-        repetition=p(repetition_penalties), frequency=p(frequency_penalties),
-        presence=p(presence_penalties),
-        logit_bias=p(logit_bias), stride_bias=s(logit_bias),
-        temperature=p(temperature), top_k=p(top_k), top_p=p(top_p), min_p=p(min_p),
-        top_logprobs=p(top_k_logprobs),
-        gumbel=p(gumbel_noise) if philox_seed is None else None,
-        stride_gumbel=s(gumbel_noise) if philox_seed is None else 0,
-        philox=philox(philox_seed, philox_offset), philox_step=philox_step, stages=STAGES[stage],
-        tokens=p(final_tokens), stride_tokens=final_tokens.stride(0),
-        logprobs=p(token_logprobs), stride_logprobs=s(token_logprobs),
-        top_values=p(top_values), top_tokens=p(top_tokens), stride_top=s(top_values),
-        probabilities=p(probabilities), stride_probabilities=s(probabilities),
-        scratch=p(bitpacked), stride_scratch=s(bitpacked),
-        stream=_native.stream_of(logits),
+    # ss_singular_args, field by field in declaration order (SINGULAR_FIELDS names them)
+    packed = SINGULAR_ARGS.pack(
+        a(logits), logits.stride(0), batch_size, vocab_size,
+        target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size),
+        block_n, lookahead, history, max_top_logprobs if top_values is not None else 0,
+        int(is_prefill), int(update_counts), int(token_logprobs is not None), int(probabilities is not None),
+        KERNEL_LAYOUTS[kernel_layout],
+        a(indicators), a(slot_mapping), a(d2t_mapping),
+        a(grammar), s(grammar), a(context_counts), s(context_counts), a(decode_counts), s(decode_counts),
+        a(drafted_tokens) if history else 0, s(drafted_tokens),
+        a(repetition_penalties), a(frequency_penalties), a(presence_penalties),
+        a(logit_bias), s(logit_bias),
+        a(temperature), a(top_k), a(top_p), a(min_p), a(top_k_logprobs),
+        0 if philox_on else a(gumbel_noise), 0 if philox_on else s(gumbel_noise),
+        philox_seed & 0xFFFFFFFFFFFFFFFF if philox_on else 0, philox_offset & 0xFFFFFFFF if philox_on else 0,
+        int(philox_on), philox_step, STAGES[stage],
+        a(final_tokens), final_tokens.stride(0), a(token_logprobs), s(token_logprobs),
+        a(top_values), a(top_tokens), s(top_values), a(probabilities), s(probabilities),
+        a(bitpacked), s(bitpacked), _native.stream_of(logits),
+        tile_start or 0, tile_end or 0, world_size, local_rank, shard_size, 0,
     )
-    args.tile_start, args.tile_end = _native.event_pair(tile_events)
-    args.world_size, args.local_rank, args.shard_size = world_size, local_rank, shard_size
 
-    lib = _native.load()
     entry = "ss_fused_singular_noalloc" if static_scratch else "ss_fused_singular"
-    _native.check(getattr(lib, entry)(ctypes.byref(args)), entry)
+    _native.check(_native.packed_entry(entry)(packed), entry)
 
     return selection

@@ -382,6 +382,37 @@ def singular_outputs(selection):
     return [t.clone() for t in (selection.tokens, lp.selected, lp.top_k.tokens, lp.top_k.logprobs)]
 
 
+def test_eager_calls_run_on_the_current_stream():
+    """A call made under a side stream launches on it: the logits are written on that stream
+    behind a GPU sleep, so a launch on any other stream would read the zeros they replace."""
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    rows, vocab = 8, 16384
+    host = random_host(rows, 1, vocab, 81, EVERY_PROCESSOR)
+    logits = spiked_logits(rows, vocab, seed=82)
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=5,
+                                                block_size=4096, device=DEV)
+    buffers = to_device(host, DEV)
+    source = logits.to(DEV)
+    target = torch.zeros_like(source)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    print("eager call under a side stream", flush=True)
+
+    with torch.cuda.stream(side):
+
+        torch.cuda._sleep(20_000_000)
+        target.copy_(source)
+        selection = sampler.autoregressive(target, buffers, logprobs=True)
+
+    side.synchronize()
+    expected = oracle.singular(logits, oracle.State.from_buffers(host), scope="target", logprobs=True,
+                               max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=True)
+
+
 def test_graph_replay_autoregressive_config1():
 
     from bench import c1_workload, to_device

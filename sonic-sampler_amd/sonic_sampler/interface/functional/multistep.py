@@ -44,7 +44,6 @@ FP32 = torch.float32
 TINY: float = torch.finfo(BF16).tiny
 
 MULTISTEP_ARGS = _native.Packer(_native.MultistepArgs)
-MULTISTEP_FIELDS = MULTISTEP_ARGS.fields
 
 
 def resolve_batch_vocab(logits: Tensor, cu_seqlens: Optional[Tensor], lookahead: Optional[int]):
@@ -261,7 +260,7 @@ def fused_multistep(
     philox_on = philox_seed is not None
     tile_start, tile_end = _native.event_pair(tile_events)
 
-    # ss_multistep_args, field by field in declaration order (MULTISTEP_FIELDS names them).
+    # ss_multistep_args, field by field in declaration order (MULTISTEP_ARGS.fields names them).
     # all_greedy: the caller vouches that every row is greedy, so each request's argmax is taken in
     # the request stage and the row launch is skipped. A hint, never inferred here: a captured graph
     # replays whatever was decided at capture while the indicators may change in place between

@@ -58,7 +58,6 @@ KERNEL_LAYOUTS = {None: _native.STRATEGY_AUTO, "tiles": _native.STRATEGY_TILES,
 STAGES = {None: 0, "tiles": _native.STAGE_TILES, "rows": _native.STAGE_ROWS}
 
 SINGULAR_ARGS = _native.Packer(_native.SingularArgs)
-SINGULAR_FIELDS = SINGULAR_ARGS.fields
 
 
 def resolve_tokens(buffer: Optional[Tensor], batch_size: int, source: Tensor) -> Tensor:
@@ -240,7 +239,7 @@ def fused_singular(
     philox_on = philox_seed is not None
     tile_start, tile_end = _native.event_pair(tile_events)
 
-    # ss_singular_args, field by field in declaration order (SINGULAR_FIELDS names them)
+    # ss_singular_args, field by field in declaration order (SINGULAR_ARGS.fields names them)
     packed = SINGULAR_ARGS.pack(
         a(logits), logits.stride(0), batch_size, vocab_size,
         target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size),

@@ -13,7 +13,6 @@ mislays rows when ``k < 128``; the dense view is what that layout encodes.)
 
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass
 from typing import Optional, Tuple
 
@@ -31,6 +30,8 @@ from sonic_sampler.ops.base import MAX_K
 BF16 = torch.bfloat16
 FP32 = torch.float32
 I32 = torch.int32
+
+TOPK_ARGS = _native.Packer(_native.TopKArgs)
 
 
 @dataclass(eq=False, kw_only=True)
@@ -161,15 +162,14 @@ class UnshardedBoundedTopK(TwoStageTiling):
             scratch, values = self.scratchpad, self.values
             dtype = _native.SS_DTYPE_BF16
 
-        args = _native.TopKArgs(
-            logits=flat.data_ptr(), stride_logits=flat.stride(0), dtype=dtype, rows=n_rows,
-            vocab_size=flat.size(-1), k=self.k, block_n=block_n, strategy=0,
-            scratch=scratch.data_ptr(), stride_scratch=scratch.stride(0),
-            values=values.data_ptr(),
-            indices=self.indices.data_ptr(), stream=_native.stream_of(flat),
+        # ss_topk_args, field by field in declaration order (TOPK_ARGS.fields names them)
+        packed = TOPK_ARGS.pack(
+            flat.data_ptr(), flat.stride(0), dtype, n_rows, flat.size(-1), self.k, block_n, 0,
+            scratch.data_ptr(), scratch.stride(0), values.data_ptr(), self.indices.data_ptr(),
+            _native.stream_of(flat),
         )
 
-        _native.check(_native.load().ss_topk(ctypes.byref(args)), "ss_topk")
+        _native.check(_native.packed_entry("ss_topk")(packed), "ss_topk")
 
         k = self.k
         dense_values = values.view(-1)[: n_rows * k].view(n_rows, k)

@@ -1,7 +1,8 @@
 """The packed argument structs of the eager call path (CPU).
 
-``fused_singular`` and ``fused_multistep`` hand the library their argument structs as bytes
-packed positionally (``_native.Packer``) instead of ctypes structs built by keyword. These tests
+``fused_singular``, ``fused_multistep`` and ``UnshardedBoundedTopK`` hand the library their
+argument structs as bytes packed positionally (``_native.Packer``) instead of ctypes structs built
+by keyword. These tests
 pin that path two ways: the packer's layout against ctypes' own for every argument struct, and the
 bytes each driver packs against a struct built field by field by name from the same tensors, for
 calls that set every field a caller can reach. The packed entry point is also called into the
@@ -326,3 +327,24 @@ def test_fused_multistep_packs_every_field_by_name(name, captured):
     assert entry == "ss_fused_multistep"
     assert packed == bytes(_native.MultistepArgs(**multistep_expected(call, ver, t, flat, scratch, values, indices,
                                                                      uniform)))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bounded_topk_packs_every_field_by_name(dtype, captured):
+
+    from sonic_sampler.interface import UnshardedBoundedTopK
+
+    topk = UnshardedBoundedTopK.initialize(vocab_size=9000, batch_size=6, k=32, block_size=2048, device="cpu")
+    logits = torch.randn(2, 3, 9000).to(dtype)
+    topk(logits)
+
+    wide = dtype == torch.float32
+    scratch, values = topk._wide_buffers(6) if wide else (topk.scratchpad, topk.values)
+    flat = logits.flatten(0, 1)
+    expected = _native.TopKArgs(
+        logits=flat.data_ptr(), stride_logits=flat.stride(0),
+        dtype=_native.SS_DTYPE_F32 if wide else _native.SS_DTYPE_BF16, rows=6, vocab_size=9000, k=32,
+        block_n=2048, strategy=0, scratch=scratch.data_ptr(), stride_scratch=scratch.stride(0),
+        values=values.data_ptr(), indices=topk.indices.data_ptr(), stream=0x5EA3)
+
+    assert captured.calls == [("ss_topk", bytes(expected))]

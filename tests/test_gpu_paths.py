@@ -796,3 +796,93 @@ def test_layouts_agree_drafting_d2t_grammar(block):
     for a, b in zip(results["tiles"], results["rowwise"]):
 
         assert torch.equal(a, b)
+
+
+def test_concurrent_calls_from_two_threads_on_two_streams():
+    """Two host threads, each with its own sampler instances, buffers and stream, call the decode
+    step and the verifier alternately: every result equals the same call made alone. The library's
+    host code keeps no per-call state outside the caller's buffers, and a ctypes call releases the
+    interpreter lock, so the two threads' launches interleave."""
+
+    import threading
+    from types import SimpleNamespace
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedMultistep, UnshardedFusedSingular
+
+    rows, vocab, gamma, calls = 8, 16384, 2, 12
+    n, batch = gamma + 1, rows // 2
+
+    def make(seed):
+
+        g = torch.Generator().manual_seed(seed)
+
+        return SimpleNamespace(
+            host=random_host(rows, n, vocab, seed, EVERY_PROCESSOR, max_top_logprobs=4),
+            singular=UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=4,
+                                                       block_size=4096, device=DEV),
+            verifier=UnshardedFusedMultistep.initialize(vocab_size=vocab, lookahead=gamma, batch_size=batch,
+                                                        max_top_logprobs=4, block_size=4096, device=DEV),
+            logits=[spiked_logits(rows, vocab, seed=seed * 100 + i).to(DEV) for i in range(3)],
+            target=[spiked_logits(batch * n, vocab, seed=seed * 100 + 50 + i).view(batch, n, vocab).to(DEV)
+                    for i in range(3)],
+            drafted=torch.randint(1, vocab, (batch, n), generator=g).to(torch.int32).to(DEV),
+            probs=torch.softmax(torch.randn(batch, gamma, vocab, generator=g), dim=-1).to(torch.bfloat16).to(DEV),
+            stream=torch.cuda.Stream())
+
+    def run(ctx, out):
+
+        with torch.cuda.stream(ctx.stream):
+
+            buffers = to_device(ctx.host, DEV)
+
+            for i in range(calls):
+
+                if i % 2 == 0:
+
+                    sel = ctx.singular.autoregressive(ctx.logits[i % 3], buffers, logprobs=True, philox_seed=7,
+                                                      philox_offset=i)
+                    out.append([t.clone() for t in (sel.tokens, sel.logprobs.selected)])
+
+                else:
+
+                    ver = ctx.verifier(ctx.target[i % 3], ctx.drafted, buffers, probabilities=ctx.probs,
+                                       logprobs=True, philox_seed=9, philox_offset=i)
+                    # logprobs are written for the emitted span only (positions up to the offset)
+                    span = torch.arange(n, device=DEV)[None] <= ver.offsets
+                    lp = torch.where(span, ver.logprobs.selected.float(), 0.0)
+                    out.append([ver.tokens.clone(), ver.offsets.clone(), lp])
+
+        ctx.stream.synchronize()
+
+    contexts = [make(91), make(92)]
+    torch.cuda.synchronize()
+    alone = []
+
+    for ctx in contexts:
+
+        out = []
+        run(ctx, out)
+        alone.append(out)
+
+    together = [[], []]
+    print("two threads, two streams", flush=True)
+    threads = [threading.Thread(target=run, args=(ctx, together[j])) for j, ctx in enumerate(contexts)]
+
+    for t in threads:
+
+        t.start()
+
+    for t in threads:
+
+        t.join()
+
+    for j in range(2):
+
+        assert len(together[j]) == calls
+
+        for i in range(calls):
+
+            for a, b in zip(alone[j][i], together[j][i]):
+
+                assert torch.equal(a.cpu(), b.cpu()), (j, i)

@@ -55,7 +55,7 @@ def sweep_cases(count: int, seed: int):
     return cases
 
 
-CASES = sweep_cases(48, 7)
+CASES = sweep_cases(96, 7)
 
 
 def sweep_logits(rows: int, vocab: int, values: str, seed: int) -> torch.Tensor:
@@ -219,7 +219,7 @@ def topk_cases(count: int, seed: int):
     return cases
 
 
-TOPK_CASES = topk_cases(48, 11)
+TOPK_CASES = topk_cases(96, 11)
 
 
 @pytest.mark.parametrize("block,vocab,rows,k,dtype,values,seed", TOPK_CASES)

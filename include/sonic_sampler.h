@@ -242,7 +242,9 @@ typedef struct ss_multistep_args {
     const uint16_t *gumbel; int64_t gumbel_stride_slot; int64_t gumbel_stride_step;
     ss_philox philox;
     /* outputs */
-    int32_t *out_tokens;         /* flat [rows] (pre-filled with the drafts by the caller) */
+    int32_t *out_tokens;         /* flat [rows]: every row's draft, each request's emitted token at
+                                    its offset; written whole by the call (no pre-fill needed), and
+                                    it may be drafted_tokens itself */
     int32_t *offsets;            /* [B] */
     uint16_t *logprobs;          /* flat [rows] bf16 or NULL */
     uint16_t *top_values; int32_t *top_tokens; int64_t stride_top; /* [rows, Z] or NULL */

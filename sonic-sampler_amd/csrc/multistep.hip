@@ -291,9 +291,24 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(const int32_t *p_c
     const int32_t *idxs = a.indices + (int64_t)rq.margin * SS_K;
 
     const bool want_lp = a.return_logprobs && a.logprobs;
+    if (p_cu) {
+        // rows outside every request's span (cu_seqlens starting above 0 or ending before the last
+        // row) keep their drafts, as in a copy of the drafts: the first request copies the rows
+        // before it, the last the rows after it (bounds clamped to the rows)
+        if (b == 0) {
+            const int hi = min(max(p_cu[0], 0), p_rows);
+            for (int r = lane; r < hi; r += 64) a.out_tokens[r] = a.drafted_tokens[r];
+        }
+        if (b == (int)gridDim.x - 1) {
+            for (int r = min(max(p_cu[gridDim.x], 0), p_rows) + lane; r < p_rows; r += 64)
+                a.out_tokens[r] = a.drafted_tokens[r];
+        }
+    }
     if (a.all_greedy && !greedy) {
         // The caller's all_greedy hint is wrong for this request: no row launch left its records.
-        // It is not served, and says so: offsets -1 (outside 0..gamma), nothing else written.
+        // It is not served, and says so: offsets -1 (outside 0..gamma), its tokens the drafts,
+        // nothing else written.
+        if (lane < n) a.out_tokens[rq.margin + lane] = drafted[lane];
         if (lane == 0) a.offsets[rq.b] = -1;
         return;
     }
@@ -396,10 +411,10 @@ __global__ __launch_bounds__(64) void multistep_verify_kernel(const int32_t *p_c
         if (tok >= 0 && tok < a.vocab_size)
             atomicAdd(a.decode_counts + (int64_t)slot * a.stride_decode + tok, 1);
     }
-    if (lane == 0) {
-        a.out_tokens[rq.margin + j] = token;
-        a.offsets[rq.b] = j;
-    }
+    // the request's tokens: its drafts, the emitted token at j (the buffer needs no pre-fill and
+    // may be the drafts' own; each lane stores one position)
+    if (lane < n) a.out_tokens[rq.margin + lane] = lane == j ? token : drafted[lane];
+    if (lane == 0) a.offsets[rq.b] = j;
 }
 
 template <int MODE>

@@ -116,8 +116,12 @@ def resolve_uniform(noise: Optional[Tensor], logits: Tensor, batch_size: int, lo
 
 
 def resolve_tokens(drafted: Tensor, output: Optional[Tensor]) -> Tensor:
+    """The output token buffer: the caller's, or a new one. The reference clones the drafts here
+    (``:163-165``); the request stage writes every row itself (the drafts, each request's emitted
+    token at its offset), so a new buffer holds the same tokens without a copy launch ahead of the
+    tile stage."""
 
-    return output if output is not None else drafted.clone()
+    return output if output is not None else torch.empty_like(drafted, memory_format=torch.contiguous_format)
 
 
 def fused_multistep(

@@ -272,6 +272,60 @@ def test_wrong_all_greedy_hint_marks_the_request():
         assert offsets[b] == expected[b].offset, b
         m = work.cu_seqlens[b]
         assert [int(t) for t in tokens[m: m + offsets[b] + 1]] == expected[b].tokens, b
+        assert torch.equal(tokens[m + offsets[b] + 1: m + n], drafted[m + offsets[b] + 1: m + n]), b
+
+    # the request that is not served keeps its drafts
+    assert torch.equal(tokens[2 * n: 3 * n], drafted[2 * n: 3 * n])
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+def test_token_buffer_written_whole(in_place):
+    """The verifier writes every row of the token buffer: each request's drafts with its emitted
+    token at its offset, and the drafts of the rows outside every request (cu_seqlens starting
+    above row 0 and ending before the last row), in a new buffer and in place over the drafts."""
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    gamma, vocab, rows = 3, 8192, 21
+    cu = [2, 6, 8, 12, 16]            # four requests over rows 2..15; rows 0-1 and 16-20 are outside
+    batch = len(cu) - 1
+    logits = spiked_logits(rows, vocab, seed=23)
+    g = torch.Generator().manual_seed(23)
+    drafted = torch.randint(1, vocab, (rows,), generator=g).to(torch.int32)
+    host = SamplingBuffers.random(size=batch, timesteps=gamma + 1, vocab_size=vocab, device="cpu", seed=23,
+                                  max_top_logprobs=5)
+    buffers = to_device(host, "cuda:0")
+    # buffers for 6 requests of gamma + 1 rows: room for the 21 rows
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=vocab, lookahead=gamma, batch_size=6,
+                                                  block_size=1024, max_top_logprobs=5, device="cuda:0")
+    tokens = drafted.to("cuda:0")
+    print(f"token buffer written whole, in_place={in_place}", flush=True)
+    verification = verifier(logits.to("cuda:0"), tokens, buffers, logprobs=True, in_place=in_place,
+                            cu_seqlens=torch.tensor(cu, dtype=torch.int32, device="cuda:0"))
+    torch.cuda.synchronize()
+
+    out = verification.tokens.cpu()
+    offsets = verification.offsets.reshape(-1).cpu().tolist()
+    assert (verification.tokens.data_ptr() == tokens.data_ptr()) == in_place
+    assert torch.equal(out[:cu[0]], drafted[:cu[0]]) and torch.equal(out[cu[-1]:], drafted[cu[-1]:])
+
+    state = oracle.State.from_buffers(host)
+    shifted = [c - cu[0] for c in cu]
+    expected = oracle.multistep(logits[cu[0]:cu[-1]], state, drafted[cu[0]:cu[-1]], shifted, logprobs=True)
+
+    for b, e in enumerate(expected):
+
+        m, end = cu[b], cu[b + 1]
+
+        if e.knife:
+
+            continue
+
+        assert offsets[b] == e.offset, b
+        assert [int(t) for t in out[m: m + offsets[b] + 1]] == e.tokens, b
+        assert torch.equal(out[m + offsets[b] + 1: end], drafted[m + offsets[b] + 1: end]), b
 
 
 def test_graph_replay_config2_all_greedy_hint():

@@ -280,7 +280,26 @@ class TwoStageTiling:
         kind: Optional[str] = None,
     ):
         """Warp config, strategy and block_n for a launch of `size` rows (reference ``:243-276``),
-        from the table of call kind `kind` where the buffers were made for it."""
+        from the table of call kind `kind` where the buffers were made for it. Without an explicit
+        strategy or tuning the answer depends only on `size`, `kind` and the instance's tables, and
+        is kept per instance (an eager call's host path looks it up once per row count)."""
+
+        if strategy is None and tuning is None:
+
+            cache = self.__dict__.setdefault("_tuning_cache", {})
+            key = (size, kind, self.block_n)
+            hit = cache.get(key)
+
+            # an entry holds the tables it was computed from: replacing them invalidates it
+            if hit is None or hit[0] is not self.dispatch or hit[1] is not self.kind_dispatch:
+
+                hit = cache[key] = (self.dispatch, self.kind_dispatch, self._tuning(size, None, None, kind))
+
+            return hit[2]
+
+        return self._tuning(size, strategy, tuning, kind)
+
+    def _tuning(self, size, strategy, tuning, kind):
 
         block_size = self.block_n
         k_strategy = strategy

@@ -76,8 +76,25 @@ class UnshardedFusedMultistep(TwoStageTiling):
 
     def tuning(self, size: int, strategy=None, tuning: Optional[ThreeStageWarpConfig] = None):
 
-        config, k_strategy, block_n = super().tuning(size, strategy, tuning and tuning.two_stage)
+        base = super().tuning(size, strategy, tuning and tuning.two_stage)
 
+        if strategy is None and tuning is None:
+
+            # the base lookup is kept per instance; so is the three-stage config built from it
+            cache = self.__dict__.setdefault("_three_stage_cache", {})
+            hit = cache.get(size)
+
+            if hit is None or hit[0] is not base:
+
+                hit = cache[size] = (base, self._three_stage(base, None))
+
+            return hit[1]
+
+        return self._three_stage(base, tuning)
+
+    def _three_stage(self, base, tuning):
+
+        config, k_strategy, block_n = base
         config = ThreeStageWarpConfig.from_config(
             config=config, third=tuning and tuning.third, gamma=self.lookahead
         )

@@ -224,6 +224,28 @@ def test_launch_width_never_leaves_a_single_tile(vocab):
             assert tiling.tuning(4)[2] == tiling.block_n == 2048
 
 
+def test_tuning_is_kept_per_instance_and_follows_its_tables():
+    """The lookup without an explicit strategy or tuning is computed once per row count, equal to
+    a fresh one, and recomputed when the instance's tables are replaced."""
+
+    from sonic_sampler.interface import UnshardedFusedMultistep
+
+    tiling, _, _ = TwoStageTiling.factory(vocab_size=128256, batch_size=64, arch="gfx950", device="cpu")
+    first = tiling.tuning(64)
+
+    assert tiling.tuning(64) is first
+    assert tiling._tuning(64, None, None, None)[2] == first[2]
+
+    tiling.dispatch = None
+
+    assert tiling.tuning(64) is not first and tiling.tuning(64)[2] == tiling.block_n
+
+    verifier = UnshardedFusedMultistep.initialize(vocab_size=128256, lookahead=3, batch_size=16, device="cpu")
+    config, _, block_n = verifier.tuning(64)
+
+    assert verifier.tuning(64)[0] is config and config.third == 4 and block_n == verifier.tuning(64)[2]
+
+
 def test_single_tile_vocabulary_is_rejected():
 
     with pytest.raises(ValueError, match="greater than 1"):

@@ -384,3 +384,27 @@ def test_autotune_writes_a_table_per_kind_from_a_log(tmp_path):
     assert shared.vocab.get(32768).batch.get(8).best.block_n == 1024
     assert [b.size for b in multistep.vocab.get(32768).batch] == [8]     # no one-row verification
     assert multistep.vocab.get(32768).batch.get(8).best.block_n == 8192
+
+
+def test_all_greedy_reads_the_mirror_the_lists_are_kept_in():
+    """all_greedy equals the lists' own test for uniform, mixed and updated indicator sets."""
+
+    from sonic_sampler.core.flags import Flags, Indicator, ScopedIndicators
+
+    greedy, stochastic = Indicator.GREEDY | Indicator.GRAMMAR, Indicator.TEMPERATURE
+
+    for target, draft in ((greedy, greedy), (greedy, stochastic), (stochastic, greedy),
+                          ([greedy] * 7 + [stochastic], None), ([stochastic] + [greedy] * 7, None)):
+
+        flags = Flags.from_values(8, 3, target, draft, device="cpu")
+        lists = flags.indicators.greedy_target and flags.indicators.greedy_draft
+
+        assert flags.all_greedy == lists, (target, draft)
+
+    flags = Flags.from_values(8, 3, greedy, device="cpu")
+    assert flags.all_greedy
+    flags.update(ScopedIndicators.from_values(size=1, timesteps=3, target=[stochastic]), positions=[5])
+    assert not flags.all_greedy and not flags.indicators.greedy_target
+    flags.update(ScopedIndicators.from_values(size=1, timesteps=3, target=[greedy]), positions=[5])
+    assert flags.all_greedy
+    assert flags.subset([0, 1, 2], torch.tensor([0, 1, 2])).all_greedy

@@ -459,6 +459,10 @@ class Flags(SliceBuffer):
 
             return False
 
+        if self.pinned.device.type != "cpu":
+
+            return self.indicators.greedy_target and self.indicators.greedy_draft
+
         return bool((self.pinned.numpy() & int(Indicator.GREEDY)).all())
 
     def selectors(self, flag: Indicator) -> Tensor:

@@ -471,8 +471,10 @@ class Flags(SliceBuffer):
 
     def update(self, indicators: ScopedIndicators, positions: Optional[List[int]], stream=None) -> "Flags":
         """Installs `indicators` at rows `positions` (the leading rows when None): the readable
-        lists, the pinned [B, 2] mirror, and an asynchronous copy of those rows of the mirror to
-        the device words the kernels read (on `stream` when given)."""
+        lists, the pinned [B, 2] mirror, and an asynchronous copy of the mirror to the device words
+        the kernels read (on `stream` when given): the leading rows, or for scattered positions the
+        whole mirror in one copy (its other rows already equal their device words, so they are
+        rewritten unchanged) instead of one copy per row."""
 
         self.indicators.update(indicators, positions)
         words = indicators.as_tensor(host=True).T  # [n, 2]: (target, draft) of each new row
@@ -498,8 +500,6 @@ class Flags(SliceBuffer):
 
             else:
 
-                for row in rows:
-
-                    self.packed[row].copy_(self.pinned[row], non_blocking=True)
+                self.packed.copy_(self.pinned, non_blocking=True)
 
         return self

@@ -79,3 +79,28 @@ def test_autotune_measures_a_small_table(tmp_path):
     back = DispatchSummary.read(path)
     assert back.vocab.get(32768).batch.get(16).best.block_n in (1024, 2048, 4096, 8192, 16384)
     assert len(back.vocab.get(8192).batch.get(1).config) == 1
+
+
+def test_flags_update_reaches_the_device_words():
+    """Flags.update at scattered and at leading positions, on a copy stream: the device words the
+    kernels read equal the readable lists afterwards, and all_greedy follows them."""
+
+    from sonic_sampler.core.flags import Flags, Indicator, ScopedIndicators
+
+    greedy, stochastic = Indicator.GREEDY | Indicator.GRAMMAR, Indicator.TEMPERATURE | Indicator.TOP_P
+    flags = Flags.from_values(16, 4, greedy, device="cuda:0")
+    stream = torch.cuda.Stream()
+    expect = lambda: torch.tensor([[int(t), int(d)] for t, d in zip(flags.indicators.target,
+                                                                     flags.indicators.draft)], dtype=torch.int32)
+
+    assert flags.all_greedy
+    flags.update(ScopedIndicators.from_values(size=3, timesteps=4, target=[stochastic] * 3,
+                                              draft=[greedy, stochastic, greedy]), positions=[11, 2, 7], stream=stream)
+    stream.synchronize()
+    assert torch.equal(flags.packed.cpu().to(torch.int32), expect())
+    assert not flags.all_greedy
+
+    flags.update(ScopedIndicators.from_values(size=2, timesteps=4, target=[greedy] * 2), positions=None, stream=stream)
+    stream.synchronize()
+    assert torch.equal(flags.packed.cpu().to(torch.int32), expect())
+    assert flags.packed.stride() == (1, 16)

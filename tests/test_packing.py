@@ -57,6 +57,22 @@ def test_packer_layout_is_the_ctypes_layout(cls):
     assert packer.pack(*values) == bytes(named_struct(cls, packer.fields, values))
 
 
+@pytest.mark.parametrize("cls", STRUCTS, ids=lambda c: c.__name__)
+def test_packer_takes_every_field_type_to_its_limits(cls):
+    """Each field at its type's extremes (and -1 for the signed ones) packs to the ctypes bytes."""
+
+    packer = _native.Packer(cls)
+    codes = [code for *_, code in _native._flat_layout(cls)]
+    limits = {"i": (-2 ** 31, 2 ** 31 - 1, -1), "q": (-2 ** 63, 2 ** 63 - 1, -1),
+              "I": (0, 2 ** 32 - 1, 1), "Q": (0, 2 ** 64 - 1, 1)}
+
+    for pick in range(3):
+
+        values = [limits[c][(pick + j) % 3] for j, c in enumerate(codes)]
+
+        assert packer.pack(*values) == bytes(named_struct(cls, packer.fields, values)), pick
+
+
 class Captured:
 
     def __init__(self):

@@ -111,6 +111,66 @@ def test_all_accepted_emits_bonus_from_last_step():
     assert torch.equal(verification.tokens.cpu().flatten(), drafted)
 
 
+def test_maximum_lookahead():
+    """gamma = 63, the most one wave per request verifies: 64 rows per request, every processor
+    on (the penalties see up to 63 drafted tokens of history), a greedy request whose drafts are
+    its argmaxes (the chain runs to the bonus row 63), one whose chain breaks at row 40 and a
+    stochastic one; the per-row top-128 ids, the tokens, offsets and logprobs against the
+    oracle."""
+
+    from bench import MultistepWorkload, spiked_logits
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    batch, gamma, vocab = 3, 63, 8192
+    n = gamma + 1
+    host = SamplingBuffers.random(size=batch, timesteps=n, vocab_size=vocab, device="cpu", seed=63,
+                                  max_top_logprobs=4)
+    every = Indicator(0x3BF) | Indicator.TOP_K_LOGPROBS
+    greedy = (every & ~Indicator.stochastic()) | Indicator.GREEDY
+    host.flags = Flags.from_values(batch, n, [greedy, greedy, every], device="cpu")
+    host.top_k.copy_(torch.tensor([1, 1, 128], dtype=torch.int32))
+    logits = spiked_logits(batch * n, vocab, seed=64)
+    g = torch.Generator().manual_seed(65)
+    state = oracle.State.from_buffers(host)
+    drafted = torch.randint(1, vocab, (batch * n,), generator=g).to(torch.int32)
+    # the greedy requests' drafts are their rows' argmaxes after the processors, the drafts before
+    # each row counting as its history (the oracle's processed rows); one chain broken at row 40
+    for b in (0, 1):
+
+        for i in range(n):
+
+            x = oracle.process_row(logits[b * n + i], state, b, int(state.target[b]), state.grammar[b, i],
+                                   [int(t) for t in drafted[b * n: b * n + i]], None)
+            drafted[b * n + i] = int(x.argmax())
+
+    drafted[1 * n + 40] = (drafted[1 * n + 40] + 1) % vocab
+    probabilities = torch.softmax(torch.randn(batch, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host,
+                             cu_seqlens=list(range(0, batch * n + 1, n)), lookahead=gamma, vocab=vocab,
+                             max_top_logprobs=4, probabilities=probabilities)
+    print("maximum lookahead: gamma=63", flush=True)
+    verification, buffers, verifier = run_verifier(work, update_counts=True, block_size=2048)
+
+    expected = oracle.multistep(logits, state, drafted, work.cu_seqlens, probabilities=probabilities,
+                                logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, work.cu_seqlens, logprobs=True, max_knife_fraction=0.34)
+    offsets = verification.offsets.reshape(-1).tolist()
+
+    assert 0 not in mismatched and offsets[0] == gamma
+    assert 1 not in mismatched and offsets[1] == 40
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[b * n + i], idx), (b, i)
+
+    counts = expected_multistep_counts(state.decode, expected, verification, work.cu_seqlens, mismatched)
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
 def test_merge_paths_at_128_tiles():
     """Multistep rows at V = 131072, block 1024 (128 lists, 4 sampled per list) whose top-128
     crowds into a few lists, into more lists than the whole-list bound, or ties everywhere: the

@@ -128,6 +128,39 @@ def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
                    slot_mapping=slot_mapping)
 
 
+def test_drafting_with_the_longest_history():
+    """Drafting at timestep 64 (the longest history a wave stages) with every processor on: the
+    penalties count the 64 drafted tokens of each row's history, through d2t and slots."""
+
+    from bench import spiked_logits, to_device
+    from sonic_sampler.interface import UnshardedFusedSingular
+
+    slots, rows, gamma, t = 10, 8, 64, 64
+    draft_vocab, target_vocab = 8192, 12288
+    g = torch.Generator().manual_seed(64)
+    host = random_host(slots, gamma + 1, target_vocab, 64, EVERY_PROCESSOR)
+    buffers = to_device(host, DEV)
+    logits = spiked_logits(rows, draft_vocab, seed=640)
+    slot_mapping = torch.randperm(slots, generator=g)[:rows].to(torch.int32)
+    d2t = torch.randperm(target_vocab, generator=g)[:draft_vocab].to(torch.int32)
+    # histories drawn from the drafter's targets, so that they hit the rows' candidates often
+    tokens = d2t[torch.randint(0, 256, (rows, gamma + 1), generator=g)].to(torch.int32)
+    print("drafting at timestep 64", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=draft_vocab, batch_size=rows, lookahead=gamma,
+                                                block_size=2048, max_top_logprobs=5, device=DEV)
+    probs = torch.zeros(slots, target_vocab, dtype=torch.bfloat16, device=DEV)
+    selection = sampler.drafting(logits.to(DEV), buffers, timestep=t, tokens=tokens.to(DEV), probabilities=probs,
+                                 slot_mapping=slot_mapping.to(DEV), d2t_mapping=d2t.to(DEV),
+                                 target_vocab=target_vocab, in_place=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="draft", timestep=t, slot_mapping=slot_mapping.tolist(),
+                               d2t=d2t, drafted=tokens, history=t, probs=True, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=False, probabilities=probs, slot_mapping=slot_mapping)
+
+
 @pytest.mark.parametrize("seed,draft_vocab,target_vocab,block", [(44, 6144, 8197, 2048), (45, 6144, 8197, 2048),
                                                                 (46, 40000, 131075, 16384),
                                                                 (47, 40000, 300007, 16384),

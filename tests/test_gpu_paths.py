@@ -128,6 +128,19 @@ def test_scalar_path_d2t_draft_vocabulary_not_a_multiple_of_4(seed):
                    slot_mapping=slot_mapping)
 
 
+def test_more_than_512_tiles():
+    """586 tiles of 1024 columns (V = 600,000): the row merge samples nothing (512 / tiles < 1)
+    and every row takes the radix merge over all 75,008 candidates, with every processor on."""
+
+    from bench import spiked_logits
+
+    rows, vocab = 4, 600_000
+    print(f"more than 512 tiles: V={vocab}", flush=True)
+    host = random_host(rows, 1, vocab, 512, EVERY_PROCESSOR)
+    logits = spiked_logits(rows, vocab, seed=513).to(DEV)
+    assert autoregressive_case(logits, host, 1024) >= rows - 1
+
+
 def test_drafting_with_the_longest_history():
     """Drafting at timestep 64 (the longest history a wave stages) with every processor on: the
     penalties count the 64 drafted tokens of each row's history, through d2t and slots."""

@@ -252,3 +252,14 @@ def test_graph_replay(rows):
             ev, ei = oracle_topk(sets[i], k)
             assert torch.equal(captured[1].cpu(), ei)
             assert torch.equal(captured[0].cpu().view(torch.int32), ev.view(torch.int32))
+
+
+@pytest.mark.parametrize("k", [32, 128])
+def test_more_than_512_tiles(k):
+    """586 tiles of 1024 columns: the merge takes the per-row radix merge over every candidate."""
+
+    from bench import spiked_logits
+
+    logits = spiked_logits(3, 600_000, seed=600 + k)
+    print(f"top-k over 586 tiles, k={k}", flush=True)
+    check(logits, k, block_size=1024)

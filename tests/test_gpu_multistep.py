@@ -111,6 +111,64 @@ def test_all_accepted_emits_bonus_from_last_step():
     assert torch.equal(verification.tokens.cpu().flatten(), drafted)
 
 
+def test_requests_without_drafts():
+    """Variable lookahead down to a request of one row (no drafts: only the bonus row, offset 0)
+    beside longer ones, stochastic and greedy, with slots: tokens, offsets, logprobs and the
+    per-row top-128 ids against the oracle."""
+
+    from bench import MultistepWorkload, spiked_logits
+    from sonic_sampler.core.flags import Flags, Indicator
+
+    gamma, vocab, slots = 3, 8192, 6
+    cu = [0, 1, 4, 5, 9, 10]
+    batch, rows = len(cu) - 1, cu[-1]
+    host = random_buffers(slots, gamma + 1, vocab, seed=71)
+    every = Indicator(0x3BF) | Indicator.TOP_K_LOGPROBS
+    greedy = (every & ~Indicator.stochastic()) | Indicator.GREEDY
+    host.flags = Flags.from_values(slots, gamma + 1, [every, greedy, every, every, greedy, every], device="cpu")
+    host.top_k.copy_(torch.tensor([128, 1, 128, 50, 1, 128], dtype=torch.int32))
+    logits = spiked_logits(rows, vocab, seed=72)
+    g = torch.Generator().manual_seed(73)
+    drafted = torch.randint(1, vocab, (rows,), generator=g).to(torch.int32)
+    slot_mapping = torch.tensor([4, 1, 0, 5, 2], dtype=torch.int32)
+    probabilities = torch.softmax(torch.randn(slots, gamma, vocab, generator=g) * 2, dim=-1).to(torch.bfloat16)
+    work = MultistepWorkload(logits=logits, drafted=drafted, buffers=host, cu_seqlens=cu, lookahead=gamma,
+                             vocab=vocab, max_top_logprobs=4, probabilities=probabilities, varlen=True)
+    print(f"requests without drafts: cu_seqlens={cu}", flush=True)
+    verification, buffers, verifier = run_verifier(work, update_counts=True, block_size=1024,
+                                                   slot_mapping=slot_mapping.to("cuda:0"))
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.multistep(logits, state, drafted, cu, slot_mapping=slot_mapping.tolist(),
+                                probabilities=probabilities, logprobs=True, max_top_logprobs=4)
+    mismatched = check_multistep(verification, expected, cu, logprobs=True, max_knife_fraction=0.2)
+    offsets = verification.offsets.reshape(-1).tolist()
+
+    for b in (0, 2, 4):
+
+        assert offsets[b] == 0, b          # one-row requests emit their bonus row's token
+
+    indices = verifier.indices.cpu()
+
+    for b, e in enumerate(expected):
+
+        for i, idx in enumerate(e.row_indices):
+
+            assert torch.equal(indices[cu[b] + i], idx), (b, i)
+
+    counts = expected_multistep_counts(state.decode, expected, verification, cu, mismatched,
+                                       slot_mapping.tolist())
+    assert torch.equal(buffers.repetition.counts.decode.cpu(), counts)
+
+
+def random_buffers(slots, timesteps, vocab, seed):
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+
+    return SamplingBuffers.random(size=slots, timesteps=timesteps, vocab_size=vocab, device="cpu", seed=seed,
+                                  max_top_logprobs=4)
+
+
 def test_maximum_lookahead():
     """gamma = 63, the most one wave per request verifies: 64 rows per request, every processor
     on (the penalties see up to 63 drafted tokens of history), a greedy request whose drafts are

@@ -294,6 +294,53 @@ def test_extreme_divisors_and_penalties():
     assert [int(t) for t in tokens] == [e.token for e in expected]
 
 
+def test_truncation_at_its_extremes():
+    """Truncation parameters at their ends, with logprobs and the top logprobs: top-p keeping only
+    the first candidate (p = 0.01) or nearly all, min-p at 0.99 (only values tied with the
+    maximum survive) and at 0.5, top-k of 2, 3 and 127, and the three combined, at temperatures
+    from 0.05 to 20 on tied and spiked rows."""
+
+    from sonic_sampler.core.buffer import SamplingBuffers
+    from sonic_sampler.core.flags import Flags, ScopedIndicators
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    rows, vocab = 16, 16384
+    bf = lambda v: float(torch.tensor(v).to(torch.bfloat16))  # noqa: E731
+    top_p = [bf(v) for v in (0.01, 0.99, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 0.5, 0.01, 0.9, 1.0, 1.0, 0.3, 1.0, 0.05)]
+    min_p = [bf(v) for v in (0.0, 0.0, 0.99, 0.5, 0.0, 0.0, 0.0, 0.0, 0.2, 0.99, 0.0, 0.05, 0.0, 0.0, 0.9, 0.0)]
+    top_k = [128, 128, 128, 128, 2, 3, 127, 128, 3, 2, 50, 20, 128, 128, 128, 127]
+    temperature = [bf(v) for v in (1.0, 0.05, 20.0, 1.0, 0.5, 3.0, 1.0, 0.05, 1.0, 20.0, 1.0, 0.7, 1.0, 2.0, 0.1, 1.0)]
+    scoped = ScopedIndicators.from_params(
+        size=rows, timesteps=1, multiplicative=[1.0] * rows, frequency=[0.0] * rows, presence=[0.0] * rows,
+        biases=[{} for _ in range(rows)], temperature=temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+        top_logprobs=[5] * rows)
+    g = torch.Generator().manual_seed(6)
+    host = SamplingBuffers.default(size=rows, timesteps=1, vocab_size=vocab, device="cpu", noise=False)
+    host.flags = Flags.from_scoped(scoped, device="cpu")
+    host.weights.gumbel.target.exponential_(1.0, generator=g).log_()
+    host.temperature.copy_(torch.tensor(temperature).to(torch.bfloat16))
+    host.top_p.copy_(torch.tensor(top_p).to(torch.bfloat16))
+    host.min_p.copy_(torch.tensor(min_p).to(torch.bfloat16))
+    host.top_k.copy_(torch.tensor(top_k, dtype=torch.int32))
+    host.top_logprobs.fill_(5)
+    logits = spiked_logits(rows, vocab, seed=606)
+    # tied rows: a few distinct values, so that truncation cuts through runs of equal candidates
+    logits[1::4] = (torch.randint(-2, 3, (rows // 4, vocab), generator=g).float() * 2.0).to(torch.bfloat16)
+    buffers = to_device(host, DEV)
+    print("truncation at its extremes", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=5,
+                                                block_size=2048, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=5)
+    _, checked = check_singular(selection, expected, logprobs=True, max_knife_fraction=0.1)
+    assert checked >= rows - 1
+
+
 def test_merge_paths_at_128_tiles():
     """V = 131072 at block 1024: 128 candidate lists of which the row merge samples 4 entries
     each. Rows whose top-128 crowds into a few lists have those lists merged whole; rows with

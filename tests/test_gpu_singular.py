@@ -341,6 +341,53 @@ def test_truncation_at_its_extremes():
     assert checked >= rows - 1
 
 
+def test_logit_bias_forcing_and_banning():
+    """Logit bias at the ends of its use: +100 on one token forces it, -inf on each row's argmax
+    (and its runner-up) bans them, alongside ordinary biases, with penalties and logprobs."""
+
+    from sonic_sampler.interface import UnshardedFusedSingular
+    from bench import spiked_logits, to_device
+
+    from test_gpu_paths import EVERY_PROCESSOR, random_host
+
+    rows, vocab = 12, 16384
+    host = random_host(rows, 1, vocab, 8, EVERY_PROCESSOR)
+    logits = spiked_logits(rows, vocab, seed=808)
+    g = torch.Generator().manual_seed(8)
+    bias = host.bias
+    top2 = logits.float().topk(2, dim=-1).indices
+    forced = torch.randint(0, vocab, (rows,), generator=g)
+
+    for r in range(rows):
+
+        if r % 3 == 0:
+
+            bias[r, forced[r]] = 100.0
+
+        elif r % 3 == 1:
+
+            bias[r, top2[r]] = float("-inf")
+
+    buffers = to_device(host, DEV)
+    print("logit bias forcing and banning", flush=True)
+
+    sampler = UnshardedFusedSingular.initialize(vocab_size=vocab, batch_size=rows, max_top_logprobs=5,
+                                                block_size=4096, device=DEV)
+    selection = sampler.autoregressive(logits.to(DEV), buffers, logprobs=True)
+    torch.cuda.synchronize()
+
+    state = oracle.State.from_buffers(host)
+    expected = oracle.singular(logits, state, scope="target", logprobs=True, max_top_logprobs=5)
+    check_singular(selection, expected, logprobs=True)
+    tokens = selection.tokens[:, 0].cpu()
+
+    for r in range(rows):
+
+        if r % 3 == 1:
+
+            assert int(tokens[r]) not in top2[r].tolist(), r
+
+
 def test_merge_paths_at_128_tiles():
     """V = 131072 at block 1024: 128 candidate lists of which the row merge samples 4 entries
     each. Rows whose top-128 crowds into a few lists have those lists merged whole; rows with

@@ -32,3 +32,16 @@ def test_gumbel_transform_matches_oracle():
     assert np.mean(noise == expected) > 0.999
     # log(Exp(1)) has mean -Euler-Mascheroni
     assert abs(float(noise.mean()) + 0.5772) < 0.02
+
+
+@pytest.mark.parametrize("seed,offset,slots,steps,vocab", [
+    (2 ** 64 - 1, 2 ** 32 - 1, 2, 2, 262144),       # every key and offset bit set, the widest vocabulary
+    (0x0123_4567_89AB_CDEF, 0, 512, 65, 16),         # the last slot of 512 and timestep 64
+])
+def test_raw_words_at_the_counter_limits(seed, offset, slots, steps, vocab):
+
+    from sonic_sampler.noise import philox_words
+
+    print(f"philox words at the limits: slots={slots} steps={steps} vocab={vocab}", flush=True)
+    words = philox_words(seed, offset, slots, steps, vocab, device="cuda:0").cpu().numpy().view(np.uint32)
+    assert np.array_equal(words, noise_words(seed, offset, slots, steps, vocab))

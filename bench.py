@@ -518,8 +518,9 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
 
     torch.cuda.synchronize()
 
-    # The tile kernel alone, from events its own dispatch records at its start and end (a second
-    # pass: recording them adds a little to each step, so the step time above runs without them).
+    # The tile kernel inside the full step, from events its own dispatch records at its start and
+    # end (a second pass: recording them adds to each step, so the step time above runs without
+    # them); reported beside the tiles-only timing below.
     tile_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(steps)]
 
@@ -535,7 +536,35 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
         step(i, tile_events[i])
 
     torch.cuda.synchronize()
-    tile_kernel_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
+    tile_dispatch_us = statistics.mean(a.elapsed_time(b) * 1e3 for a, b in tile_events)
+
+    # The tile kernel's average launch duration: the tile stage alone (`stage="tiles"`, the same
+    # arguments and input rotation), launched back to back between one event pair behind a GPU
+    # sleep. The dispatch events above put marker packets around every launch, whose cache
+    # actions add about 1.3 us to each; this measure has none inside the timed region.
+    def tiles_only(i: int):
+
+        from sonic_sampler.base.tensor import plain_view
+        from sonic_sampler.interface.functional.singular import fused_singular
+
+        logits, buffers = inputs[i % sets]
+        pen = buffers.repetition
+        return fused_singular(
+            logits=logits, indicators=buffers.flags.target, max_top_logprobs=5, update_counts=True,
+            return_logprobs=True, block_n=sampler.tuning(batch)[2], scratchpad=sampler.scratchpad,
+            grammar=plain_view(buffers.grammar, 0), context_counts=pen.counts.context,
+            decode_counts=pen.counts.decode, repetition_penalties=pen.multiplicative,
+            frequency_penalties=pen.frequency, presence_penalties=pen.presence, logit_bias=buffers.bias,
+            temperature=buffers.temperature, top_k=buffers.top_k, top_p=buffers.top_p,
+            min_p=buffers.min_p, top_k_logprobs=buffers.top_logprobs,
+            philox_seed=1234 if philox else None, philox_offset=i,
+            gumbel_noise=None if philox else plain_view(buffers.weights.gumbel.target, 0), stage="tiles")
+
+    for i in range(warmup):
+
+        tiles_only(i)
+
+    tile_kernel_us = _time_back_to_back(tiles_only, steps)
 
     graph_us, graph_single_us, graph_median_us = _time_graphs(step, steps, sets)
 
@@ -572,6 +601,7 @@ def run_bench(steps: int, warmup: int, sets: Optional[int] = None, cpu_baseline:
             "event_pair_us_per_step": round(statistics.mean(launch_us), 3),
             "median_event_pair_us": round(statistics.median(launch_us), 3),
             "tile_kernel_us": round(tile_kernel_us, 3),
+            "tile_kernel_dispatch_events_us": round(tile_dispatch_us, 3),
             "graph_replay_us_per_step": round(graph_us, 3),
             "graph_replay_single_step_us": round(graph_single_us, 3),
             "graph_replay_median_us": round(graph_median_us, 3),

@@ -72,6 +72,28 @@ def unit_stride(name: str, tensor: Optional[Tensor]) -> None:
         raise ValueError(f"`{name}` must be contiguous along its last dimension")
 
 
+def require_cover(name: str, tensor: Optional[Tensor], rows: int, cols: int, steps: int = 1) -> None:
+    """A buffer the kernels address by slot: rows [0, rows), columns [0, cols) and, for a
+    [slots, steps, cols] buffer, steps [0, steps). Its storage must hold the last such element: a
+    strided view of a larger buffer passes (an engine's `draft_probs[:rows, t]`), while a buffer
+    smaller than the slots it is indexed by raises here instead of being addressed past its end."""
+
+    if tensor is None or rows <= 0 or cols <= 0:
+
+        return
+
+    last = tensor.storage_offset() + (rows - 1) * tensor.stride(0) + (cols - 1) * tensor.stride(-1)
+
+    if tensor.dim() >= 3:
+
+        last += (steps - 1) * tensor.stride(1)
+
+    if last >= tensor.untyped_storage().nbytes() // tensor.element_size():
+
+        raise ValueError(f"`{name}` does not cover the {rows} slots x {cols} columns it is indexed by "
+                         f"(shape {tuple(tensor.shape)}, strides {tensor.stride()})")
+
+
 def fresh_seed() -> int:
     """A seed drawn from torch's default CPU generator (fresh noise for a call without noise)."""
 

@@ -32,6 +32,7 @@ from sonic_sampler.interface.functional.base import (
     I32,
     collapse_2d,
     fresh_seed,
+    require_cover,
     resolve_scratchpad,
     unit_stride,
     validate_block,
@@ -218,6 +219,10 @@ def fused_multistep(
     _native.require_device(logits, indicators, drafted_tokens)
 
     rows = flat_logits.size(0)
+    # draft probabilities are read at [slot, step, token]: every slot of the buffers with a slot
+    # mapping, every step of the lookahead
+    require_cover("draft_probabilities", draft_probabilities,
+                  indicators.size(0) if slot_mapping is not None else batch_size, vocab_size, steps=max(gamma, 1))
 
     _, _, bitpacked, vocab_blocks = resolve_scratchpad(flat_logits, block_n, scratchpad)
     values_buffer, indices_buffer = resolve_unpack_buffers(flat_logits, values, indices)

@@ -45,6 +45,7 @@ from sonic_sampler.interface.functional.base import (
     BF16,
     I32,
     fresh_seed,
+    require_cover,
     unit_stride,
     validate_block,
     validate_count_update,
@@ -196,6 +197,14 @@ def fused_singular(
             raise ValueError("scratchpad too small for the given logits, block_n and world size")
 
     final_tokens = resolve_tokens(output_tokens, batch_size, logits)
+    # the width of the probability rows and of the processors' per-slot planes
+    target_width = target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size)
+
+    if return_probabilities:
+
+        # the selection scatters at [slot, target id]: every slot of the buffers with a slot mapping
+        require_cover("draft_probabilities", draft_probabilities,
+                      indicators.size(0) if slot_mapping is not None else batch_size, target_width)
 
     probabilities = resolve_probabilities(
         precondition=return_probabilities,
@@ -242,8 +251,7 @@ def fused_singular(
     # ss_singular_args, field by field in declaration order (SINGULAR_ARGS.fields names them)
     packed = SINGULAR_ARGS.pack(
         a(logits), logits.stride(0), batch_size, vocab_size,
-        target_vocab or (logit_bias.size(-1) if logit_bias is not None else world_size * shard_size),
-        block_n, lookahead, history, max_top_logprobs if top_values is not None else 0,
+        target_width, block_n, lookahead, history, max_top_logprobs if top_values is not None else 0,
         int(is_prefill), int(update_counts), int(token_logprobs is not None), int(probabilities is not None),
         KERNEL_LAYOUTS[kernel_layout],
         a(indicators), a(slot_mapping), a(d2t_mapping),

@@ -364,3 +364,45 @@ def test_bounded_topk_packs_every_field_by_name(dtype, captured):
         values=values.data_ptr(), indices=topk.indices.data_ptr(), stream=0x5EA3)
 
     assert captured.calls == [("ss_topk", bytes(expected))]
+
+
+def test_undersized_probability_buffers_are_rejected(captured):
+    """A draft-probability buffer is addressed by slot: one whose storage does not reach the last
+    slot it may be indexed by raises before any launch, while a strided view of a buffer that does
+    (an engine's `draft_probs[:rows, t]`) passes."""
+
+    from sonic_sampler.interface.functional import multistep as fm
+
+    t = tensors(rows=6, vocab=9000, slots=8, target=12000)
+    g = torch.Generator().manual_seed(3)
+    slot_mapping = torch.randperm(8, generator=g)[:6].to(torch.int32)
+    d2t = torch.randperm(12000, generator=g)[:9000].to(torch.int32)
+    call = dict(slot_mapping=slot_mapping, d2t_mapping=d2t, target_vocab=12000, return_probabilities=True,
+                philox_seed=1, drafted_tokens=torch.zeros(6, 4, dtype=torch.int32), timestep=1, lookahead=3)
+
+    with pytest.raises(ValueError, match="does not cover"):
+
+        fs.fused_singular(**t, **call, draft_probabilities=torch.zeros(6, 3, 12000, dtype=torch.bfloat16)[:, 1])
+
+    fs.fused_singular(**t, **call, draft_probabilities=torch.zeros(8, 3, 12000, dtype=torch.bfloat16)[:6, 1])
+    assert len(captured.calls) == 1
+
+    # the verifier reads [slot, step, token] of every step of the lookahead
+    batch, gamma, vocab = 3, 2, 9000
+    v = tensors(rows=batch * (gamma + 1), vocab=vocab, slots=5, target=vocab)
+    v["grammar"] = torch.zeros(5, gamma + 1, -(-vocab // 32), dtype=torch.int32)
+    logits = v.pop("logits").view(batch, gamma + 1, vocab)
+    drafted = torch.zeros(batch, gamma + 1, dtype=torch.int32)
+    base = dict(logits=logits, drafted_tokens=drafted, uniform_noise=torch.rand(batch, gamma), philox_seed=2,
+                slot_mapping=torch.tensor([4, 0, 2], dtype=torch.int32), **v)
+
+    with pytest.raises(ValueError, match="does not cover"):
+
+        fm.fused_multistep(**base, draft_probabilities=torch.zeros(3, gamma, vocab, dtype=torch.bfloat16))
+
+    with pytest.raises(ValueError, match="does not cover"):
+
+        fm.fused_multistep(**base, draft_probabilities=torch.zeros(5, gamma - 1, vocab, dtype=torch.bfloat16))
+
+    fm.fused_multistep(**base, draft_probabilities=torch.zeros(5, gamma, vocab, dtype=torch.bfloat16))
+    assert len(captured.calls) == 2

@@ -118,6 +118,10 @@ int ss_topk(const ss_topk_args *args);
  * with optional logprobs, top-Z logprobs, draft-probability scatter and decode-count update.
  * Replaces fused_singular (reference interface/functional/singular.py:75-322).
  * Row r reads its request state at slot = slot_mapping ? slot_mapping[r] : r.
+ * Caller contract, not checked on the device (as in the reference): slot_mapping values lie in
+ * [0, slots) of every slot-indexed buffer, d2t values in [0, target_vocab), and `probabilities`
+ * has a row for every slot a row may map to (the Python driver checks the last against the
+ * buffer's storage before the call).
  * ------------------------------------------------------------------------------------------- */
 typedef struct ss_singular_args {
     /* logits [rows, vocab] bf16 */
@@ -209,6 +213,9 @@ int ss_fused_singular_noalloc(const ss_singular_args *args);
  * logit rows: logit processors -> bounded top-128 -> truncation -> softmax -> greedy or
  * stochastic acceptance with residual resampling.
  * Replaces fused_multistep (reference interface/functional/multistep.py:175-461).
+ * Caller contract, not checked on the device: slot_mapping values lie in [0, slots), drafted
+ * tokens in [0, vocab_size), and draft_probabilities has a [gamma, vocab] block for every slot a
+ * request may map to (the Python driver checks the last before the call).
  * ------------------------------------------------------------------------------------------- */
 typedef struct ss_multistep_args {
     const uint16_t *logits;      /* [rows, vocab] bf16 */

@@ -215,8 +215,8 @@ int ss_fused_singular_noalloc(const ss_singular_args *args);
  * Replaces fused_multistep (reference interface/functional/multistep.py:175-461).
  * Caller contract, not checked on the device: slot_mapping values lie in [0, slots), and
  * draft_probabilities has a [gamma, vocab] block for every slot a request may map to (the Python
- * driver checks the last before the call). Drafted tokens outside [0, vocab_size) are treated as
- * absent from every candidate list.
+ * driver checks the last before the call). A drafted token outside [0, vocab_size) reads no
+ * memory out of bounds, but its acceptance is not defined (the reference indexes with it).
  * ------------------------------------------------------------------------------------------- */
 typedef struct ss_multistep_args {
     const uint16_t *logits;      /* [rows, vocab] bf16 */

@@ -6,6 +6,7 @@ from __future__ import annotations
 import ctypes
 import os
 import re
+import shutil
 import subprocess
 import sys
 
@@ -69,6 +70,51 @@ def test_abi_version_and_struct_sizes():
     assert lib.ss_args_size(2) == ctypes.sizeof(_native.MultistepArgs)
     assert lib.ss_args_size(3) == ctypes.sizeof(_native.IndexedCopyArgs)
     assert lib.ss_args_size(4) == -1
+
+
+C_STRUCTS = {"ss_philox": _native.Philox, "ss_topk_args": _native.TopKArgs,
+             "ss_singular_args": _native.SingularArgs, "ss_multistep_args": _native.MultistepArgs,
+             "ss_indexed_copy_args": _native.IndexedCopyArgs}
+
+
+@pytest.mark.parametrize("compiler,std", [("gcc", "-std=c99"), ("g++", "-std=c++11")])
+def test_header_layout_is_the_mirrors_layout(tmp_path, compiler, std):
+    """The header compiles alone as strict C99 and as C++11, and the compiler places every field
+    of every argument struct at the offset, and with the size, that the ctypes mirrors give it.
+    The struct sizes the library reports cannot tell two swapped fields of one size apart."""
+
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} is not installed")
+
+    prints = []
+
+    for cname, cls in C_STRUCTS.items():
+        prints.append(f'printf("{cname} %zu %zu\\n", (size_t)0, sizeof({cname}));')
+
+        for name, _ in cls._fields_:
+            prints.append(f'printf("{cname}.{name} %zu %zu\\n", offsetof({cname}, {name}), '
+                          f'sizeof((({cname} *)0)->{name}));')
+
+    source = tmp_path / ("layout.c" if compiler == "gcc" else "layout.cpp")
+    source.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"sonic_sampler.h\"\n"
+                      "int main(void) {\n" + "\n".join(prints) + "\nreturn 0;\n}\n")
+    exe = tmp_path / "layout"
+    build = subprocess.run([compiler, std, "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", str(HEADER.parent),
+                            str(source), "-o", str(exe)], capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+
+    placed = {}
+
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        name, offset, size = line.split()
+        placed[name] = (int(offset), int(size))
+
+    for cname, cls in C_STRUCTS.items():
+        assert placed[cname] == (0, ctypes.sizeof(cls)), cname
+
+        for name, _ in cls._fields_:
+            field = getattr(cls, name)
+            assert placed[f"{cname}.{name}"] == (field.offset, field.size), f"{cname}.{name}"
 
 
 def test_status_strings():

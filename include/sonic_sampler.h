@@ -202,6 +202,10 @@ int ss_fused_singular(const ss_singular_args *args);
  * first call while args->stream is capturing fails with SS_ERR_UNSUPPORTED, and every later call
  * on that device may be captured. All calls on one device share the array:
  * calls that overlap on one device (two streams, or two threads) race, so they must be ordered.
+ * With the stages split (SS_STAGE_TILES per shard, then SS_STAGE_ROWS), the row-stage call reads
+ * the lists the tile-stage calls left in the array: no other call on the device may come between
+ * them, and the row count, world_size and tile count must match (the array's row stride is
+ * world_size * tiles * 128 words); the array then holds rows * world_size * tiles lists.
  * Every other argument, output and error is that of ss_fused_singular.
  * ------------------------------------------------------------------------------------------- */
 #define SS_STATIC_SCRATCH_BYTES (8u << 20)

@@ -494,8 +494,10 @@ extern "C" int ss_fused_singular_noalloc(const ss_singular_args *a) {
     uint32_t *ptr = nullptr;
     const int st = static_scratch((hipStream_t)a->stream, &ptr);
     if (st != SS_OK) return st;
-    // Every list entry the row stage uses is written by the tile stage of the same call (a greedy
-    // row's merge samples are read but ignored), so the array needs no clearing between calls.
+    // Every list entry the row stage uses is written by the tile stage of the same call, or, with
+    // the stages split, by the tile-stage calls of every shard made just before it on the device
+    // (a greedy row's merge samples are read but ignored), so the array needs no clearing between
+    // calls.
     ss_singular_args b = *a;
     b.scratch = ptr;
     b.stride_scratch = world * tiles * SS_K;

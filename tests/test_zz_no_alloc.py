@@ -103,6 +103,44 @@ def test_noalloc_matches_scratchpad_entry_point_on_consecutive_calls():
             assert torch.equal(a, b), f"{name} differ at rows={rows} V={vocab}"
 
 
+def test_noalloc_sharded_stages_match_the_scratchpad():
+    """A tensor-parallel caller that cannot allocate: the W shards' tile stages into the static
+    array (each into its slice), then the row stage over the W slices. Tokens, counts and logprobs
+    equal the same stages through a caller scratchpad, bit for bit."""
+
+    from bench import to_device
+    from sonic_sampler.interface.functional import fused_singular
+    from test_gpu_sharded import buffer_kwargs, outputs as shard_outputs, run_sharded
+
+    rows, vocab, world, block = 8, 4 * 8192, 4, 2048
+    host, logits = build_case(rows, vocab, seed=41)
+    logits = logits.to(DEV)
+    common = dict(max_top_logprobs=5, return_logprobs=True, update_counts=True)
+    print(f"noalloc sharded: rows={rows} V={vocab} W={world} block={block}", flush=True)
+
+    ref_buffers = to_device(host, DEV)
+    reference = run_sharded(logits, ref_buffers, world, block, vocab, **buffer_kwargs(ref_buffers, "target", 0),
+                            **common)
+
+    buffers = to_device(host, DEV)
+    kw = dict(buffer_kwargs(buffers, "target", 0), **common)
+    shard = vocab // world
+
+    for rank in range(world):
+
+        fused_singular(logits[:, rank * shard:(rank + 1) * shard], world_size=world, local_rank=rank,
+                       shard_size=shard, target_vocab=vocab, block_n=block, static_scratch=True,
+                       stage="tiles", **kw)
+
+    selection = fused_singular(logits[:, :shard], world_size=world, local_rank=0, shard_size=shard,
+                               target_vocab=vocab, block_n=block, static_scratch=True, stage="rows", **kw)
+    torch.cuda.synchronize()
+
+    for want, got in zip(shard_outputs(reference, ref_buffers), shard_outputs(selection, buffers)):
+
+        assert torch.equal(want, got)
+
+
 def test_noalloc_refuses_calls_beyond_the_static_scratch():
 
     from sonic_sampler import _native
